@@ -1,0 +1,75 @@
+/* C ABI of the MI355X quantized-linear library (libgsq.so).
+ *
+ * Plain pointers and sizes only; no framework types cross this boundary. All device
+ * pointers belong to the caller and must live on the device that is current when the
+ * call is made. Work is enqueued on `stream` (a hipStream_t; NULL = default stream) and
+ * nothing synchronizes with the host. Functions return 0 on success and a nonzero
+ * GSQ_E_* code otherwise; gsq_last_error() then describes the failure (per thread).
+ *
+ * Quant type ids are GGML's (mlx_gsq/gguf/parser.py:26-31): Q2_K 10, Q4_K 12, Q6_K 14,
+ * IQ2_XXS 16, IQ2_XS 17, IQ3_XXS 18, IQ1_S 19, IQ3_S 21, IQ2_S 22, IQ4_XS 23, IQ1_M 29.
+ * Packed weights are the untouched GGUF superblocks of an N x K matrix, row-major:
+ * N * (K/256) blocks of gsq_block_bytes(type) bytes (qmv.py:539-543).
+ * Activation/output dtype codes: GSQ_F32 0, GSQ_F16 1, GSQ_BF16 2.
+ */
+#ifndef GSQ_H
+#define GSQ_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GSQ_OK 0
+#define GSQ_E_VALUE 1       /* bad shape/size/alignment (the reference raises ValueError) */
+#define GSQ_E_UNSUPPORTED 2 /* unknown quant type (NotImplementedError) */
+#define GSQ_E_TABLES 3      /* codebook of a grid type not set on this device */
+#define GSQ_E_HIP 4         /* HIP runtime error */
+#define GSQ_E_TYPE 5        /* bad dtype code (TypeError) */
+
+#define GSQ_F32 0
+#define GSQ_F16 1
+#define GSQ_BF16 2
+
+/* Library ABI version. */
+int gsq_version(void);
+
+/* Bytes per 256-weight superblock, or -1 for an unsupported type.
+ * Replaces QUANT_BLOCK_SIZES lookups (mlx_gsq/gguf/parser.py:35-42). */
+int gsq_block_bytes(int qtype_id);
+
+/* Upload a codebook for a grid type (IQ1_S, IQ1_M, IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS,
+ * IQ3_S) and the 128-entry ksigns table to the current device. `grid` is a host array
+ * of entries x coords float32 values; every value must be exact in fp16.
+ * Replaces the table buffers the reference hands its kernels
+ * (iq_lookup_decode.py:46-53 `_tables`, iq3_s_decode.py:56-61 `_grid`). */
+int gsq_set_tables(int qtype_id, const float* grid, int64_t entries, int64_t coords,
+                   const uint8_t* ksigns, int64_t n_ksigns);
+
+/* 1 if the current device holds the tables `qtype_id` needs, else 0. */
+int gsq_tables_ready(int qtype_id);
+
+/* Dequantize `nblocks` superblocks to float32 (nblocks * 256 values, 16-byte aligned).
+ * Bit-exact with the CPU dequantizer. Replaces registry.decode
+ * (mlx_gsq/runtime/kernels/registry.py:28-32) and the decode kernels behind it. */
+int gsq_dequant(int qtype_id, const void* packed, int64_t nblocks, float* out, void* stream);
+
+/* y[M, N] = x[M, K] * W[N, K]^T with the fused-dequant matrix-vector kernel (decode path,
+ * small M). Replaces quantized_matvec (mlx_gsq/runtime/kernels/qmv.py:537-576). */
+int gsq_qmv(int qtype_id, const void* packed, const void* x, int x_dtype, void* y, int y_dtype,
+            int64_t M, int64_t N, int64_t K, void* stream);
+
+/* Same product with the tiled MFMA kernel (prefill, large M). Replaces quantized_matmul
+ * (mlx_gsq/runtime/kernels/qmm.py:559-594). */
+int gsq_qmm(int qtype_id, const void* packed, const void* x, int x_dtype, void* y, int y_dtype,
+            int64_t M, int64_t N, int64_t K, void* stream);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* gsq_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GSQ_H */

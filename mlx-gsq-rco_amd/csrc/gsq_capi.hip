@@ -1,0 +1,219 @@
+// C ABI of libgsq.so: validation, per-device codebook tables and kernel dispatch.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "../../include/gsq.h"
+#include "gsq_common.h"
+
+namespace gsq {
+hipError_t launch_dequant(int qt, const uint8_t* packed, int64_t nblocks, float* out, const DevTables& t,
+                          hipStream_t s);
+hipError_t launch_qmv(int qt, const uint8_t* packed, const void* x, int xdt, void* y, int ydt, int M, int64_t N,
+                      int K, const DevTables& tb, int num_cus, hipStream_t s);
+hipError_t launch_qmm(int qt, const uint8_t* packed, const void* x, int xdt, void* y, int ydt, int64_t M, int64_t N,
+                      int K, const DevTables& tb, hipStream_t s);
+}  // namespace gsq
+
+using namespace gsq;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+const char* type_name(int t) {
+  switch (t) {
+    case Q2_K: return "Q2_K"; case Q4_K: return "Q4_K"; case Q6_K: return "Q6_K";
+    case IQ2_XXS: return "IQ2_XXS"; case IQ2_XS: return "IQ2_XS"; case IQ3_XXS: return "IQ3_XXS";
+    case IQ1_S: return "IQ1_S"; case IQ3_S: return "IQ3_S"; case IQ2_S: return "IQ2_S";
+    case IQ4_XS: return "IQ4_XS"; case IQ1_M: return "IQ1_M";
+    default: return "?";
+  }
+}
+
+bool is_grid_type(int t) {
+  int e, c;
+  grid_shape_of(t, &e, &c);
+  return e > 0;
+}
+
+bool uses_ksigns(int t) { return t == IQ2_XXS || t == IQ2_XS || t == IQ3_XXS; }
+
+struct DevState {
+  std::map<int, uint16_t*> grids;  // per grid type
+  uint8_t* ksigns = nullptr;
+  int num_cus = 0;
+};
+
+std::mutex g_mu;
+std::map<int, DevState> g_dev;
+
+int current_device(int* dev) {
+  hipError_t e = hipGetDevice(dev);
+  if (e != hipSuccess) return fail(GSQ_E_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+  return GSQ_OK;
+}
+
+// Resolve the device tables for `qt` on the current device (caller holds no lock).
+int resolve(int qt, DevTables* tb, int* num_cus) {
+  int dev;
+  if (int rc = current_device(&dev)) return rc;
+  std::lock_guard<std::mutex> lk(g_mu);
+  DevState& st = g_dev[dev];
+  if (st.num_cus == 0) {
+    hipError_t e = hipDeviceGetAttribute(&st.num_cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return fail(GSQ_E_HIP, "hipDeviceGetAttribute: %s", hipGetErrorString(e));
+  }
+  *num_cus = st.num_cus;
+  tb->grid16 = nullptr;
+  tb->ks_masks = nullptr;
+  tb->ksigns = st.ksigns;
+  if (is_grid_type(qt)) {
+    auto it = st.grids.find(qt);
+    if (it == st.grids.end())
+      return fail(GSQ_E_TABLES, "codebook for %s is not set on device %d (call gsq_set_tables)", type_name(qt), dev);
+    tb->grid16 = it->second;
+    if (uses_ksigns(qt) && !st.ksigns)
+      return fail(GSQ_E_TABLES, "ksigns table is not set on device %d", dev);
+  }
+  return GSQ_OK;
+}
+
+int check_common(int qt, const void* packed, int64_t M, int64_t N, int64_t K, int xdt, int ydt) {
+  if (block_bytes_of(qt) == 0) return fail(GSQ_E_UNSUPPORTED, "unsupported quant type id %d", qt);
+  if (K <= 0 || K % 256) return fail(GSQ_E_VALUE, "invalid %s matrix width %lld", type_name(qt), (long long)K);
+  if (N <= 0 || M <= 0) return fail(GSQ_E_VALUE, "invalid shape M=%lld N=%lld", (long long)M, (long long)N);
+  if (K > (1ll << 30) || N > (1ll << 40)) return fail(GSQ_E_VALUE, "matrix too large");
+  if (!packed) return fail(GSQ_E_VALUE, "packed is NULL");
+  if (reinterpret_cast<uintptr_t>(packed) & 1) return fail(GSQ_E_VALUE, "packed must be 2-byte aligned");
+  if (xdt < 0 || xdt > 2 || ydt < 0 || ydt > 2) return fail(GSQ_E_TYPE, "bad dtype code x=%d y=%d", xdt, ydt);
+  return GSQ_OK;
+}
+
+size_t esize(int dt) { return dt == GSQ_F32 ? 4 : 2; }
+
+}  // namespace
+
+extern "C" {
+
+int gsq_version(void) { return 1; }
+
+int gsq_block_bytes(int qtype_id) {
+  int bb = block_bytes_of(qtype_id);
+  return bb ? bb : -1;
+}
+
+const char* gsq_last_error(void) { return g_err.c_str(); }
+
+int gsq_set_tables(int qt, const float* grid, int64_t entries, int64_t coords, const uint8_t* ksigns,
+                   int64_t n_ksigns) {
+  if (block_bytes_of(qt) == 0) return fail(GSQ_E_UNSUPPORTED, "unsupported quant type id %d", qt);
+  int ee, cc;
+  grid_shape_of(qt, &ee, &cc);
+  if (ee == 0) return fail(GSQ_E_VALUE, "%s has no codebook", type_name(qt));
+  if (!grid || entries != ee || coords != cc)
+    return fail(GSQ_E_VALUE, "%s codebook must be %dx%d, got %lldx%lld", type_name(qt), ee, cc,
+                (long long)entries, (long long)coords);
+  if (!ksigns || n_ksigns != 128) return fail(GSQ_E_VALUE, "ksigns must have 128 entries");
+  std::vector<uint16_t> h16((size_t)ee * cc);
+  for (size_t i = 0; i < h16.size(); ++i) {
+    const float v = grid[i];
+    const _Float16 h = (_Float16)v;
+    if (!std::isfinite(v) || (float)h != v)
+      return fail(GSQ_E_VALUE, "%s codebook value %g at %zu is not exact in fp16", type_name(qt), (double)v, i);
+    h16[i] = __builtin_bit_cast(uint16_t, h);
+  }
+  int dev;
+  if (int rc = current_device(&dev)) return rc;
+  std::lock_guard<std::mutex> lk(g_mu);
+  DevState& st = g_dev[dev];
+  hipError_t e;
+  if (!st.ksigns) {
+    e = hipMalloc(&st.ksigns, 128);
+    if (e != hipSuccess) { st.ksigns = nullptr; return fail(GSQ_E_HIP, "hipMalloc: %s", hipGetErrorString(e)); }
+  }
+  e = hipMemcpy(st.ksigns, ksigns, 128, hipMemcpyHostToDevice);
+  if (e != hipSuccess) return fail(GSQ_E_HIP, "hipMemcpy: %s", hipGetErrorString(e));
+  uint16_t*& g = st.grids[qt];
+  if (!g) {
+    e = hipMalloc(&g, h16.size() * 2);
+    if (e != hipSuccess) { st.grids.erase(qt); return fail(GSQ_E_HIP, "hipMalloc: %s", hipGetErrorString(e)); }
+  }
+  e = hipMemcpy(g, h16.data(), h16.size() * 2, hipMemcpyHostToDevice);
+  if (e != hipSuccess) return fail(GSQ_E_HIP, "hipMemcpy: %s", hipGetErrorString(e));
+  return GSQ_OK;
+}
+
+int gsq_tables_ready(int qt) {
+  if (block_bytes_of(qt) == 0) return 0;
+  if (!is_grid_type(qt)) return 1;
+  DevTables tb;
+  int cus;
+  return resolve(qt, &tb, &cus) == GSQ_OK ? 1 : 0;
+}
+
+int gsq_dequant(int qt, const void* packed, int64_t nblocks, float* out, void* stream) {
+  if (block_bytes_of(qt) == 0) return fail(GSQ_E_UNSUPPORTED, "unsupported quant type id %d", qt);
+  if (nblocks < 0) return fail(GSQ_E_VALUE, "negative block count");
+  if (nblocks == 0) return GSQ_OK;
+  if (!packed || !out) return fail(GSQ_E_VALUE, "NULL pointer");
+  if (reinterpret_cast<uintptr_t>(out) & 15) return fail(GSQ_E_VALUE, "out must be 16-byte aligned");
+  DevTables tb;
+  int cus;
+  if (int rc = resolve(qt, &tb, &cus)) return rc;
+  hipError_t e = launch_dequant(qt, static_cast<const uint8_t*>(packed), nblocks, out, tb,
+                                static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(GSQ_E_HIP, "dequant launch: %s", hipGetErrorString(e));
+  return GSQ_OK;
+}
+
+int gsq_qmv(int qt, const void* packed, const void* x, int xdt, void* y, int ydt, int64_t M, int64_t N, int64_t K,
+            void* stream) {
+  if (int rc = check_common(qt, packed, M, N, K, xdt, ydt)) return rc;
+  if (!x || !y) return fail(GSQ_E_VALUE, "NULL pointer");
+  if (K / 32 > 576) return fail(GSQ_E_VALUE, "QMV supports K <= 18432 (got %lld); use gsq_qmm", (long long)K);
+  DevTables tb;
+  int cus;
+  if (int rc = resolve(qt, &tb, &cus)) return rc;
+  const int64_t chunk = xdt == GSQ_F16 ? 4 : 2;
+  for (int64_t r = 0; r < M; r += chunk) {
+    const int64_t mr = (M - r) < chunk ? (M - r) : chunk;
+    const void* xr = static_cast<const char*>(x) + r * K * esize(xdt);
+    void* yr = static_cast<char*>(y) + r * N * esize(ydt);
+    hipError_t e = launch_qmv(qt, static_cast<const uint8_t*>(packed), xr, xdt, yr, ydt, (int)mr, N, (int)K, tb, cus,
+                              static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(GSQ_E_HIP, "qmv launch: %s", hipGetErrorString(e));
+  }
+  return GSQ_OK;
+}
+
+int gsq_qmm(int qt, const void* packed, const void* x, int xdt, void* y, int ydt, int64_t M, int64_t N, int64_t K,
+            void* stream) {
+  if (int rc = check_common(qt, packed, M, N, K, xdt, ydt)) return rc;
+  if (!x || !y) return fail(GSQ_E_VALUE, "NULL pointer");
+  DevTables tb;
+  int cus;
+  if (int rc = resolve(qt, &tb, &cus)) return rc;
+  hipError_t e = launch_qmm(qt, static_cast<const uint8_t*>(packed), x, xdt, y, ydt, M, N, (int)K, tb,
+                            static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(GSQ_E_HIP, "qmm launch: %s", hipGetErrorString(e));
+  return GSQ_OK;
+}
+
+}  // extern "C"

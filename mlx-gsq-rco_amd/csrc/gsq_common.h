@@ -1,0 +1,114 @@
+// Common definitions for the gfx950 quantized-linear kernels.
+//
+// Superblock layouts and decode formulas follow the reference decoders
+// (mlx_gsq/runtime/kernels/k_decode.py:18-80, iq_lookup_decode.py:6-39,
+// iq3_s_decode.py:16-40). Every supported format packs 256 weights per superblock.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gsq {
+
+enum QType : int {
+  Q2_K = 10, Q4_K = 12, Q6_K = 14, IQ2_XXS = 16, IQ2_XS = 17, IQ3_XXS = 18,
+  IQ1_S = 19, IQ3_S = 21, IQ2_S = 22, IQ4_XS = 23, IQ1_M = 29,
+};
+
+template <int T> struct BlockBytes;
+template <> struct BlockBytes<Q2_K> { static constexpr int v = 84; };
+template <> struct BlockBytes<Q4_K> { static constexpr int v = 144; };
+template <> struct BlockBytes<Q6_K> { static constexpr int v = 210; };
+template <> struct BlockBytes<IQ2_XXS> { static constexpr int v = 66; };
+template <> struct BlockBytes<IQ2_XS> { static constexpr int v = 74; };
+template <> struct BlockBytes<IQ3_XXS> { static constexpr int v = 98; };
+template <> struct BlockBytes<IQ1_S> { static constexpr int v = 50; };
+template <> struct BlockBytes<IQ3_S> { static constexpr int v = 110; };
+template <> struct BlockBytes<IQ2_S> { static constexpr int v = 82; };
+template <> struct BlockBytes<IQ4_XS> { static constexpr int v = 136; };
+template <> struct BlockBytes<IQ1_M> { static constexpr int v = 56; };
+
+inline int block_bytes_of(int t) {
+  switch (t) {
+    case Q2_K: return 84; case Q4_K: return 144; case Q6_K: return 210;
+    case IQ2_XXS: return 66; case IQ2_XS: return 74; case IQ3_XXS: return 98;
+    case IQ1_S: return 50; case IQ3_S: return 110; case IQ2_S: return 82;
+    case IQ4_XS: return 136; case IQ1_M: return 56;
+    default: return 0;
+  }
+}
+
+// Codebook geometry of the grid types (entries, coordinates); 0 for the others.
+inline void grid_shape_of(int t, int* entries, int* coords) {
+  *entries = 0; *coords = 0;
+  switch (t) {
+    case IQ1_S: case IQ1_M: *entries = 2048; *coords = 8; break;
+    case IQ2_XXS: *entries = 256; *coords = 8; break;
+    case IQ2_XS: *entries = 512; *coords = 8; break;
+    case IQ2_S: *entries = 1024; *coords = 8; break;
+    case IQ3_XXS: *entries = 256; *coords = 4; break;
+    case IQ3_S: *entries = 512; *coords = 4; break;
+    default: break;
+  }
+}
+
+// Device-resident tables for one type, built by gsq_set_tables.
+struct DevTables {
+  const uint16_t* grid16;    // fp16 codebook, entries x coords (grid types)
+  const uint32_t* ks_masks;  // [128][4] fp16-pair sign XOR masks for a ksigns index
+  const uint8_t* ksigns;     // [128]
+};
+
+// Non-linear IQ4_XS values (k_decode.py:77).
+__device__ __constant__ static const int8_t kIQ4Values[16] = {
+    -127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a), __builtin_bit_cast(half2_t, b), c, false);
+}
+
+__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
+  _Float16 a = (_Float16)lo, b = (_Float16)hi;
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+// ---- byte access helpers -----------------------------------------------------------
+// Global memory: byte loads (the dequant instrument does not need wide loads).
+__device__ __forceinline__ uint32_t gb(const uint8_t* p, int i) { return p[i]; }
+__device__ __forceinline__ uint32_t gu16(const uint8_t* p, int i) { return (uint32_t)p[i] | ((uint32_t)p[i + 1] << 8); }
+__device__ __forceinline__ uint32_t gu32(const uint8_t* p, int i) {
+  return (uint32_t)p[i] | ((uint32_t)p[i + 1] << 8) | ((uint32_t)p[i + 2] << 16) | ((uint32_t)p[i + 3] << 24);
+}
+
+// LDS: N consecutive 32-bit words starting at an even byte offset (blocks are only
+// 2-byte aligned). Reads N+1 aligned words and funnel-shifts them into place.
+template <int N>
+__device__ __forceinline__ void lds_words(const uint8_t* base, uint32_t off, uint32_t (&w)[N]) {
+  const uint32_t* p = reinterpret_cast<const uint32_t*>(base + (off & ~3u));
+  uint32_t sh = off & 3u;
+  uint32_t a[N + 1];
+#pragma unroll
+  for (int i = 0; i <= N; ++i) a[i] = p[i];
+#pragma unroll
+  for (int i = 0; i < N; ++i) w[i] = __builtin_amdgcn_alignbyte(a[i + 1], a[i], sh);
+}
+__device__ __forceinline__ uint32_t lds_w32(const uint8_t* base, uint32_t off) {
+  uint32_t w[1];
+  lds_words<1>(base, off, w);
+  return w[0];
+}
+__device__ __forceinline__ uint32_t lds_u16(const uint8_t* base, uint32_t off) {
+  return *reinterpret_cast<const uint16_t*>(base + off);
+}
+__device__ __forceinline__ uint32_t lds_u8(const uint8_t* base, uint32_t off) { return base[off]; }
+
+__device__ __forceinline__ uint32_t bfe(uint32_t v, uint32_t off, uint32_t width) {
+  return __builtin_amdgcn_ubfe(v, off, width);
+}
+
+}  // namespace gsq

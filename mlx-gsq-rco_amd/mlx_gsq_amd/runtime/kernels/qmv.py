@@ -1,0 +1,67 @@
+"""Fused dequant + matrix-vector product on packed GGUF weights (decode path).
+
+Drop-in counterpart of mlx_gsq/runtime/kernels/qmv.py:537-576 ``quantized_matvec`` on
+torch tensors: same name, keyword arguments, validation order and exceptions. Inputs
+with at least ``QMM_MIN_ROWS`` rows are routed to the tiled QMM, as in the reference
+(qmv.py:548-549). The work runs in libgsq.so's gfx950 QMV kernel on the tensors' device
+and current stream.
+"""
+from __future__ import annotations
+
+import torch
+
+from ... import _lib
+from ...formats import QTYPES, TYPE_IDS
+from ...gguf.parser import GGMLQuantizationType, QUANT_BLOCK_SIZES
+from .qmm import QMM_MIN_ROWS, quantized_matmul
+
+
+def _validate(x, packed, qtype, out_features, in_features):
+    type_id = int(GGMLQuantizationType[qtype])  # KeyError for unknown names, as qmv.py:540
+    block_elements, block_bytes = QUANT_BLOCK_SIZES[type_id]
+    if block_elements != 256 or in_features % 256:
+        raise ValueError(f"invalid {qtype} matrix width")
+    expected = out_features * (in_features // 256) * block_bytes
+    if packed.numel() != expected:
+        raise ValueError(f"packed size {packed.numel()} != expected {expected}")
+    if x.shape[-1] != in_features:
+        raise ValueError("input feature size mismatch")
+
+
+def _check_tensors(x, packed):
+    if packed.dtype != torch.uint8:
+        raise TypeError("packed input must be uint8")
+    if x.dtype not in _lib.DTYPE_CODES:
+        raise TypeError(f"unsupported activation dtype {x.dtype}")
+    if x.device.type != "cuda" or packed.device != x.device:
+        raise ValueError("x and packed must be on the same GPU device")
+
+
+def quantized_matvec(x, packed, *, qtype: str, out_features: int, in_features: int, out_dtype=None):
+    """y = x @ W.T for packed ``W`` of shape ``(out_features, in_features)``.
+
+    ``x`` has shape ``(..., in_features)``; the result has shape ``(..., out_features)`` and
+    dtype ``out_dtype`` (default: ``x.dtype``, as the reference).
+    """
+    _validate(x, packed, qtype, out_features, in_features)
+    original = x.shape[:-1]
+    rows = x.numel() // in_features
+    flat = x.reshape(rows, in_features)
+    if rows >= QMM_MIN_ROWS or in_features > 18432:
+        return quantized_matmul(flat, packed, qtype=qtype, out_features=out_features,
+                                in_features=in_features, out_dtype=out_dtype).reshape(*original, out_features)
+    if qtype not in QTYPES:
+        raise KeyError(qtype)
+    _check_tensors(x, packed)
+    odt = out_dtype or x.dtype
+    flat = flat.contiguous()
+    packed = packed.contiguous()
+    y = torch.empty((rows, out_features), dtype=odt, device=x.device)
+    if rows:
+        _lib.ensure_tables(qtype, x.device)
+        with torch.cuda.device(x.device):
+            _lib.check(_lib.lib().gsq_qmv(TYPE_IDS[qtype], packed.data_ptr(), flat.data_ptr(),
+                                          _lib.DTYPE_CODES[flat.dtype], y.data_ptr(), _lib.DTYPE_CODES[odt],
+                                          rows, out_features, in_features, _lib.stream_handle(x.device)),
+                       "quantized_matvec")
+    return y.reshape(*original, out_features)

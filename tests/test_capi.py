@@ -1,0 +1,124 @@
+"""CPU tests of the boundary: libgsq.so loads and exports every symbol include/gsq.h
+declares, and the host wrappers raise the reference's exception types and messages
+(mlx_gsq/runtime/kernels/qmv.py:539-544, qmm.py:569-579, registry.py:28-46) without
+touching a GPU."""
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_symbols():
+    text = open(os.path.join(ROOT, "include", "gsq.h")).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(gsq_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_header_symbols():
+    from mlx_gsq_amd import _lib
+    lib = _lib.lib()
+    syms = header_symbols()
+    assert syms and set(syms) == set(_lib.EXPORTS), syms
+    for s in syms:
+        assert hasattr(lib, s)
+    assert lib.gsq_version() == 1
+
+
+def test_block_bytes_match_format_table():
+    from mlx_gsq_amd import _lib
+    from mlx_gsq_amd.formats import BLOCK_BYTES, TYPE_IDS
+    from mlx_gsq_amd.gguf.parser import QUANT_BLOCK_SIZES
+    lib = _lib.lib()
+    for q, tid in TYPE_IDS.items():
+        assert lib.gsq_block_bytes(tid) == BLOCK_BYTES[q] == QUANT_BLOCK_SIZES[tid][1]
+    assert lib.gsq_block_bytes(2) == -1  # Q4_0: not a 256-block type of this path
+
+
+def test_c_validation_errors_without_gpu():
+    from mlx_gsq_amd import _lib
+    lib = _lib.lib()
+    assert lib.gsq_qmv(12, 2, 4, 1, 8, 0, 1, 4, 300, None) == _lib.GSQ_E_VALUE  # K % 256
+    assert b"matrix width" in lib.gsq_last_error()
+    assert lib.gsq_qmv(12, 3, 4, 1, 8, 0, 1, 4, 256, None) == _lib.GSQ_E_VALUE  # odd packed address
+    assert lib.gsq_qmm(99, 2, 4, 1, 8, 0, 1, 4, 256, None) == _lib.GSQ_E_UNSUPPORTED
+    assert lib.gsq_qmm(12, 2, 4, 7, 8, 0, 1, 4, 256, None) == _lib.GSQ_E_TYPE
+    assert lib.gsq_dequant(99, 2, 1, 16, None) == _lib.GSQ_E_UNSUPPORTED
+    assert lib.gsq_set_tables(12, None, 0, 0, None, 0) == _lib.GSQ_E_VALUE  # Q4_K has no codebook
+    g = np.zeros((10, 8), np.float32)
+    ks = np.zeros(128, np.uint8)
+    assert lib.gsq_set_tables(16, g.ctypes.data, 10, 8, ks.ctypes.data, 128) == _lib.GSQ_E_VALUE
+
+
+def test_python_validation_mirrors_reference():
+    from mlx_gsq_amd.runtime.kernels import decode, decode_weight, quantized_matmul, quantized_matvec
+    from mlx_gsq_amd.runtime.store import PackedWeight
+    x = torch.zeros(1, 512, dtype=torch.float16)
+    p = torch.zeros(2 * 2 * 144, dtype=torch.uint8)
+    with pytest.raises(ValueError, match="invalid Q4_K matrix width"):
+        quantized_matvec(torch.zeros(1, 300), p, qtype="Q4_K", out_features=2, in_features=300)
+    with pytest.raises(ValueError, match="packed size"):
+        quantized_matvec(x, p[:-1], qtype="Q4_K", out_features=2, in_features=512)
+    with pytest.raises(ValueError, match="input feature size mismatch"):
+        quantized_matvec(torch.zeros(1, 256), p, qtype="Q4_K", out_features=2, in_features=512)
+    with pytest.raises(KeyError):
+        quantized_matvec(x, p, qtype="NOPE", out_features=2, in_features=512)
+    with pytest.raises(KeyError):  # a 256-block GGML type with no kernel (reference: KeyError)
+        quantized_matvec(x, torch.zeros(2 * 2 * 176, dtype=torch.uint8), qtype="Q5_K", out_features=2, in_features=512)
+    with pytest.raises(NotImplementedError, match="no tiled QMM kernel"):
+        quantized_matmul(x, p, qtype="Q5_K", out_features=2, in_features=512)
+    with pytest.raises(NotImplementedError):
+        decode(p, "Q5_K")
+    with pytest.raises(TypeError):
+        decode(p.to(torch.int8), "Q4_K")
+    with pytest.raises(ValueError, match="not block aligned"):
+        decode(p[:-1], "Q4_K")
+    w = PackedWeight("t", p, (512, 2), (2, 512), "F16", 1, 1024, 576)
+    with pytest.raises(TypeError, match="not a supported quantized weight"):
+        decode_weight(w)
+
+
+def test_codebook_validation():
+    from mlx_gsq_amd import tables
+    t = tables.synthetic_tables(3)
+    for q, g in t.items():
+        tables.validate_grid(q, g)
+    bad = t["IQ2_XS"].copy()
+    bad[0, 0] = 9.0
+    with pytest.raises(ValueError, match="outside"):
+        tables.validate_grid("IQ2_XS", bad)
+    dup = t["IQ3_S"].copy()
+    dup[1] = dup[0]
+    with pytest.raises(ValueError, match="unique"):
+        tables.validate_grid("IQ3_S", dup)
+    assert list(tables.ksigns()[:8]) == [0, 129, 130, 3, 132, 5, 6, 135]
+
+
+def test_missing_codebook_is_an_error(monkeypatch):
+    from mlx_gsq_amd import tables
+    monkeypatch.delenv("GSQ_CODEBOOKS", raising=False)
+    saved = dict(tables._registered)
+    tables.clear_tables()
+    try:
+        with pytest.raises(RuntimeError, match="no codebook"):
+            tables.grid("IQ2_XXS")
+    finally:
+        tables._registered.update(saved)
+
+
+def test_codebook_file_source(tmp_path, monkeypatch):
+    from mlx_gsq_amd import tables
+    t = tables.synthetic_tables(4)
+    path = tmp_path / "books.npz"
+    np.savez(path, **{k: v for k, v in t.items() if k != "IQ1_M"})
+    monkeypatch.setenv("GSQ_CODEBOOKS", str(path))
+    saved = dict(tables._registered)
+    tables.clear_tables()
+    try:
+        np.testing.assert_array_equal(tables.grid("IQ1_M"), t["IQ1_S"])
+        np.testing.assert_array_equal(tables.grid("IQ3_XXS"), t["IQ3_XXS"])
+    finally:
+        tables.clear_tables()
+        tables._registered.update(saved)

@@ -1,0 +1,194 @@
+"""GPU parity of the HIP path against the CPU oracle (run on an MI355X).
+
+Bars (north star): dequantized weights bit-exact; QMV/QMM outputs within rel-L2 1e-3 for
+fp32 output and 1e-2 for fp16 output of the oracle's dequant + float32 matmul on the same
+seeded inputs. The fused QMV keeps fp32 accumulation of exact fp16 products, so it is also
+held to the reference's own QMV tolerance (tests/test_all_qmv.py:24: rtol 3e-5, atol 5e-4).
+Codebooks are seeded synthetic tables with the published shapes and value sets (the real
+ones come from gguf-py, which is absent here), so table *content* is not pinned by these
+tests; indexing, sign and scale arithmetic are.
+"""
+import numpy as np
+import pytest
+import torch
+
+from mlx_gsq_amd import synth, tables
+from mlx_gsq_amd.formats import QTYPES, packed_size
+from oracle import gsq_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TABLES = tables.synthetic_tables(0)
+
+
+@pytest.fixture(autouse=True, scope="module")
+def _codebooks():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    tables.set_tables(TABLES)
+    yield
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+@pytest.mark.parametrize("qtype", QTYPES)
+def test_dequant_bit_exact(qtype):
+    from mlx_gsq_amd.runtime.kernels.registry import decode
+    print(f"dequant {qtype}", flush=True)
+    packed = synth.make_packed(qtype, 64, 1024, seed=11)
+    got = decode(dev(packed), qtype).cpu().numpy()
+    want = O.dequantize_reference(packed, qtype, TABLES.get(qtype))
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("qtype", QTYPES)
+def test_dequant_raw_random_bytes(qtype):
+    """Fully random payloads (fp16 fields may be Inf/NaN): same values, same NaN positions."""
+    from mlx_gsq_amd.runtime.kernels.registry import decode
+    rng = np.random.default_rng(5)
+    packed = rng.integers(0, 256, 37 * O.BLOCK_BYTES[qtype], dtype=np.uint8)
+    got = decode(dev(packed), qtype).cpu().numpy()
+    want = O.dequantize_reference(packed, qtype, TABLES.get(qtype))
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    ok = ~np.isnan(want)
+    np.testing.assert_array_equal(got[ok], want[ok])
+
+
+@pytest.mark.parametrize("qtype", QTYPES)
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 5])
+def test_qmv_matches_oracle(qtype, rows):
+    from mlx_gsq_amd.runtime.kernels.qmv import quantized_matvec
+    N, K = 4100, 512  # several rows per workgroup and several staging steps
+    print(f"qmv {qtype} M={rows} N={N} K={K}", flush=True)
+    packed = synth.make_packed(qtype, N, K, seed=21)
+    x = synth.make_x(rows, K, seed=123, dtype=np.float16)
+    y = quantized_matvec(dev(x), dev(packed), qtype=qtype, out_features=N, in_features=K,
+                         out_dtype=torch.float32).cpu().numpy()
+    want = O.matmul_reference(x, packed, qtype, N, K, TABLES.get(qtype))
+    assert rel_l2(y, want) <= 1e-4, rel_l2(y, want)
+    np.testing.assert_allclose(y, want, rtol=3e-5, atol=5e-4)
+
+
+@pytest.mark.parametrize("qtype", QTYPES)
+@pytest.mark.parametrize("xdtype", [np.float32, "bf16"])
+def test_qmv_split_precision_inputs(qtype, xdtype):
+    from mlx_gsq_amd.runtime.kernels.qmv import quantized_matvec
+    N, K = 700, 768
+    packed = synth.make_packed(qtype, N, K, seed=3)
+    x32 = synth.make_x(2, K, seed=9, dtype=np.float32)
+    xt = dev(x32) if xdtype is np.float32 else dev(x32).to(torch.bfloat16)
+    y = quantized_matvec(xt, dev(packed), qtype=qtype, out_features=N, in_features=K,
+                         out_dtype=torch.float32).cpu().numpy()
+    want = O.matmul_reference(xt.float().cpu().numpy(), packed, qtype, N, K, TABLES.get(qtype))
+    assert rel_l2(y, want) <= 1e-4, rel_l2(y, want)
+
+
+@pytest.mark.parametrize("qtype", QTYPES)
+@pytest.mark.parametrize("shape", [(1024, 5120), (512, 17408)])
+def test_qmv_27b_row_widths(qtype, shape):
+    from mlx_gsq_amd.runtime.kernels.qmv import quantized_matvec
+    N, K = shape
+    packed = synth.make_packed(qtype, N, K, seed=7)
+    x = synth.make_x(1, K, seed=1, dtype=np.float16)
+    y = quantized_matvec(dev(x), dev(packed), qtype=qtype, out_features=N, in_features=K,
+                         out_dtype=torch.float32).cpu().numpy()
+    want = O.matmul_reference(x, packed, qtype, N, K, TABLES.get(qtype))
+    assert rel_l2(y, want) <= 1e-4, rel_l2(y, want)
+
+
+def test_qmv_unaligned_packed_view_and_odd_rows():
+    """A 2-byte (not 16-byte) aligned packed view and an odd N exercise the staged copy's edges."""
+    from mlx_gsq_amd.runtime.kernels.qmv import quantized_matvec
+    for qtype in ("IQ1_S", "Q6_K", "IQ3_S"):
+        N, K = 37, 256
+        packed = synth.make_packed(qtype, N, K, seed=2)
+        big = torch.zeros(packed.size + 64, dtype=torch.uint8, device="cuda")
+        big[6:6 + packed.size] = dev(packed)
+        view = big[6:6 + packed.size]
+        x = synth.make_x(1, K, seed=4, dtype=np.float16)
+        y = quantized_matvec(dev(x), view, qtype=qtype, out_features=N, in_features=K,
+                             out_dtype=torch.float32).cpu().numpy()
+        want = O.matmul_reference(x, packed, qtype, N, K, TABLES.get(qtype))
+        assert rel_l2(y, want) <= 1e-4, (qtype, rel_l2(y, want))
+
+
+@pytest.mark.parametrize("qtype", QTYPES)
+@pytest.mark.parametrize("rows", [8, 16, 33, 182])
+def test_qmm_matches_oracle(qtype, rows):
+    from mlx_gsq_amd.runtime.kernels.qmm import quantized_matmul
+    N, K = 200, 512
+    print(f"qmm {qtype} M={rows}", flush=True)
+    packed = synth.make_packed(qtype, N, K, seed=31)
+    x = synth.make_x(rows, K, seed=123, dtype=np.float16)
+    y = quantized_matmul(dev(x), dev(packed), qtype=qtype, out_features=N, in_features=K,
+                         out_dtype=torch.float32).cpu().numpy()
+    want = O.matmul_reference(x, packed, qtype, N, K, TABLES.get(qtype))
+    assert rel_l2(y, want) <= 1e-3, rel_l2(y, want)
+    scale = np.abs(want).max()
+    np.testing.assert_allclose(y, want, rtol=2e-3, atol=2e-3 * scale)  # reference test_all_qmm.py:38-39
+
+
+@pytest.mark.parametrize("qtype", ["Q4_K", "IQ3_S", "Q6_K"])
+def test_qmm_fp16_output_and_fp32_input(qtype):
+    from mlx_gsq_amd.runtime.kernels.qmm import quantized_matmul
+    N, K = 96, 1024
+    packed = synth.make_packed(qtype, N, K, seed=8)
+    x = synth.make_x(16, K, seed=7, dtype=np.float32)
+    want = O.matmul_reference(x, packed, qtype, N, K, TABLES.get(qtype))
+    y16 = quantized_matmul(dev(x).half(), dev(packed), qtype=qtype, out_features=N, in_features=K).float().cpu().numpy()
+    assert rel_l2(y16, want) <= 1e-2
+    y32 = quantized_matmul(dev(x), dev(packed), qtype=qtype, out_features=N, in_features=K).cpu().numpy()
+    assert rel_l2(y32, want) <= 1e-3
+
+
+def test_matvec_routes_many_rows_to_qmm():
+    from mlx_gsq_amd.runtime.kernels.qmv import quantized_matvec
+    N, K = 64, 512
+    packed = synth.make_packed("Q4_K", N, K, seed=1)
+    x = synth.make_x(9, K, seed=2, dtype=np.float16)
+    y = quantized_matvec(dev(x).reshape(3, 3, K), dev(packed), qtype="Q4_K", out_features=N, in_features=K,
+                         out_dtype=torch.float32)
+    assert y.shape == (3, 3, N)
+    want = O.matmul_reference(x, packed, "Q4_K", N, K)
+    assert rel_l2(y.reshape(9, N).cpu().numpy(), want) <= 1e-3
+
+
+def test_gsq_linear_and_store_roundtrip(tmp_path):
+    import json
+    from safetensors.torch import save_file
+    from mlx_gsq_amd.nn import GSQLinear
+    from mlx_gsq_amd.runtime import PackedModelStore
+    N, K = 48, 512
+    packed = synth.make_packed("IQ2_XS", N, K, seed=4)
+    info = {"w": {"qtype": "IQ2_XS", "qtype_id": 17, "gguf_shape": [K, N], "logical_shape": [N, K],
+                  "num_elements": N * K, "block_elements": 256, "block_bytes": 74}}
+    path = tmp_path / "m.safetensors"
+    save_file({"w": torch.from_numpy(packed)}, str(path),
+              metadata={"format": "mlx-gsq-packed-v1", "tensor_quantization": json.dumps(info)})
+    store = PackedModelStore(path)
+    lin = GSQLinear(store.weight("w"))
+    x = synth.make_x(1, K, seed=5, dtype=np.float16)
+    want = O.matmul_reference(x, packed, "IQ2_XS", N, K, TABLES["IQ2_XS"])
+    y1 = lin(dev(x)).float().cpu().numpy()
+    assert rel_l2(y1, want) <= 1e-2  # fp16 output, as the reference returns x.dtype
+    x4 = synth.make_x(4, K, seed=6, dtype=np.float32)
+    y4 = lin(dev(x4)).cpu().numpy()
+    assert rel_l2(y4, O.matmul_reference(x4, packed, "IQ2_XS", N, K, TABLES["IQ2_XS"])) <= 1e-3
+
+
+def test_deterministic_repeat():
+    from mlx_gsq_amd.runtime.kernels.qmv import quantized_matvec
+    N, K = 2048, 5120
+    packed = dev(synth.make_packed("IQ3_XXS", N, K, seed=9))
+    x = dev(synth.make_x(1, K, seed=3, dtype=np.float16))
+    a = quantized_matvec(x, packed, qtype="IQ3_XXS", out_features=N, in_features=K, out_dtype=torch.float32)
+    b = quantized_matvec(x, packed, qtype="IQ3_XXS", out_features=N, in_features=K, out_dtype=torch.float32)
+    assert torch.equal(a, b)

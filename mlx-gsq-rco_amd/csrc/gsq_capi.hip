@@ -187,11 +187,13 @@ int gsq_qmv(int qt, const void* packed, const void* x, int xdt, void* y, int ydt
             void* stream) {
   if (int rc = check_common(qt, packed, M, N, K, xdt, ydt)) return rc;
   if (!x || !y) return fail(GSQ_E_VALUE, "NULL pointer");
-  if (K / 32 > 576) return fail(GSQ_E_VALUE, "QMV supports K <= 18432 (got %lld); use gsq_qmm", (long long)K);
+  if (K / 32 > 2048) return fail(GSQ_E_VALUE, "QMV supports K <= 65536 (got %lld); use gsq_qmm", (long long)K);
+  if (reinterpret_cast<uintptr_t>(x) & 15) return fail(GSQ_E_VALUE, "x must be 16-byte aligned");
   DevTables tb;
   int cus;
   if (int rc = resolve(qt, &tb, &cus)) return rc;
-  const int64_t chunk = xdt == GSQ_F16 ? 4 : 2;
+  // rows per launch: 4 only for fp16 activations with K/32 <= 320 (one group per lane)
+  const int64_t chunk = (xdt == GSQ_F16 && K / 32 <= 320) ? 4 : 2;
   for (int64_t r = 0; r < M; r += chunk) {
     const int64_t mr = (M - r) < chunk ? (M - r) : chunk;
     const void* xr = static_cast<const char*>(x) + r * K * esize(xdt);

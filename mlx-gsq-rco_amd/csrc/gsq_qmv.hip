@@ -26,13 +26,12 @@ struct QmvArgs {
   int64_t N;
   int64_t total_bytes;
   int K, M, x_dtype, y_dtype;
-  int rows_per_wg, J, row_bytes, buf_bytes, tbl_bytes;
+  int rows_per_wg, J, row_bytes, buf_bytes, tbl_bytes, red_bytes;
+  int slots, lanes_per_slot, red_tpr;
   DevTables tb;
 };
 
 enum { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
-constexpr int kJMax = 8;
-constexpr int kQmvMaxThreads = 576;  // K <= 18432
 
 // ---- activation pairing ------------------------------------------------------------
 enum Pairing { PAIR_NAT = 0, PAIR_K = 1, PAIR_16 = 2 };
@@ -60,15 +59,26 @@ __device__ __forceinline__ void dacc(uint32_t w, const XReg<MR, XS>& x, int i, f
   }
 }
 
-// (C + q, C + q') as an fp16 pair -> (q, q') exactly (one v_pk_add_f16). The magic-number
-// decode yields fp16 values 1024 + code; removing the offset before the dot keeps the fp32
-// sums free of cancellation.
-template <int C>
-__device__ __forceinline__ uint32_t sub_magic(uint32_t v) {
-  const half2_t r = __builtin_bit_cast(half2_t, v) - (half2_t){(_Float16)(float)C, (_Float16)(float)C};
-  return __builtin_bit_cast(uint32_t, r);
+// Small unsigned codes q (< 1024) placed in the low bits of an fp16 lane are the subnormal
+// values q * 2^-24, so a masked code pair is directly a v_dot2_f32_f16 operand: the fp16 x
+// fp16 products are exact in fp32 and the group scale absorbs the 2^24.
+constexpr float kSub = 16777216.f;  // 2^24
+
+// Split-precision activations (XS: fp32/bf16 split into fp16 hi + lo) have subnormal lo
+// parts, and subnormal x subnormal products lose bits in v_dot2, so those variants encode
+// codes as exact normal fp16 integers instead: (1024 + q) with the 1024 removed by one
+// v_pk_add_f16.
+template <bool XS>
+__device__ __forceinline__ uint32_t enc_codes(uint32_t codes) {
+  if constexpr (XS) {
+    const half2_t r = __builtin_bit_cast(half2_t, codes | 0x64006400u) - (half2_t){(_Float16)1024.f, (_Float16)1024.f};
+    return __builtin_bit_cast(uint32_t, r);
+  } else {
+    return codes;
+  }
 }
-__device__ __forceinline__ uint32_t sub_magic1024(uint32_t v) { return sub_magic<1024>(v); }
+template <bool XS>
+__device__ __forceinline__ constexpr float enc_scale() { return XS ? 1.f : kSub; }
 
 // ---- per-type decode + dot -----------------------------------------------------------
 template <int T> struct Qmv;
@@ -96,11 +106,11 @@ template <> struct Qmv<Q4_K> {
     for (int m = 0; m < MR; ++m) acc[m] = 0.f;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      uint32_t v = q[k] >> sh;
-      dacc<MR, XS>(sub_magic1024((v & 0x000F000Fu) | 0x64006400u), x, 2 * k, acc);
-      dacc<MR, XS>(sub_magic1024(((v >> 8) & 0x000F000Fu) | 0x64006400u), x, 2 * k + 1, acc);
+      const uint32_t v = q[k] >> sh;
+      dacc<MR, XS>(enc_codes<XS>(v & 0x000F000Fu), x, 2 * k, acc);
+      dacc<MR, XS>(enc_codes<XS>((v >> 8) & 0x000F000Fu), x, 2 * k + 1, acc);
     }
-    const float s = d * (float)sc;
+    const float s = d * (float)sc * enc_scale<XS>();
     const float o = -(dmin * (float)mn);
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
@@ -130,13 +140,13 @@ template <> struct Qmv<Q2_K> {
     for (int k = 0; k < 8; ++k) {
       // 2-bit values are small next to the 1024 magic offset: remove it exactly in fp16
       // before the dot so the fp32 sums carry no cancellation.
-      uint32_t v = q[k] >> sh;
-      const uint32_t A = sub_magic1024((v & 0x00030003u) | 0x64006400u);
-      const uint32_t B = sub_magic1024(((v >> 8) & 0x00030003u) | 0x64006400u);
+      const uint32_t v = q[k] >> sh;
+      const uint32_t A = enc_codes<XS>(v & 0x00030003u);
+      const uint32_t B = enc_codes<XS>((v >> 8) & 0x00030003u);
       if (k < 4) { dacc<MR, XS>(A, x, 2 * k, a0); dacc<MR, XS>(B, x, 2 * k + 1, a0); }
       else { dacc<MR, XS>(A, x, 2 * k, a1); dacc<MR, XS>(B, x, 2 * k + 1, a1); }
     }
-    const float s0 = d * (float)(sm & 15u), s1 = d * (float)((sm >> 8) & 15u);
+    const float s0 = d * (float)(sm & 15u) * enc_scale<XS>(), s1 = d * (float)((sm >> 8) & 15u) * enc_scale<XS>();
     const float o0 = -(dmin * (float)((sm >> 4) & 15u));
     const float o1 = -(dmin * (float)((sm >> 12) & 15u));
 #pragma unroll
@@ -165,15 +175,16 @@ template <> struct Qmv<Q6_K> {
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const uint32_t L = ql[k] >> ls, H = qh[k] >> hs;
-      const uint32_t A = sub_magic<1056>((L & 0x000F000Fu) | ((H & 0x00030003u) << 4) | 0x64006400u);
-      const uint32_t B = sub_magic<1056>(((L >> 8) & 0x000F000Fu) | (((H >> 8) & 0x00030003u) << 4) | 0x64006400u);
+      const uint32_t A = enc_codes<XS>((L & 0x000F000Fu) | ((H & 0x00030003u) << 4));
+      const uint32_t B = enc_codes<XS>(((L >> 8) & 0x000F000Fu) | (((H >> 8) & 0x00030003u) << 4));
       if (k < 4) { dacc<MR, XS>(A, x, 2 * k, a0); dacc<MR, XS>(B, x, 2 * k + 1, a0); }
       else { dacc<MR, XS>(A, x, 2 * k, a1); dacc<MR, XS>(B, x, 2 * k + 1, a1); }
     }
     const float s0 = d * (float)(int)(int8_t)(sc2 & 0xFFu), s1 = d * (float)(int)(int8_t)(sc2 >> 8);
 #pragma unroll
     for (int m = 0; m < MR; ++m)
-      out[m] += s0 * a0[m] + s1 * a1[m];
+      out[m] += s0 * (enc_scale<XS>() * a0[m] - 32.f * (x.s8[m][0] + x.s8[m][1])) +
+                s1 * (enc_scale<XS>() * a1[m] - 32.f * (x.s8[m][2] + x.s8[m][3]));
   }
 };
 
@@ -493,28 +504,45 @@ template <> struct Qmv<IQ1_M> {
 
 // ---- staging: bytes [start, end) of the packed matrix -> LDS ---------------------------
 // LDS byte i of dst holds global byte (A0 + i), A0 = (packed + start) rounded down to 16.
-// Interior 16-byte chunks go through the LDS DMA path; chunks that straddle either end of
-// the packed allocation are copied byte by byte so nothing outside it is read.
-__device__ __forceinline__ void stage_rows(const uint8_t* packed, int64_t total, int64_t start, int64_t end,
-                                           uint8_t* dst, int tid, int nthr) {
+// Interior 16-byte chunks go through the LDS DMA path (global_load_lds_dwordx4). Chunks that
+// straddle either end of the packed allocation are copied byte by byte, so nothing outside
+// it is read. Returns the number of DMA instructions this wave issued (wave-uniform), which
+// the consumer uses for an exact vmcnt wait.
+__device__ __forceinline__ int stage_rows(const uint8_t* packed, int64_t total, int64_t start, int64_t end,
+                                          uint8_t* dst, int tid, int nthr) {
   const uintptr_t lo = reinterpret_cast<uintptr_t>(packed), hi = lo + (uintptr_t)total;
   const uintptr_t A0 = (lo + (uintptr_t)start) & ~(uintptr_t)15;
   const uintptr_t A1 = (lo + (uintptr_t)end + 15) & ~(uintptr_t)15;
   const int nchunks = (int)((A1 - A0) >> 4);
   const int wave = tid >> 6, lane = tid & 63, nw = nthr >> 6;
+  int issued = 0;
   for (int c0 = wave * 64; c0 < nchunks; c0 += nw * 64) {
     const int c = c0 + lane;
     const uintptr_t ca = A0 + (uintptr_t)c * 16;
-    if (c < nchunks) {
-      if (ca >= lo && ca + 16 <= hi) {
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(ca),
-                                         (__attribute__((address_space(3))) void*)(dst + c0 * 16), 16, 0, 0);
-      } else {
-        for (int k = 0; k < 16; ++k)
-          if (ca + k >= lo && ca + k < hi) dst[c * 16 + k] = *reinterpret_cast<const uint8_t*>(ca + k);
-      }
+    const bool valid = c < nchunks;
+    const bool dma = valid && ca >= lo && ca + 16 <= hi;
+    if (__builtin_amdgcn_ballot_w64(dma) != 0) ++issued;
+    if (dma) {
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(ca),
+                                       (__attribute__((address_space(3))) void*)(dst + c0 * 16), 16, 0, 0);
+    } else if (valid) {
+      for (int k = 0; k < 16; ++k)
+        if (ca + k >= lo && ca + k < hi) dst[c * 16 + k] = *reinterpret_cast<const uint8_t*>(ca + k);
     }
   }
+  return __builtin_amdgcn_readfirstlane(issued);
+}
+
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding); n is clamped to 63,
+// and a smaller immediate only waits longer.
+__device__ __forceinline__ void wait_vmcnt(int n) {
+#define GSQ_VMW(k) case k: __builtin_amdgcn_s_waitcnt(0x0F70 | ((k) & 15) | (((k) >> 4) << 14)); break;
+  switch (n < 0 ? 0 : n) {
+    GSQ_VMW(0) GSQ_VMW(1) GSQ_VMW(2) GSQ_VMW(3) GSQ_VMW(4) GSQ_VMW(5) GSQ_VMW(6) GSQ_VMW(7)
+    GSQ_VMW(8) GSQ_VMW(9) GSQ_VMW(10) GSQ_VMW(11) GSQ_VMW(12) GSQ_VMW(13) GSQ_VMW(14) GSQ_VMW(15)
+    default: __builtin_amdgcn_s_waitcnt(0x0F70 | 15); break;
+  }
+#undef GSQ_VMW
 }
 
 __device__ __forceinline__ float load_x(const void* x, int dt, int64_t i) {
@@ -526,6 +554,46 @@ __device__ __forceinline__ float load_x(const void* x, int dt, int64_t i) {
   return reinterpret_cast<const float*>(x)[i];
 }
 
+// 32 consecutive activations starting at element i0 (64-byte aligned) -> float, with
+// 16-byte vector loads all in flight before the first use; zeros when !valid.
+__device__ __forceinline__ void load_x32(const void* x, int dt, int64_t i0, bool valid, float (&xv)[32]) {
+  if (!valid) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) xv[i] = 0.f;
+    return;
+  }
+  if (dt == DT_F32) {
+    const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(x) + i0);
+    uint4 v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = p[k];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      xv[4 * k] = __builtin_bit_cast(float, v[k].x); xv[4 * k + 1] = __builtin_bit_cast(float, v[k].y);
+      xv[4 * k + 2] = __builtin_bit_cast(float, v[k].z); xv[4 * k + 3] = __builtin_bit_cast(float, v[k].w);
+    }
+  } else {
+    const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(x) + i0);
+    uint4 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = p[k];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t w[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (dt == DT_F16) {
+          xv[8 * k + 2 * j] = h2f(w[j] & 0xFFFFu);
+          xv[8 * k + 2 * j + 1] = h2f(w[j] >> 16);
+        } else {
+          xv[8 * k + 2 * j] = __builtin_bit_cast(float, w[j] << 16);
+          xv[8 * k + 2 * j + 1] = __builtin_bit_cast(float, w[j] & 0xFFFF0000u);
+        }
+      }
+    }
+  }
+}
+
 __device__ __forceinline__ void store_y(void* y, int dt, int64_t i, float v) {
   if (dt == DT_F16) reinterpret_cast<_Float16*>(y)[i] = (_Float16)v;
   else if (dt == DT_BF16) {
@@ -535,93 +603,158 @@ __device__ __forceinline__ void store_y(void* y, int dt, int64_t i, float v) {
   } else reinterpret_cast<float*>(y)[i] = v;
 }
 
-template <int T, int MR, bool XS>
-__global__ void __launch_bounds__(576) qmv_kernel(QmvArgs a) {
+// Sum over the 64 lanes of a wave with DPP row operations; the total lands in lane 63.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, ROW_MASK, 0xF, false));
+}
+
+__device__ __forceinline__ float wave_sum_to_lane63(float v) {
+  v += dpp_f<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f<0x141, 0xF>(v);  // row_half_mirror
+  v += dpp_f<0x140, 0xF>(v);  // row_mirror: every lane holds its row (16 lanes) total
+  v += dpp_f<0x142, 0xA>(v);  // row_bcast15 into rows 1 and 3
+  v += dpp_f<0x143, 0xC>(v);  // row_bcast31 into rows 2 and 3
+  return v;
+}
+
+// Register-heavy variants (4 activation rows, or 2 rows x 2 groups) run at most 512 threads.
+template <int W> struct QmvBounds { static constexpr int v = W >= 4 ? 512 : 1024; };
+
+template <int T, int MR, bool XS, int GL>
+__global__ void __launch_bounds__(QmvBounds<MR * GL>::v) qmv_kernel(QmvArgs a) {
   using P = Qmv<T>;
   constexpr int BB = BlockBytes<T>::v;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int tid = threadIdx.x, nthr = blockDim.x;
   uint8_t* tbl = smem;
-  uint8_t* bufs = smem + a.tbl_bytes;
-  float* red = reinterpret_cast<float*>(bufs + 2 * a.buf_bytes);  // [kJMax*MR][nthr]
+  float* red = reinterpret_cast<float*>(smem + a.tbl_bytes);  // [rows_per_wg][MR][Ua]
+  uint8_t* ring = smem + a.tbl_bytes + a.red_bytes;            // 3 x buf_bytes
 
   const int64_t r0 = (int64_t)blockIdx.x * a.rows_per_wg;
   const int64_t r1 = min(a.N, r0 + (int64_t)a.rows_per_wg);
   if (r0 >= r1) return;
-  if (r0 < r1) stage_rows(a.packed, a.total_bytes, r0 * a.row_bytes, min(r1, r0 + a.J) * a.row_bytes, bufs, tid, nthr);
-  P::load_tables(tbl, a.tb, tid, nthr);
-
-  const int U = a.K >> 5;
-  const bool active = tid < U;
-  const int u = active ? tid : 0;
-  const int b = u >> 3, g = u & 7;
-
-  XReg<MR, XS> xr;
-#pragma unroll
-  for (int m = 0; m < MR; ++m) {
-    float xv[32];
-#pragma unroll
-    for (int i = 0; i < 32; ++i) xv[i] = (active && m < a.M) ? load_x(a.x, a.x_dtype, (int64_t)m * a.K + 32 * u + i) : 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float s = 0.f;
-#pragma unroll
-      for (int c = 0; c < 8; ++c) s += xv[8 * i + c];
-      xr.s8[m][i] = s;
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      int e0, e1;
-      pair_idx<P::kPair>(i, e0, e1);
-      const _Float16 h0 = (_Float16)xv[e0], h1 = (_Float16)xv[e1];
-      xr.h[m][i] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-      if constexpr (XS) xr.l[m][i] = pack_h2(xv[e0] - (float)h0, xv[e1] - (float)h1);
+  const int nsteps = (int)((r1 - r0 + a.J - 1) / a.J);
+  auto step_rows = [&](int s, int64_t& rs, int64_t& re) {
+    rs = r0 + (int64_t)s * a.J;
+    re = min(r1, rs + (int64_t)a.J);
+  };
+  // DMA instructions this wave issued for the next step (kept in scalars: a runtime-indexed
+  // array would live in scratch, and scratch reads wait for every outstanding DMA)
+  int cnt_next = 0;
+  {
+    int64_t rs, re;
+    step_rows(0, rs, re);
+    stage_rows(a.packed, a.total_bytes, rs * a.row_bytes, re * a.row_bytes, ring, tid, nthr);
+    if (nsteps > 1) {
+      step_rows(1, rs, re);
+      cnt_next = stage_rows(a.packed, a.total_bytes, rs * a.row_bytes, re * a.row_bytes, ring + a.buf_bytes, tid, nthr);
     }
   }
+  P::load_tables(tbl, a.tb, tid, nthr);
 
-  int bi = 0;
-  for (int64_t rs = r0; rs < r1; rs += a.J) {
-    const int64_t re = min(r1, rs + (int64_t)a.J);
-    __builtin_amdgcn_s_waitcnt(0);
+  const int Ls = a.lanes_per_slot;
+  const int slot = min(tid / Ls, a.slots), ls = tid - min(tid / Ls, a.slots) * Ls;
+  const int U = a.K >> 5;
+  const int Ua = (U + GL - 1) / GL;  // lanes of a slot that hold partials
+  XReg<MR, XS> xr[GL];
+  int gb[GL], gg[GL];
+  bool act[GL];
+#pragma unroll
+  for (int q = 0; q < GL; ++q) {
+    const int u = ls * GL + q;
+    act[q] = slot < a.slots && u < U;
+    const int uu = act[q] ? u : 0;
+    gb[q] = uu >> 3;
+    gg[q] = uu & 7;
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      float xv[32];
+      load_x32(a.x, a.x_dtype, (int64_t)m * a.K + 32 * uu, act[q] && m < a.M, xv);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float s = 0.f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) s += xv[8 * i + c];
+        xr[q].s8[m][i] = s;
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        int e0, e1;
+        pair_idx<P::kPair>(i, e0, e1);
+        const _Float16 h0 = (_Float16)xv[e0], h1 = (_Float16)xv[e1];
+        xr[q].h[m][i] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+        if constexpr (XS) xr[q].l[m][i] = pack_h2(xv[e0] - (float)h0, xv[e1] - (float)h1);
+      }
+    }
+  }
+  const bool any_act = act[0];
+
+  for (int s = 0; s < nsteps; ++s) {
+    wait_vmcnt(s + 1 < nsteps ? cnt_next : 0);
     __syncthreads();
-    if (re < r1) stage_rows(a.packed, a.total_bytes, re * a.row_bytes, min(r1, re + a.J) * a.row_bytes,
-                            bufs + (bi ^ 1) * a.buf_bytes, tid, nthr);
-    const uint8_t* buf = bufs + bi * a.buf_bytes;
+    int cnt_after = 0;
+    if (s + 2 < nsteps) {
+      int64_t rs2, re2;
+      step_rows(s + 2, rs2, re2);
+      cnt_after = stage_rows(a.packed, a.total_bytes, rs2 * a.row_bytes, re2 * a.row_bytes,
+                             ring + ((s + 2) % 3) * a.buf_bytes, tid, nthr);
+    }
+    cnt_next = cnt_after;
+    int64_t rs, re;
+    step_rows(s, rs, re);
+    const uint8_t* buf = ring + (s % 3) * a.buf_bytes;
     const uint32_t delta = (uint32_t)((reinterpret_cast<uintptr_t>(a.packed) + (uintptr_t)(rs * a.row_bytes)) & 15u);
     const int nj = (int)(re - rs);
-    float acc[kJMax][MR];
+    if (any_act) {
+      for (int j = slot; j < nj; j += a.slots) {
+        float acc[MR];
 #pragma unroll
-    for (int j = 0; j < kJMax; ++j)
+        for (int m = 0; m < MR; ++m) acc[m] = 0.f;
 #pragma unroll
-      for (int m = 0; m < MR; ++m) acc[j][m] = 0.f;
-    if (active) {
+        for (int q = 0; q < GL; ++q)
+          if (act[q]) P::template dot<MR, XS>(buf, delta + (uint32_t)(j * a.row_bytes + gb[q] * BB), gg[q], tbl, xr[q], acc);
+        const int rl = (int)(rs - r0) + j;
 #pragma unroll
-      for (int j = 0; j < kJMax; ++j)
-        if (j < nj) P::template dot<MR, XS>(buf, delta + (uint32_t)(j * a.row_bytes + b * BB), g, tbl, xr, acc[j]);
+        for (int m = 0; m < MR; ++m) red[(rl * MR + m) * Ua + ls] = acc[m];
+      }
     }
-#pragma unroll
-    for (int j = 0; j < kJMax; ++j)
-#pragma unroll
-      for (int m = 0; m < MR; ++m)
-        if (j < nj) red[(j * MR + m) * nthr + tid] = acc[j][m];
-    __syncthreads();
-    // one wave per output (row j, activation row m)
-    const int wave = tid >> 6, lane = tid & 63, nw = nthr >> 6;
-    for (int o = wave; o < nj * MR; o += nw) {
-      float s = 0.f;
-      for (int i = lane; i < nthr; i += 64) s += red[o * nthr + i];
-#pragma unroll
-      for (int w = 32; w >= 1; w >>= 1) s += __shfl_xor(s, w, 64);
-      const int j = o / MR, m = o % MR;
-      if (lane == 0 && m < a.M) store_y(a.y, a.y_dtype, (int64_t)m * a.N + rs + j, s);
+  }
+  __syncthreads();
+  // final reduction: TPR consecutive threads per (row, activation row); each sums a
+  // contiguous run of partials, then the run sums are combined with DPP inside 16-lane rows.
+  const int nout = (int)(r1 - r0) * MR;
+  const int TPR = a.red_tpr;
+  const int per = ((Ua + TPR - 1) / TPR + 3) & ~3;
+  for (int o0 = 0; o0 < nout; o0 += nthr / TPR) {
+    const int o = o0 + tid / TPR, p = tid % TPR;
+    float v = 0.f;
+    if (o < nout) {
+      const float4* rp = reinterpret_cast<const float4*>(red + (size_t)o * Ua);
+      const int i0 = p * per, i1 = min(Ua, i0 + per);  // multiples of 4
+      float4 s4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+      for (int i = i0 >> 2; i < (i1 >> 2); ++i) {
+        const float4 t = rp[i];
+        s4.x += t.x; s4.y += t.y; s4.z += t.z; s4.w += t.w;
+      }
+      v = (s4.x + s4.y) + (s4.z + s4.w);
     }
-    bi ^= 1;
+    if (TPR >= 2) v += dpp_f<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+    if (TPR >= 4) v += dpp_f<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+    if (TPR >= 8) v += dpp_f<0x141, 0xF>(v);  // row_half_mirror
+    if (TPR >= 16) v += dpp_f<0x140, 0xF>(v); // row_mirror
+    if (o < nout && p == 0) {
+      const int rl = o / MR, m = o - rl * MR;
+      if (m < a.M) store_y(a.y, a.y_dtype, (int64_t)m * a.N + r0 + rl, v);
+    }
   }
 }
 
-template <int T, int MR, bool XS>
+template <int T, int MR, bool XS, int GL>
 static hipError_t launch_qmv_t(const QmvArgs& a, int grid, int threads, size_t lds, hipStream_t s) {
-  auto k = qmv_kernel<T, MR, XS>;
+  auto k = qmv_kernel<T, MR, XS, GL>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
@@ -635,13 +768,21 @@ static hipError_t launch_qmv_t(const QmvArgs& a, int grid, int threads, size_t l
 template <int T>
 static int qmv_tbl_bytes() { return Qmv<T>::kTbl; }
 
+template <int T, int GL>
+static hipError_t launch_qmv_gl(const QmvArgs& a, int mr, bool xs, int grid, int threads, size_t lds,
+                                hipStream_t s) {
+  if (mr == 1) return xs ? launch_qmv_t<T, 1, true, GL>(a, grid, threads, lds, s) : launch_qmv_t<T, 1, false, GL>(a, grid, threads, lds, s);
+  if (mr == 2) return xs ? launch_qmv_t<T, 2, true, GL>(a, grid, threads, lds, s) : launch_qmv_t<T, 2, false, GL>(a, grid, threads, lds, s);
+  // 4 activation rows only with fp16 activations and one group per lane (register budget)
+  if (xs || GL != 1) return hipErrorInvalidValue;
+  return launch_qmv_t<T, 4, false, 1>(a, grid, threads, lds, s);
+}
+
 template <int T>
-static hipError_t launch_qmv_type(const QmvArgs& a, int mr, bool xs, int grid, int threads, size_t lds,
+static hipError_t launch_qmv_type(const QmvArgs& a, int gl, int mr, bool xs, int grid, int threads, size_t lds,
                                   hipStream_t s) {
-  if (mr == 1) return xs ? launch_qmv_t<T, 1, true>(a, grid, threads, lds, s) : launch_qmv_t<T, 1, false>(a, grid, threads, lds, s);
-  if (mr == 2) return xs ? launch_qmv_t<T, 2, true>(a, grid, threads, lds, s) : launch_qmv_t<T, 2, false>(a, grid, threads, lds, s);
-  if (xs) return hipErrorInvalidValue;  // split-precision activations run at most 2 rows per launch
-  return launch_qmv_t<T, 4, false>(a, grid, threads, lds, s);
+  return gl == 1 ? launch_qmv_gl<T, 1>(a, mr, xs, grid, threads, lds, s)
+                 : launch_qmv_gl<T, 2>(a, mr, xs, grid, threads, lds, s);
 }
 
 int qmv_table_bytes(int qt) {
@@ -656,8 +797,10 @@ int qmv_table_bytes(int qt) {
   }
 }
 
-// Launch plan: one workgroup of K/32 lanes (rounded up to whole waves) per CU, each
-// owning N/#CU consecutive rows, J rows per double-buffered step.
+// Launch plan. One workgroup per CU, each owning ceil(N / #CU) consecutive rows (one
+// contiguous byte range). A workgroup has `slots` row slots of `lanes_per_slot` lanes;
+// lane l of a slot owns GL consecutive 32-weight groups of every row the slot processes.
+// Rows stream through a 3-deep LDS ring, J rows per step.
 hipError_t launch_qmv(int qt, const uint8_t* packed, const void* x, int xdt, void* y, int ydt, int M, int64_t N,
                       int K, const DevTables& tb, int num_cus, hipStream_t s) {
   QmvArgs a;
@@ -667,36 +810,51 @@ hipError_t launch_qmv(int qt, const uint8_t* packed, const void* x, int xdt, voi
   a.total_bytes = N * (int64_t)a.row_bytes;
   a.tbl_bytes = (qmv_table_bytes(qt) + 15) & ~15;
   const int U = K / 32;
-  const int threads = ((U + 63) / 64) * 64;
-  if (threads > kQmvMaxThreads) return hipErrorInvalidValue;
+  const int gl = U > 320 ? 2 : 1;
+  const int Ls = (U + gl - 1) / gl;  // lanes per row slot; slots need not align to waves
   const int mr = M <= 1 ? 1 : (M <= 2 ? 2 : 4);
-  if (xdt != DT_F16 && mr > 2) return hipErrorInvalidValue;
-  const int jmax = kJMax;
-  const int red_bytes = jmax * mr * threads * 4;
-  const int budget = 160 * 1024 - a.tbl_bytes - red_bytes - 256;
-  int J = (budget / 2 - 48) / a.row_bytes;
-  if (J > jmax) J = jmax;
-  if (J < 1) return hipErrorInvalidValue;
-  a.J = J;
-  a.buf_bytes = ((J * a.row_bytes + 48) + 15) & ~15;
+  const int max_threads = mr * gl >= 4 ? 512 : 1024;
+  if (Ls > max_threads) return hipErrorInvalidValue;
+  int slots = max_threads / Ls;
+  if (slots > 16) slots = 16;
+  const int threads = (slots * Ls + 63) / 64 * 64;
+  if ((xdt != DT_F16 || gl != 1) && mr > 2) return hipErrorInvalidValue;
   int grid = num_cus;
   if (N < grid) grid = (int)N;
   a.rows_per_wg = (int)((N + grid - 1) / grid);
+  const int Ua = (U + gl - 1) / gl;
+  // the per-row partials must fit in LDS next to the tables and a ring of >= 2-row steps
+  const int ring_min = 3 * (2 * a.row_bytes + 64);
+  int max_rows = (160 * 1024 - a.tbl_bytes - ring_min - 64) / (mr * Ua * 4);
+  if (max_rows < 1) max_rows = 1;
+  if (a.rows_per_wg > max_rows) a.rows_per_wg = max_rows;
   grid = (int)((N + a.rows_per_wg - 1) / a.rows_per_wg);
-  const size_t lds = (size_t)a.tbl_bytes + 2 * (size_t)a.buf_bytes + (size_t)red_bytes;
+  a.red_bytes = ((a.rows_per_wg * mr * Ua * 4) + 15) & ~15;
+  a.red_tpr = Ua >= 256 ? 16 : (Ua >= 64 ? 8 : 4);
+  const int budget = 160 * 1024 - a.tbl_bytes - a.red_bytes - 64;
+  int J = (budget / 3 - 48) / a.row_bytes;
+  if (J > a.rows_per_wg) J = a.rows_per_wg;
+  if (J > 2 * slots) J = 2 * slots;
+  if (J < 1) return hipErrorInvalidValue;
+  a.J = J;
+  a.buf_bytes = ((J * a.row_bytes + 48) + 15) & ~15;
+  a.slots = slots;
+  a.lanes_per_slot = Ls;
+  const size_t lds = (size_t)a.tbl_bytes + (size_t)a.red_bytes + 3 * (size_t)a.buf_bytes;
+  if (lds > 160 * 1024) return hipErrorInvalidValue;
   const bool xs = xdt != DT_F16;
   switch (qt) {
-    case Q2_K: return launch_qmv_type<Q2_K>(a, mr, xs, grid, threads, lds, s);
-    case Q4_K: return launch_qmv_type<Q4_K>(a, mr, xs, grid, threads, lds, s);
-    case Q6_K: return launch_qmv_type<Q6_K>(a, mr, xs, grid, threads, lds, s);
-    case IQ4_XS: return launch_qmv_type<IQ4_XS>(a, mr, xs, grid, threads, lds, s);
-    case IQ3_S: return launch_qmv_type<IQ3_S>(a, mr, xs, grid, threads, lds, s);
-    case IQ3_XXS: return launch_qmv_type<IQ3_XXS>(a, mr, xs, grid, threads, lds, s);
-    case IQ2_XXS: return launch_qmv_type<IQ2_XXS>(a, mr, xs, grid, threads, lds, s);
-    case IQ2_XS: return launch_qmv_type<IQ2_XS>(a, mr, xs, grid, threads, lds, s);
-    case IQ2_S: return launch_qmv_type<IQ2_S>(a, mr, xs, grid, threads, lds, s);
-    case IQ1_S: return launch_qmv_type<IQ1_S>(a, mr, xs, grid, threads, lds, s);
-    case IQ1_M: return launch_qmv_type<IQ1_M>(a, mr, xs, grid, threads, lds, s);
+    case Q2_K: return launch_qmv_type<Q2_K>(a, gl, mr, xs, grid, threads, lds, s);
+    case Q4_K: return launch_qmv_type<Q4_K>(a, gl, mr, xs, grid, threads, lds, s);
+    case Q6_K: return launch_qmv_type<Q6_K>(a, gl, mr, xs, grid, threads, lds, s);
+    case IQ4_XS: return launch_qmv_type<IQ4_XS>(a, gl, mr, xs, grid, threads, lds, s);
+    case IQ3_S: return launch_qmv_type<IQ3_S>(a, gl, mr, xs, grid, threads, lds, s);
+    case IQ3_XXS: return launch_qmv_type<IQ3_XXS>(a, gl, mr, xs, grid, threads, lds, s);
+    case IQ2_XXS: return launch_qmv_type<IQ2_XXS>(a, gl, mr, xs, grid, threads, lds, s);
+    case IQ2_XS: return launch_qmv_type<IQ2_XS>(a, gl, mr, xs, grid, threads, lds, s);
+    case IQ2_S: return launch_qmv_type<IQ2_S>(a, gl, mr, xs, grid, threads, lds, s);
+    case IQ1_S: return launch_qmv_type<IQ1_S>(a, gl, mr, xs, grid, threads, lds, s);
+    case IQ1_M: return launch_qmv_type<IQ1_M>(a, gl, mr, xs, grid, threads, lds, s);
     default: return hipErrorInvalidValue;
   }
 }

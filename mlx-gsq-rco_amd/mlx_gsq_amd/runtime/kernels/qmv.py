@@ -47,7 +47,7 @@ def quantized_matvec(x, packed, *, qtype: str, out_features: int, in_features: i
     original = x.shape[:-1]
     rows = x.numel() // in_features
     flat = x.reshape(rows, in_features)
-    if rows >= QMM_MIN_ROWS or in_features > 18432:
+    if rows >= QMM_MIN_ROWS or in_features > 65536:
         return quantized_matmul(flat, packed, qtype=qtype, out_features=out_features,
                                 in_features=in_features, out_dtype=out_dtype).reshape(*original, out_features)
     if qtype not in QTYPES:

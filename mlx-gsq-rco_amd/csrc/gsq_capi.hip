@@ -15,10 +15,12 @@
 namespace gsq {
 hipError_t launch_dequant(int qt, const uint8_t* packed, int64_t nblocks, float* out, const DevTables& t,
                           hipStream_t s);
-hipError_t launch_qmv(int qt, const uint8_t* packed, const void* x, int xdt, void* y, int ydt, int M, int64_t N,
+hipError_t launch_qmv(int qt, const uint8_t* packed, const void* x, int xdt, void* y, int ydt, int64_t M, int64_t N,
                       int K, const DevTables& tb, int num_cus, hipStream_t s);
 hipError_t launch_qmm(int qt, const uint8_t* packed, const void* x, int xdt, void* y, int ydt, int64_t M, int64_t N,
                       int K, const DevTables& tb, hipStream_t s);
+int qmv_table_bytes(int qt);
+bool build_qmv_table(int qt, const uint16_t* grid16, const uint8_t* ksigns, std::vector<uint8_t>& out);
 }  // namespace gsq
 
 using namespace gsq;
@@ -56,10 +58,26 @@ bool is_grid_type(int t) {
 bool uses_ksigns(int t) { return t == IQ2_XXS || t == IQ2_XS || t == IQ3_XXS; }
 
 struct DevState {
-  std::map<int, uint16_t*> grids;  // per grid type
+  std::map<int, uint16_t*> grids;     // per grid type
+  std::map<int, uint8_t*> qmv_tbls;   // per type with a QMV LDS table
   uint8_t* ksigns = nullptr;
   int num_cus = 0;
 };
+
+// Upload (or refresh) the QMV LDS table image of `qt` on the current device; caller holds g_mu.
+int upload_qmv_table(DevState& st, int qt, const uint16_t* grid16_host, const uint8_t* ksigns_host) {
+  std::vector<uint8_t> img;
+  if (!build_qmv_table(qt, grid16_host, ksigns_host, img)) return GSQ_OK;
+  uint8_t*& d = st.qmv_tbls[qt];
+  hipError_t e;
+  if (!d) {
+    e = hipMalloc(&d, img.size());
+    if (e != hipSuccess) { st.qmv_tbls.erase(qt); return fail(GSQ_E_HIP, "hipMalloc: %s", hipGetErrorString(e)); }
+  }
+  e = hipMemcpy(d, img.data(), img.size(), hipMemcpyHostToDevice);
+  if (e != hipSuccess) return fail(GSQ_E_HIP, "hipMemcpy: %s", hipGetErrorString(e));
+  return GSQ_OK;
+}
 
 std::mutex g_mu;
 std::map<int, DevState> g_dev;
@@ -82,8 +100,8 @@ int resolve(int qt, DevTables* tb, int* num_cus) {
   }
   *num_cus = st.num_cus;
   tb->grid16 = nullptr;
-  tb->ks_masks = nullptr;
   tb->ksigns = st.ksigns;
+  tb->qmv_tbl = nullptr;
   if (is_grid_type(qt)) {
     auto it = st.grids.find(qt);
     if (it == st.grids.end())
@@ -91,7 +109,12 @@ int resolve(int qt, DevTables* tb, int* num_cus) {
     tb->grid16 = it->second;
     if (uses_ksigns(qt) && !st.ksigns)
       return fail(GSQ_E_TABLES, "ksigns table is not set on device %d", dev);
+  } else if (qmv_table_bytes(qt) > 0 && !st.qmv_tbls.count(qt)) {
+    // fixed tables (IQ4_XS values) are built on first use on each device
+    if (int rc = upload_qmv_table(st, qt, nullptr, nullptr)) return rc;
   }
+  auto tt = st.qmv_tbls.find(qt);
+  if (tt != st.qmv_tbls.end()) tb->qmv_tbl = tt->second;
   return GSQ_OK;
 }
 
@@ -105,8 +128,6 @@ int check_common(int qt, const void* packed, int64_t M, int64_t N, int64_t K, in
   if (xdt < 0 || xdt > 2 || ydt < 0 || ydt > 2) return fail(GSQ_E_TYPE, "bad dtype code x=%d y=%d", xdt, ydt);
   return GSQ_OK;
 }
-
-size_t esize(int dt) { return dt == GSQ_F32 ? 4 : 2; }
 
 }  // namespace
 
@@ -157,6 +178,22 @@ int gsq_set_tables(int qt, const float* grid, int64_t entries, int64_t coords, c
   }
   e = hipMemcpy(g, h16.data(), h16.size() * 2, hipMemcpyHostToDevice);
   if (e != hipSuccess) return fail(GSQ_E_HIP, "hipMemcpy: %s", hipGetErrorString(e));
+  // the QMV kernels of every type that reads this codebook or the ksigns table
+  for (int t : {IQ1_S, IQ1_M, IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S}) {
+    if (t != qt && !(uses_ksigns(t) && st.qmv_tbls.count(t))) continue;
+    auto git = st.grids.find(t);
+    if (git == st.grids.end()) continue;
+    std::vector<uint16_t> gh;
+    if (t == qt) gh = h16;
+    else {
+      int te, tc;
+      grid_shape_of(t, &te, &tc);
+      gh.resize((size_t)te * tc);
+      e = hipMemcpy(gh.data(), git->second, gh.size() * 2, hipMemcpyDeviceToHost);
+      if (e != hipSuccess) return fail(GSQ_E_HIP, "hipMemcpy: %s", hipGetErrorString(e));
+    }
+    if (int rc = upload_qmv_table(st, t, gh.data(), ksigns)) return rc;
+  }
   return GSQ_OK;
 }
 
@@ -187,21 +224,16 @@ int gsq_qmv(int qt, const void* packed, const void* x, int xdt, void* y, int ydt
             void* stream) {
   if (int rc = check_common(qt, packed, M, N, K, xdt, ydt)) return rc;
   if (!x || !y) return fail(GSQ_E_VALUE, "NULL pointer");
-  if (K / 32 > 2048) return fail(GSQ_E_VALUE, "QMV supports K <= 65536 (got %lld); use gsq_qmm", (long long)K);
+  if (K > (xdt == GSQ_F16 ? 65536 : 32768))
+    return fail(GSQ_E_VALUE, "QMV supports K <= %d for this activation dtype (got %lld); use gsq_qmm",
+                xdt == GSQ_F16 ? 65536 : 32768, (long long)K);
   if (reinterpret_cast<uintptr_t>(x) & 15) return fail(GSQ_E_VALUE, "x must be 16-byte aligned");
   DevTables tb;
   int cus;
   if (int rc = resolve(qt, &tb, &cus)) return rc;
-  // rows per launch: 4 only for fp16 activations with K/32 <= 320 (one group per lane)
-  const int64_t chunk = (xdt == GSQ_F16 && K / 32 <= 320) ? 4 : 2;
-  for (int64_t r = 0; r < M; r += chunk) {
-    const int64_t mr = (M - r) < chunk ? (M - r) : chunk;
-    const void* xr = static_cast<const char*>(x) + r * K * esize(xdt);
-    void* yr = static_cast<char*>(y) + r * N * esize(ydt);
-    hipError_t e = launch_qmv(qt, static_cast<const uint8_t*>(packed), xr, xdt, yr, ydt, (int)mr, N, (int)K, tb, cus,
-                              static_cast<hipStream_t>(stream));
-    if (e != hipSuccess) return fail(GSQ_E_HIP, "qmv launch: %s", hipGetErrorString(e));
-  }
+  hipError_t e = launch_qmv(qt, static_cast<const uint8_t*>(packed), x, xdt, y, ydt, M, N, (int)K, tb, cus,
+                            static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(GSQ_E_HIP, "qmv launch: %s", hipGetErrorString(e));
   return GSQ_OK;
 }
 

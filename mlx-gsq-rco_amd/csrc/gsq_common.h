@@ -53,9 +53,17 @@ inline void grid_shape_of(int t, int* entries, int* coords) {
 
 // Device-resident tables for one type, built by gsq_set_tables.
 struct DevTables {
-  const uint16_t* grid16;    // fp16 codebook, entries x coords (grid types)
-  const uint32_t* ks_masks;  // [128][4] fp16-pair sign XOR masks for a ksigns index
-  const uint8_t* ksigns;     // [128]
+  const uint16_t* grid16;   // fp16 codebook, entries x coords (grid types)
+  const uint8_t* ksigns;    // [128]
+  const uint8_t* qmv_tbl;   // the QMV kernel's LDS table image of this type (see gsq_qmv.hip)
+};
+
+// Launch-plan parameters of the QMV kernel: waves per workgroup, target in-flight weight
+// bytes per CU, workgroups per CU.
+struct QmvTuning {
+  int waves;
+  int inflight_bytes;
+  int wg_per_cu;
 };
 
 // Non-linear IQ4_XS values (k_decode.py:77).

@@ -4,17 +4,29 @@
 // (mlx_gsq/runtime/kernels/qmv.py:76-528, dispatched by quantized_matvec qmv.py:537-576).
 // Layout and arithmetic follow the decoder formulas; the schedule is gfx950-specific:
 //
-// * A workgroup owns a contiguous range of whole weight rows, i.e. one contiguous byte range
-//   of the packed matrix, and streams it through LDS with direct-to-LDS DMA loads
-//   (global_load_lds_dwordx4), J rows per step, double buffered. Streams of whole rows keep
-//   HBM accesses long and sequential.
-// * Lane u of the workgroup owns 32-weight group u of every row (K/32 lanes). Its 32
-//   activations stay in registers for the whole kernel as fp16 pairs, permuted to match
-//   the type's decode pairing, with per-8 sums for the offset terms.
-// * The decode turns packed bits into fp16 pairs with magic-number ORs (K-quants), byte
-//   lookups (IQ4_XS) or LDS-resident codebook entries with sign masks (IQ types) and
-//   accumulates with v_dot2_f32_f16 in fp32. Per-group scales are applied once per group.
-// * Per step, lane partials are reduced through LDS and written as y.
+// * A "slice" is 8 consecutive superblocks (64 groups of 32 weights) of one row; lane l of a
+//   wave decodes group l of a slice (block l/8, group l%8).
+// * A wave owns up to GL consecutive slices of every row it processes (a K range, at most
+//   GL*8 superblocks) and keeps their activations in registers as fp16 pairs, permuted to
+//   match the type's decode pairing, with the partial sums the offset terms need. Rows with
+//   more slices are split across W waves (a row slot); each wave reduces its 64 lanes with
+//   DPP, and W > 1 partials are combined once at the end.
+// * Every wave streams its K range of consecutive rows (one "item" per row) through a
+//   private LDS ring with direct-to-LDS DMA loads (global_load_lds_dwordx4), nb-1 items in
+//   flight, and waits only on its own vmcnt: the main loop has no workgroup barriers, so
+//   waves never wait for each other. Every item issues the same number of DMA instructions,
+//   so the wait count is plain arithmetic.
+// * A workgroup owns a contiguous range of rows; each row slot owns a contiguous sub-range, so
+//   every wave reads long sequential spans of the packed matrix.
+// * The decode turns packed bits into fp16 pairs with masks (K-quants, small integer codes
+//   are exact fp16 subnormals), byte lookups (IQ4_XS) or LDS-resident codebook entries with
+//   sign masks (IQ types) and accumulates with v_dot2_f32_f16 in fp32. Per-group scales are
+//   applied once per group.
+// * Prologue: the type's LDS table and the activations are fetched once per workgroup (DMA),
+//   behind the first weight slices of every wave.
+#include <cstring>
+#include <vector>
+
 #include "gsq_common.h"
 
 namespace gsq {
@@ -24,10 +36,17 @@ struct QmvArgs {
   const void* x;
   void* y;
   int64_t N;
-  int64_t total_bytes;
   int K, M, x_dtype, y_dtype;
-  int rows_per_wg, J, row_bytes, buf_bytes, tbl_bytes, red_bytes;
-  int slots, lanes_per_slot, red_tpr;
+  int row_bytes;    // packed bytes per row
+  int nblk;         // superblocks per row (K / 256)
+  int nslices;      // slices per row, ceil(nblk / 8)
+  int W;            // waves per row slot (the row's slices split GL per wave)
+  int slots;        // row slots per workgroup
+  int rows_per_wg;
+  int nb;           // ring depth per wave (items)
+  int sbuf;         // bytes per ring buffer (cdma KB)
+  int cdma;         // DMA instructions per item
+  int tbl_bytes, x_off, x_bytes, x_lds, red_off, ring_off;  // LDS layout
   DevTables tb;
 };
 
@@ -43,15 +62,18 @@ __device__ __forceinline__ void pair_idx(int i, int& a, int& b) {
   else { a = i; b = i + 16; }
 }
 
-template <int MR, bool XS>
+// Activations of one 32-weight group for MR activation rows: 16 fp16 pairs (hi parts), the
+// lo parts for split-precision inputs, and NS partial sums the type's offset terms need
+// (NS=1: all 32, NS=2: the two halves of 16, NS=4: the four runs of 8).
+template <int MR, bool XS, int NS>
 struct XReg {
   uint32_t h[MR][16];
   uint32_t l[MR][XS ? 16 : 1];
-  float s8[MR][4];  // sums of elements 8i..8i+7
+  float s8[MR][NS > 0 ? NS : 1];
 };
 
-template <int MR, bool XS>
-__device__ __forceinline__ void dacc(uint32_t w, const XReg<MR, XS>& x, int i, float (&acc)[MR]) {
+template <int MR, bool XS, int NS>
+__device__ __forceinline__ void dacc(uint32_t w, const XReg<MR, XS, NS>& x, int i, float (&acc)[MR]) {
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
     acc[m] = dot2(w, x.h[m][i], acc[m]);
@@ -81,14 +103,17 @@ template <bool XS>
 __device__ __forceinline__ constexpr float enc_scale() { return XS ? 1.f : kSub; }
 
 // ---- per-type decode + dot -----------------------------------------------------------
+// Qmv<T>::kTbl is the size of the type's LDS table: an exact byte image prepared on the host
+// (build_qmv_table below) and copied into LDS with DMA at kernel start. Codebooks are fp16;
+// sign tables hold XOR masks that flip the fp16 sign bits of a pair of codebook values.
 template <int T> struct Qmv;
 
 template <> struct Qmv<Q4_K> {
   static constexpr int kPair = PAIR_K;
+  static constexpr int kSums = 1;
   static constexpr int kTbl = 0;
-  __device__ static void load_tables(uint8_t*, const DevTables&, int, int) {}
   template <int MR, bool XS>
-  __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t*, const XReg<MR, XS>& x,
+  __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t*, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
     uint32_t h[4];
     lds_words<4>(buf, off, h);
@@ -114,7 +139,7 @@ template <> struct Qmv<Q4_K> {
     const float o = -(dmin * (float)mn);
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
-      float xs = (x.s8[m][0] + x.s8[m][1]) + (x.s8[m][2] + x.s8[m][3]);
+      const float xs = x.s8[m][0];
       out[m] += s * acc[m] + o * xs;
     }
   }
@@ -122,10 +147,10 @@ template <> struct Qmv<Q4_K> {
 
 template <> struct Qmv<Q2_K> {
   static constexpr int kPair = PAIR_K;
+  static constexpr int kSums = 2;
   static constexpr int kTbl = 0;
-  __device__ static void load_tables(uint8_t*, const DevTables&, int, int) {}
   template <int MR, bool XS>
-  __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t*, const XReg<MR, XS>& x,
+  __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t*, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
     const uint32_t sm = lds_u16(buf, off + 2 * g);
     const uint32_t dd = lds_w32(buf, off + 80);
@@ -151,16 +176,16 @@ template <> struct Qmv<Q2_K> {
     const float o1 = -(dmin * (float)((sm >> 12) & 15u));
 #pragma unroll
     for (int m = 0; m < MR; ++m)
-      out[m] += s0 * a0[m] + s1 * a1[m] + o0 * (x.s8[m][0] + x.s8[m][1]) + o1 * (x.s8[m][2] + x.s8[m][3]);
+      out[m] += s0 * a0[m] + s1 * a1[m] + o0 * x.s8[m][0] + o1 * x.s8[m][1];
   }
 };
 
 template <> struct Qmv<Q6_K> {
   static constexpr int kPair = PAIR_K;
+  static constexpr int kSums = 2;
   static constexpr int kTbl = 0;
-  __device__ static void load_tables(uint8_t*, const DevTables&, int, int) {}
   template <int MR, bool XS>
-  __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t*, const XReg<MR, XS>& x,
+  __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t*, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
     const int chunk = g >> 2, plane = g & 3;
     uint32_t ql[8], qh[8];
@@ -183,21 +208,17 @@ template <> struct Qmv<Q6_K> {
     const float s0 = d * (float)(int)(int8_t)(sc2 & 0xFFu), s1 = d * (float)(int)(int8_t)(sc2 >> 8);
 #pragma unroll
     for (int m = 0; m < MR; ++m)
-      out[m] += s0 * (enc_scale<XS>() * a0[m] - 32.f * (x.s8[m][0] + x.s8[m][1])) +
-                s1 * (enc_scale<XS>() * a1[m] - 32.f * (x.s8[m][2] + x.s8[m][3]));
+      out[m] += s0 * (enc_scale<XS>() * a0[m] - 32.f * x.s8[m][0]) +
+                s1 * (enc_scale<XS>() * a1[m] - 32.f * x.s8[m][1]);
   }
 };
 
 template <> struct Qmv<IQ4_XS> {
   static constexpr int kPair = PAIR_16;
+  static constexpr int kSums = 0;
   static constexpr int kTbl = 1024;  // 256 fp16 pairs (kvalues[lo nibble], kvalues[hi nibble])
-  __device__ static void load_tables(uint8_t* tbl, const DevTables&, int tid, int nthr) {
-    uint32_t* t = reinterpret_cast<uint32_t*>(tbl);
-    for (int i = tid; i < 256; i += nthr)
-      t[i] = pack_h2((float)kIQ4Values[i & 15], (float)kIQ4Values[i >> 4]);
-  }
   template <int MR, bool XS>
-  __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS>& x,
+  __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
     const uint32_t hd = lds_w32(buf, off);
     const float d = h2f(hd & 0xFFFFu);
@@ -221,37 +242,13 @@ template <> struct Qmv<IQ4_XS> {
   }
 };
 
-// Sign masks: for sign byte s, dword i flips the fp16 signs of elements 2i (bit 15) and
-// 2i+1 (bit 31).
-__device__ __forceinline__ uint32_t sign_mask_pair(uint32_t s, int i) {
-  return (((s >> (2 * i)) & 1u) << 15) | (((s >> (2 * i + 1)) & 1u) << 31);
-}
-
-template <int ENTRIES, int COORDS>
-__device__ __forceinline__ void copy_grid(uint8_t* tbl, const DevTables& tb, int tid, int nthr) {
-  const uint4* src = reinterpret_cast<const uint4*>(tb.grid16);
-  uint4* dst = reinterpret_cast<uint4*>(tbl);
-  constexpr int n = ENTRIES * COORDS * 2 / 16;
-  for (int i = tid; i < n; i += nthr) dst[i] = src[i];
-}
-
-// 128 x 16 B sign masks of the ksigns table, after a grid of GRIDB bytes.
-__device__ __forceinline__ void build_ks_masks(uint8_t* dst, const DevTables& tb, int tid, int nthr) {
-  uint32_t* t = reinterpret_cast<uint32_t*>(dst);
-  for (int i = tid; i < 128 * 4; i += nthr) t[i] = sign_mask_pair(tb.ksigns[i >> 2], i & 3);
-}
-
 template <> struct Qmv<IQ3_S> {
   static constexpr int kPair = PAIR_NAT;
+  static constexpr int kSums = 0;
   static constexpr int kGridB = 512 * 4 * 2;
   static constexpr int kTbl = kGridB + 16 * 8;  // grid + 16 nibble sign masks
-  __device__ static void load_tables(uint8_t* tbl, const DevTables& tb, int tid, int nthr) {
-    copy_grid<512, 4>(tbl, tb, tid, nthr);
-    uint32_t* t = reinterpret_cast<uint32_t*>(tbl + kGridB);
-    for (int i = tid; i < 32; i += nthr) t[i] = sign_mask_pair(i >> 1, i & 1);
-  }
   template <int MR, bool XS>
-  __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS>& x,
+  __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
     const float d = h2f(lds_u16(buf, off));
     const uint32_t snib = (lds_u8(buf, off + 106 + (g >> 1)) >> (4 * (g & 1))) & 15u;
@@ -280,14 +277,11 @@ template <> struct Qmv<IQ3_S> {
 
 template <> struct Qmv<IQ3_XXS> {
   static constexpr int kPair = PAIR_NAT;
+  static constexpr int kSums = 0;
   static constexpr int kGridB = 256 * 4 * 2;
   static constexpr int kTbl = kGridB + 128 * 16;
-  __device__ static void load_tables(uint8_t* tbl, const DevTables& tb, int tid, int nthr) {
-    copy_grid<256, 4>(tbl, tb, tid, nthr);
-    build_ks_masks(tbl + kGridB, tb, tid, nthr);
-  }
   template <int MR, bool XS>
-  __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS>& x,
+  __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
     const float dh = h2f(lds_u16(buf, off));
     uint32_t q[2];
@@ -316,14 +310,11 @@ template <> struct Qmv<IQ3_XXS> {
 
 template <> struct Qmv<IQ2_XXS> {
   static constexpr int kPair = PAIR_NAT;
+  static constexpr int kSums = 0;
   static constexpr int kGridB = 256 * 8 * 2;
   static constexpr int kTbl = kGridB + 128 * 16;
-  __device__ static void load_tables(uint8_t* tbl, const DevTables& tb, int tid, int nthr) {
-    copy_grid<256, 8>(tbl, tb, tid, nthr);
-    build_ks_masks(tbl + kGridB, tb, tid, nthr);
-  }
   template <int MR, bool XS>
-  __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS>& x,
+  __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
     const float dh = h2f(lds_u16(buf, off));
     uint32_t q[2];
@@ -351,14 +342,11 @@ template <> struct Qmv<IQ2_XXS> {
 
 template <> struct Qmv<IQ2_XS> {
   static constexpr int kPair = PAIR_NAT;
+  static constexpr int kSums = 0;
   static constexpr int kGridB = 512 * 8 * 2;
   static constexpr int kTbl = kGridB + 128 * 16;
-  __device__ static void load_tables(uint8_t* tbl, const DevTables& tb, int tid, int nthr) {
-    copy_grid<512, 8>(tbl, tb, tid, nthr);
-    build_ks_masks(tbl + kGridB, tb, tid, nthr);
-  }
   template <int MR, bool XS>
-  __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS>& x,
+  __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
     const float dh = h2f(lds_u16(buf, off));
     uint32_t q[2];
@@ -390,15 +378,11 @@ template <> struct Qmv<IQ2_XS> {
 
 template <> struct Qmv<IQ2_S> {
   static constexpr int kPair = PAIR_NAT;
+  static constexpr int kSums = 0;
   static constexpr int kGridB = 1024 * 8 * 2;
-  static constexpr int kTbl = kGridB + 256 * 16;
-  __device__ static void load_tables(uint8_t* tbl, const DevTables& tb, int tid, int nthr) {
-    copy_grid<1024, 8>(tbl, tb, tid, nthr);
-    uint32_t* t = reinterpret_cast<uint32_t*>(tbl + kGridB);
-    for (int i = tid; i < 256 * 4; i += nthr) t[i] = sign_mask_pair(i >> 2, i & 3);
-  }
+  static constexpr int kTbl = kGridB + 256 * 16;  // grid + 256 byte sign masks
   template <int MR, bool XS>
-  __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS>& x,
+  __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
     const float dh = h2f(lds_u16(buf, off));
     const uint32_t qs = lds_w32(buf, off + 2 + 4 * g);
@@ -431,12 +415,10 @@ template <> struct Qmv<IQ2_S> {
 
 template <> struct Qmv<IQ1_S> {
   static constexpr int kPair = PAIR_NAT;
+  static constexpr int kSums = 1;
   static constexpr int kTbl = 2048 * 8 * 2;
-  __device__ static void load_tables(uint8_t* tbl, const DevTables& tb, int tid, int nthr) {
-    copy_grid<2048, 8>(tbl, tb, tid, nthr);
-  }
   template <int MR, bool XS>
-  __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS>& x,
+  __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
     const float dh = h2f(lds_u16(buf, off));
     const uint32_t qs = lds_w32(buf, off + 2 + 4 * g);
@@ -455,7 +437,7 @@ template <> struct Qmv<IQ1_S> {
     }
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
-      float xs = (x.s8[m][0] + x.s8[m][1]) + (x.s8[m][2] + x.s8[m][3]);
+      const float xs = x.s8[m][0];
       out[m] += d * (acc[m] + delta * xs);
     }
   }
@@ -463,12 +445,10 @@ template <> struct Qmv<IQ1_S> {
 
 template <> struct Qmv<IQ1_M> {
   static constexpr int kPair = PAIR_NAT;
+  static constexpr int kSums = 4;
   static constexpr int kTbl = 2048 * 8 * 2;
-  __device__ static void load_tables(uint8_t* tbl, const DevTables& tb, int tid, int nthr) {
-    copy_grid<2048, 8>(tbl, tb, tid, nthr);
-  }
   template <int MR, bool XS>
-  __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS>& x,
+  __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
     const uint32_t qs = lds_w32(buf, off + 4 * g);
     const uint32_t qh = lds_u16(buf, off + 32 + 2 * g);
@@ -502,45 +482,49 @@ template <> struct Qmv<IQ1_M> {
   }
 };
 
-// ---- staging: bytes [start, end) of the packed matrix -> LDS ---------------------------
-// LDS byte i of dst holds global byte (A0 + i), A0 = (packed + start) rounded down to 16.
-// Interior 16-byte chunks go through the LDS DMA path (global_load_lds_dwordx4). Chunks that
-// straddle either end of the packed allocation are copied byte by byte, so nothing outside
-// it is read. Returns the number of DMA instructions this wave issued (wave-uniform), which
-// the consumer uses for an exact vmcnt wait.
-__device__ __forceinline__ int stage_rows(const uint8_t* packed, int64_t total, int64_t start, int64_t end,
-                                          uint8_t* dst, int tid, int nthr) {
-  const uintptr_t lo = reinterpret_cast<uintptr_t>(packed), hi = lo + (uintptr_t)total;
-  const uintptr_t A0 = (lo + (uintptr_t)start) & ~(uintptr_t)15;
-  const uintptr_t A1 = (lo + (uintptr_t)end + 15) & ~(uintptr_t)15;
-  const int nchunks = (int)((A1 - A0) >> 4);
-  const int wave = tid >> 6, lane = tid & 63, nw = nthr >> 6;
-  int issued = 0;
-  for (int c0 = wave * 64; c0 < nchunks; c0 += nw * 64) {
-    const int c = c0 + lane;
-    const uintptr_t ca = A0 + (uintptr_t)c * 16;
-    const bool valid = c < nchunks;
-    const bool dma = valid && ca >= lo && ca + 16 <= hi;
-    if (__builtin_amdgcn_ballot_w64(dma) != 0) ++issued;
-    if (dma) {
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(ca),
-                                       (__attribute__((address_space(3))) void*)(dst + c0 * 16), 16, 0, 0);
-    } else if (valid) {
-      for (int k = 0; k < 16; ++k)
-        if (ca + k >= lo && ca + k < hi) dst[c * 16 + k] = *reinterpret_cast<const uint8_t*>(ca + k);
-    }
+// ---- staging ------------------------------------------------------------------------
+// DMA of the whole 16-byte granules covering [start, start + bytes) into LDS at dst with
+// exactly n wave instructions (lane i of instruction j writes dst + (64 j + i) * 16, so dst
+// must hold n KB). Lanes past the last granule reload the first one into their own slot,
+// which keeps the instruction count fixed. A granule that holds any byte of a tensor lies in
+// the same memory page as that byte, so the granules at an unaligned start or end of the
+// packed matrix are read whole; their bytes outside the matrix are never used.
+__device__ __forceinline__ void dma_item(uintptr_t start, int bytes, int n, uint8_t* dst, int lane) {
+  const uintptr_t A0 = start & ~(uintptr_t)15;
+  const int ngran = (int)((start + (uintptr_t)bytes + 15 - A0) >> 4);
+  for (int j = 0; j < n; ++j) {
+    const int c = j * 64 + lane;
+    const uintptr_t src = A0 + (uintptr_t)(c < ngran ? c : 0) * 16;
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
+                                     (__attribute__((address_space(3))) void*)(dst + j * 1024), 16, 0, 0);
   }
-  return __builtin_amdgcn_readfirstlane(issued);
 }
 
-// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding); n is clamped to 63,
-// and a smaller immediate only waits longer.
+// Cooperative DMA of a 16-byte aligned buffer of `bytes` (a multiple of 16) by all waves of
+// the workgroup; returns the instructions this wave issued.
+__device__ __forceinline__ int dma_copy(const void* src, int bytes, uint8_t* dst, int wave, int nw, int lane) {
+  const int ngran = bytes >> 4, per_wave = 64;
+  int issued = 0;
+  for (int c0 = wave * per_wave; c0 < ngran; c0 += nw * per_wave) {
+    const int c = c0 + lane;
+    if (c < ngran)
+      __builtin_amdgcn_global_load_lds(static_cast<const uint8_t*>(src) + (size_t)c * 16,
+                                       (__attribute__((address_space(3))) void*)(dst + c0 * 16), 16, 0, 0);
+    ++issued;
+  }
+  return issued;
+}
+
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding); n above 31 waits for
+// vmcnt(31), and a smaller immediate only waits longer.
 __device__ __forceinline__ void wait_vmcnt(int n) {
 #define GSQ_VMW(k) case k: __builtin_amdgcn_s_waitcnt(0x0F70 | ((k) & 15) | (((k) >> 4) << 14)); break;
   switch (n < 0 ? 0 : n) {
     GSQ_VMW(0) GSQ_VMW(1) GSQ_VMW(2) GSQ_VMW(3) GSQ_VMW(4) GSQ_VMW(5) GSQ_VMW(6) GSQ_VMW(7)
     GSQ_VMW(8) GSQ_VMW(9) GSQ_VMW(10) GSQ_VMW(11) GSQ_VMW(12) GSQ_VMW(13) GSQ_VMW(14) GSQ_VMW(15)
-    default: __builtin_amdgcn_s_waitcnt(0x0F70 | 15); break;
+    GSQ_VMW(16) GSQ_VMW(17) GSQ_VMW(18) GSQ_VMW(19) GSQ_VMW(20) GSQ_VMW(21) GSQ_VMW(22) GSQ_VMW(23)
+    GSQ_VMW(24) GSQ_VMW(25) GSQ_VMW(26) GSQ_VMW(27) GSQ_VMW(28) GSQ_VMW(29) GSQ_VMW(30) GSQ_VMW(31)
+    default: __builtin_amdgcn_s_waitcnt(0x0F70 | 15 | (1 << 14)); break;
   }
 #undef GSQ_VMW
 }
@@ -603,12 +587,11 @@ __device__ __forceinline__ void store_y(void* y, int dt, int64_t i, float v) {
   } else reinterpret_cast<float*>(y)[i] = v;
 }
 
-// Sum over the 64 lanes of a wave with DPP row operations; the total lands in lane 63.
+// Full-wave sum with DPP row operations; the total lands in lane 63.
 template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ float dpp_f(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, ROW_MASK, 0xF, false));
 }
-
 __device__ __forceinline__ float wave_sum_to_lane63(float v) {
   v += dpp_f<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
   v += dpp_f<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
@@ -619,133 +602,152 @@ __device__ __forceinline__ float wave_sum_to_lane63(float v) {
   return v;
 }
 
-// Register-heavy variants (4 activation rows, or 2 rows x 2 groups) run at most 512 threads.
-template <int W> struct QmvBounds { static constexpr int v = W >= 4 ? 512 : 1024; };
+// Register weight of a variant = activation rows x slices per wave, doubled for
+// split-precision (fp32/bf16) activations, which keep two fp16 parts per value. Workgroups
+// shrink as the weight grows so that no variant spills: weight <= 2: 16 waves, 3: 12 waves,
+// 4 and more: 8 waves.
+constexpr int qmv_weight(int mr, int gl, bool xs) { return mr * gl * (xs ? 2 : 1); }
+constexpr int qmv_max_threads(int w) { return w >= 4 ? 512 : (w == 3 ? 768 : 1024); }
+template <int W> struct QmvBounds { static constexpr int v = qmv_max_threads(W); };
+constexpr int kMaxRing = 16;
+
+template <int T, int MR, bool XS>
+__device__ __forceinline__ void qmv_load_x1(XReg<MR, XS, Qmv<T>::kSums>& xr, bool act, int u, const void* x, int dt,
+                                            int K, int M) {
+  constexpr int NS = Qmv<T>::kSums;
+  using P = Qmv<T>;
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    float xv[32];
+    load_x32(x, dt, (int64_t)m * K + 32 * u, act && m < M, xv);
+    if constexpr (NS > 0) {
+      float s8[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float sm = 0.f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) sm += xv[8 * i + c];
+        s8[i] = sm;
+      }
+      if constexpr (NS == 4) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xr.s8[m][i] = s8[i];
+      } else if constexpr (NS == 2) {
+        xr.s8[m][0] = s8[0] + s8[1];
+        xr.s8[m][1] = s8[2] + s8[3];
+      } else {
+        xr.s8[m][0] = (s8[0] + s8[1]) + (s8[2] + s8[3]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      int e0, e1;
+      pair_idx<P::kPair>(i, e0, e1);
+      const _Float16 h0 = (_Float16)xv[e0], h1 = (_Float16)xv[e1];
+      xr.h[m][i] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+      if constexpr (XS) xr.l[m][i] = pack_h2(xv[e0] - (float)h0, xv[e1] - (float)h1);
+    }
+  }
+}
 
 template <int T, int MR, bool XS, int GL>
-__global__ void __launch_bounds__(QmvBounds<MR * GL>::v) qmv_kernel(QmvArgs a) {
+__global__ void __launch_bounds__(QmvBounds<qmv_weight(MR, GL, XS)>::v) qmv_kernel(QmvArgs a) {
   using P = Qmv<T>;
   constexpr int BB = BlockBytes<T>::v;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
   uint8_t* tbl = smem;
-  float* red = reinterpret_cast<float*>(smem + a.tbl_bytes);  // [rows_per_wg][MR][Ua]
-  uint8_t* ring = smem + a.tbl_bytes + a.red_bytes;            // 3 x buf_bytes
+  uint8_t* xst = smem + a.x_off;
+  float* red = reinterpret_cast<float*>(smem + a.red_off);   // [rows_per_wg][MR][W] (W > 1)
+  uint8_t* ring = smem + a.ring_off + wave * a.nb * a.sbuf;  // this wave's ring
 
   const int64_t r0 = (int64_t)blockIdx.x * a.rows_per_wg;
   const int64_t r1 = min(a.N, r0 + (int64_t)a.rows_per_wg);
-  if (r0 >= r1) return;
-  const int nsteps = (int)((r1 - r0 + a.J - 1) / a.J);
-  auto step_rows = [&](int s, int64_t& rs, int64_t& re) {
-    rs = r0 + (int64_t)s * a.J;
-    re = min(r1, rs + (int64_t)a.J);
-  };
-  // DMA instructions this wave issued for the next step (kept in scalars: a runtime-indexed
-  // array would live in scratch, and scratch reads wait for every outstanding DMA)
-  int cnt_next = 0;
-  {
-    int64_t rs, re;
-    step_rows(0, rs, re);
-    stage_rows(a.packed, a.total_bytes, rs * a.row_bytes, re * a.row_bytes, ring, tid, nthr);
-    if (nsteps > 1) {
-      step_rows(1, rs, re);
-      cnt_next = stage_rows(a.packed, a.total_bytes, rs * a.row_bytes, re * a.row_bytes, ring + a.buf_bytes, tid, nthr);
-    }
+  // row slot of this wave and its K range (slices sl0 .. sl0 + nq - 1)
+  const int slot = wave / a.W, ws = wave - slot * a.W;
+  const bool live = slot < a.slots && r0 < r1;
+  int64_t sr0 = r1, sr1 = r1;
+  if (live) {
+    const int64_t nrows = r1 - r0;
+    const int64_t per = (nrows + a.slots - 1) / a.slots;
+    sr0 = min(r1, r0 + (int64_t)slot * per);
+    sr1 = min(r1, sr0 + per);
   }
-  P::load_tables(tbl, a.tb, tid, nthr);
+  const int sl0 = ws * GL;
+  const int nq = live ? max(0, min(GL, a.nslices - sl0)) : 0;
+  const int nbk = min(8 * GL, a.nblk - sl0 * 8);             // superblocks per item
+  const int item_bytes = nbk * BB;
+  const int nitems = nq > 0 ? (int)(sr1 - sr0) : 0;
+  // item t = K range of row sr0 + t
+  const uintptr_t base = reinterpret_cast<uintptr_t>(a.packed) + (uintptr_t)(sr0 * a.row_bytes + (int64_t)sl0 * 8 * BB);
 
-  const int Ls = a.lanes_per_slot;
-  const int slot = min(tid / Ls, a.slots), ls = tid - min(tid / Ls, a.slots) * Ls;
-  const int U = a.K >> 5;
-  const int Ua = (U + GL - 1) / GL;  // lanes of a slot that hold partials
-  XReg<MR, XS> xr[GL];
-  int gb[GL], gg[GL];
-  bool act[GL];
+  // ---- prologue: table + activations (once per workgroup), then this wave's first items ----
+  if constexpr (P::kTbl > 0) dma_copy(a.tb.qmv_tbl, P::kTbl, tbl, wave, nw, lane);
+  if (a.x_lds) dma_copy(a.x, a.x_bytes, xst, wave, nw, lane);
+  const int pre = min(a.nb - 1, nitems);
+  for (int i = 0; i < pre; ++i)
+    dma_item(base + (uintptr_t)i * a.row_bytes, item_bytes, a.cdma, ring + i * a.sbuf, lane);
+  wait_vmcnt(pre * a.cdma);  // this wave's share of the table and activations has landed
+  __syncthreads();           // ... and every other wave's share
+
+  XReg<MR, XS, P::kSums> xr[GL];
 #pragma unroll
   for (int q = 0; q < GL; ++q) {
-    const int u = ls * GL + q;
-    act[q] = slot < a.slots && u < U;
-    const int uu = act[q] ? u : 0;
-    gb[q] = uu >> 3;
-    gg[q] = uu & 7;
+    const int u = (sl0 + q) * 64 + lane;
+    const bool act = q < nq && u < (a.K >> 5);
+    if (a.x_lds) qmv_load_x1<T, MR, XS>(xr[q], act, act ? u : 0, xst, a.x_dtype, a.K, a.M);
+    else qmv_load_x1<T, MR, XS>(xr[q], act, act ? u : 0, a.x, a.x_dtype, a.K, a.M);
+  }
+
+  // ---- main loop: one item per row, nb-1 items in flight ----
+  int buf = 0;
+  for (int t = 0; t < nitems; ++t) {
+    wait_vmcnt(min(a.nb - 2, nitems - 1 - t) * a.cdma);  // item t has landed
+    if (t + a.nb - 1 < nitems) {
+      int nbuf = buf + a.nb - 1;
+      if (nbuf >= a.nb) nbuf -= a.nb;
+      dma_item(base + (uintptr_t)(t + a.nb - 1) * a.row_bytes, item_bytes, a.cdma, ring + nbuf * a.sbuf, lane);
+    }
+    const int64_t row = sr0 + t;
+    const uint32_t delta = (uint32_t)((base + (uintptr_t)t * a.row_bytes) & 15u);
+    const uint8_t* b = ring + buf * a.sbuf;
+    float acc[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[m] = 0.f;
+#pragma unroll
+    for (int q = 0; q < GL; ++q) {
+      if (q < nq) {
+        // lane -> group (block lane/8, group lane%8) of slice sl0 + q
+        const int blk = q * 8 + (lane >> 3);
+        const bool ok = blk < nbk;
+        float part[MR];
+#pragma unroll
+        for (int m = 0; m < MR; ++m) part[m] = 0.f;
+        P::template dot<MR, XS>(b, delta + (uint32_t)((ok ? blk : 0) * BB), lane & 7, tbl, xr[q], part);
+#pragma unroll
+        for (int m = 0; m < MR; ++m) acc[m] += ok ? part[m] : 0.f;
+      }
+    }
+    if (++buf == a.nb) buf = 0;
+    const int rl = (int)(row - r0);
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
-      float xv[32];
-      load_x32(a.x, a.x_dtype, (int64_t)m * a.K + 32 * uu, act[q] && m < a.M, xv);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float s = 0.f;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) s += xv[8 * i + c];
-        xr[q].s8[m][i] = s;
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        int e0, e1;
-        pair_idx<P::kPair>(i, e0, e1);
-        const _Float16 h0 = (_Float16)xv[e0], h1 = (_Float16)xv[e1];
-        xr[q].h[m][i] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-        if constexpr (XS) xr[q].l[m][i] = pack_h2(xv[e0] - (float)h0, xv[e1] - (float)h1);
+      const float v = wave_sum_to_lane63(acc[m]);
+      if (lane == 63) {
+        if (a.W == 1) {
+          if (m < a.M) store_y(a.y, a.y_dtype, (int64_t)m * a.N + row, v);
+        } else {
+          red[(rl * MR + m) * a.W + ws] = v;
+        }
       }
     }
   }
-  const bool any_act = act[0];
-
-  for (int s = 0; s < nsteps; ++s) {
-    wait_vmcnt(s + 1 < nsteps ? cnt_next : 0);
+  if (a.W > 1) {
     __syncthreads();
-    int cnt_after = 0;
-    if (s + 2 < nsteps) {
-      int64_t rs2, re2;
-      step_rows(s + 2, rs2, re2);
-      cnt_after = stage_rows(a.packed, a.total_bytes, rs2 * a.row_bytes, re2 * a.row_bytes,
-                             ring + ((s + 2) % 3) * a.buf_bytes, tid, nthr);
-    }
-    cnt_next = cnt_after;
-    int64_t rs, re;
-    step_rows(s, rs, re);
-    const uint8_t* buf = ring + (s % 3) * a.buf_bytes;
-    const uint32_t delta = (uint32_t)((reinterpret_cast<uintptr_t>(a.packed) + (uintptr_t)(rs * a.row_bytes)) & 15u);
-    const int nj = (int)(re - rs);
-    if (any_act) {
-      for (int j = slot; j < nj; j += a.slots) {
-        float acc[MR];
-#pragma unroll
-        for (int m = 0; m < MR; ++m) acc[m] = 0.f;
-#pragma unroll
-        for (int q = 0; q < GL; ++q)
-          if (act[q]) P::template dot<MR, XS>(buf, delta + (uint32_t)(j * a.row_bytes + gb[q] * BB), gg[q], tbl, xr[q], acc);
-        const int rl = (int)(rs - r0) + j;
-#pragma unroll
-        for (int m = 0; m < MR; ++m) red[(rl * MR + m) * Ua + ls] = acc[m];
-      }
-    }
-  }
-  __syncthreads();
-  // final reduction: TPR consecutive threads per (row, activation row); each sums a
-  // contiguous run of partials, then the run sums are combined with DPP inside 16-lane rows.
-  const int nout = (int)(r1 - r0) * MR;
-  const int TPR = a.red_tpr;
-  const int per = ((Ua + TPR - 1) / TPR + 3) & ~3;
-  for (int o0 = 0; o0 < nout; o0 += nthr / TPR) {
-    const int o = o0 + tid / TPR, p = tid % TPR;
-    float v = 0.f;
-    if (o < nout) {
-      const float4* rp = reinterpret_cast<const float4*>(red + (size_t)o * Ua);
-      const int i0 = p * per, i1 = min(Ua, i0 + per);  // multiples of 4
-      float4 s4 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-      for (int i = i0 >> 2; i < (i1 >> 2); ++i) {
-        const float4 t = rp[i];
-        s4.x += t.x; s4.y += t.y; s4.z += t.z; s4.w += t.w;
-      }
-      v = (s4.x + s4.y) + (s4.z + s4.w);
-    }
-    if (TPR >= 2) v += dpp_f<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
-    if (TPR >= 4) v += dpp_f<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
-    if (TPR >= 8) v += dpp_f<0x141, 0xF>(v);  // row_half_mirror
-    if (TPR >= 16) v += dpp_f<0x140, 0xF>(v); // row_mirror
-    if (o < nout && p == 0) {
+    const int nout = (int)(r1 - r0) * MR;
+    for (int o = tid; o < nout; o += blockDim.x) {
+      float v = 0.f;
+      for (int w = 0; w < a.W; ++w) v += red[o * a.W + w];
       const int rl = o / MR, m = o - rl * MR;
       if (m < a.M) store_y(a.y, a.y_dtype, (int64_t)m * a.N + r0 + rl, v);
     }
@@ -768,21 +770,21 @@ static hipError_t launch_qmv_t(const QmvArgs& a, int grid, int threads, size_t l
 template <int T>
 static int qmv_tbl_bytes() { return Qmv<T>::kTbl; }
 
-template <int T, int GL>
-static hipError_t launch_qmv_gl(const QmvArgs& a, int mr, bool xs, int grid, int threads, size_t lds,
-                                hipStream_t s) {
-  if (mr == 1) return xs ? launch_qmv_t<T, 1, true, GL>(a, grid, threads, lds, s) : launch_qmv_t<T, 1, false, GL>(a, grid, threads, lds, s);
-  if (mr == 2) return xs ? launch_qmv_t<T, 2, true, GL>(a, grid, threads, lds, s) : launch_qmv_t<T, 2, false, GL>(a, grid, threads, lds, s);
-  // 4 activation rows only with fp16 activations and one group per lane (register budget)
-  if (xs || GL != 1) return hipErrorInvalidValue;
-  return launch_qmv_t<T, 4, false, 1>(a, grid, threads, lds, s);
+// Slices per wave of each variant: activation registers per lane stay near 60 (fp16, one
+// activation row: 3 slices x 20) to keep 16 waves per CU resident.
+static int qmv_gl(int mr, bool xs) {
+  if (mr == 1) return xs ? 1 : 3;
+  if (mr == 2) return 1;
+  return 1;
 }
 
 template <int T>
-static hipError_t launch_qmv_type(const QmvArgs& a, int gl, int mr, bool xs, int grid, int threads, size_t lds,
+static hipError_t launch_qmv_type(const QmvArgs& a, int mr, bool xs, int grid, int threads, size_t lds,
                                   hipStream_t s) {
-  return gl == 1 ? launch_qmv_gl<T, 1>(a, mr, xs, grid, threads, lds, s)
-                 : launch_qmv_gl<T, 2>(a, mr, xs, grid, threads, lds, s);
+  if (mr == 1) return xs ? launch_qmv_t<T, 1, true, 1>(a, grid, threads, lds, s) : launch_qmv_t<T, 1, false, 3>(a, grid, threads, lds, s);
+  if (mr == 2) return xs ? launch_qmv_t<T, 2, true, 1>(a, grid, threads, lds, s) : launch_qmv_t<T, 2, false, 1>(a, grid, threads, lds, s);
+  if (mr == 4 && !xs) return launch_qmv_t<T, 4, false, 1>(a, grid, threads, lds, s);
+  return hipErrorInvalidValue;
 }
 
 int qmv_table_bytes(int qt) {
@@ -797,66 +799,144 @@ int qmv_table_bytes(int qt) {
   }
 }
 
-// Launch plan. One workgroup per CU, each owning ceil(N / #CU) consecutive rows (one
-// contiguous byte range). A workgroup has `slots` row slots of `lanes_per_slot` lanes;
-// lane l of a slot owns GL consecutive 32-weight groups of every row the slot processes.
-// Rows stream through a 3-deep LDS ring, J rows per step.
-hipError_t launch_qmv(int qt, const uint8_t* packed, const void* x, int xdt, void* y, int ydt, int M, int64_t N,
-                      int K, const DevTables& tb, int num_cus, hipStream_t s) {
+// Sign XOR mask for elements 2i (bit 15) and 2i+1 (bit 31) of sign byte s.
+static uint32_t sign_mask_pair_host(uint32_t s, int i) {
+  return (((s >> (2 * i)) & 1u) << 15) | (((s >> (2 * i + 1)) & 1u) << 31);
+}
+
+// The exact LDS table image of type qt (qmv_table_bytes(qt) bytes): the fp16 codebook
+// (grid16, entries x coords) followed by the type's sign masks, or the IQ4_XS value pairs.
+// Returns false for a type without a table.
+bool build_qmv_table(int qt, const uint16_t* grid16, const uint8_t* ksigns, std::vector<uint8_t>& out) {
+  const int bytes = qmv_table_bytes(qt);
+  if (bytes <= 0) return false;
+  out.assign((size_t)bytes, 0);
+  uint32_t* w = reinterpret_cast<uint32_t*>(out.data());
+  int grid_bytes = 0;
+  switch (qt) {
+    case IQ1_S: case IQ1_M: grid_bytes = 2048 * 8 * 2; break;
+    case IQ2_XXS: grid_bytes = 256 * 8 * 2; break;
+    case IQ2_XS: grid_bytes = 512 * 8 * 2; break;
+    case IQ2_S: grid_bytes = 1024 * 8 * 2; break;
+    case IQ3_XXS: grid_bytes = 256 * 4 * 2; break;
+    case IQ3_S: grid_bytes = 512 * 4 * 2; break;
+    default: break;
+  }
+  if (grid_bytes) std::memcpy(out.data(), grid16, (size_t)grid_bytes);
+  uint32_t* m = reinterpret_cast<uint32_t*>(out.data() + grid_bytes);
+  switch (qt) {
+    case IQ4_XS: {
+      static const int8_t kv[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+      for (int i = 0; i < 256; ++i) {
+        const _Float16 lo = (_Float16)(float)kv[i & 15], hi = (_Float16)(float)kv[i >> 4];
+        w[i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+      }
+      break;
+    }
+    case IQ3_S:  // 16 nibble masks, 2 dwords each
+      for (int i = 0; i < 32; ++i) m[i] = sign_mask_pair_host((uint32_t)(i >> 1), i & 1);
+      break;
+    case IQ2_S:  // 256 byte masks, 4 dwords each
+      for (int i = 0; i < 256 * 4; ++i) m[i] = sign_mask_pair_host((uint32_t)(i >> 2), i & 3);
+      break;
+    case IQ2_XXS: case IQ2_XS: case IQ3_XXS:  // 128 ksigns masks, 4 dwords each
+      for (int i = 0; i < 128 * 4; ++i) m[i] = sign_mask_pair_host(ksigns[i >> 2], i & 3);
+      break;
+    default: break;
+  }
+  return true;
+}
+
+static constexpr int kLdsBytes = 160 * 1024;
+
+// Launch-plan parameters: waves per workgroup, in-flight bytes per CU the ring depth aims
+// for, and workgroups per CU.
+QmvTuning g_qmv_tuning = {16, 96 * 1024, 1};
+
+// Activation rows per launch: up to 4 for fp16 activations, 2 for fp32/bf16.
+static int qmv_rows_per_launch(int xdt) { return xdt == DT_F16 ? 4 : 2; }
+
+// Launch plan for up to 4 activation rows: one workgroup of nw waves per CU, each owning about
+// N / #CU consecutive rows; W waves per row (ceil(slices / GL)), nw / W row slots.
+static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, int xdt, void* y, int ydt, int mr,
+                                  int M, int64_t N, int K, const DevTables& tb, int num_cus, hipStream_t s) {
   QmvArgs a;
   a.packed = packed; a.x = x; a.y = y; a.N = N; a.K = K; a.M = M; a.x_dtype = xdt; a.y_dtype = ydt; a.tb = tb;
   const int bb = block_bytes_of(qt);
-  a.row_bytes = (K / 256) * bb;
-  a.total_bytes = N * (int64_t)a.row_bytes;
+  a.nblk = K / 256;
+  a.row_bytes = a.nblk * bb;
+  a.nslices = (a.nblk + 7) / 8;
+  const bool xs = xdt != DT_F16;
+  const int gl = qmv_gl(mr, xs);
+  a.W = (a.nslices + gl - 1) / gl;
+  const int wpc = g_qmv_tuning.wg_per_cu < 1 ? 1 : g_qmv_tuning.wg_per_cu;
+  const int max_waves = qmv_max_threads(qmv_weight(mr, gl, xs)) / 64;
   a.tbl_bytes = (qmv_table_bytes(qt) + 15) & ~15;
-  const int U = K / 32;
-  const int gl = U > 320 ? 2 : 1;
-  const int Ls = (U + gl - 1) / gl;  // lanes per row slot; slots need not align to waves
-  const int mr = M <= 1 ? 1 : (M <= 2 ? 2 : 4);
-  const int max_threads = mr * gl >= 4 ? 512 : 1024;
-  if (Ls > max_threads) return hipErrorInvalidValue;
-  int slots = max_threads / Ls;
-  if (slots > 16) slots = 16;
-  const int threads = (slots * Ls + 63) / 64 * 64;
-  if ((xdt != DT_F16 || gl != 1) && mr > 2) return hipErrorInvalidValue;
-  int grid = num_cus;
+  if (a.tbl_bytes > 0 && !tb.qmv_tbl) return hipErrorInvalidValue;
+  const int lds_cap = kLdsBytes / wpc;
+  a.x_bytes = M * K * (xdt == DT_F32 ? 4 : 2);
+  // item: GL slices of a row (+15 bytes of granule alignment, +4 of decoder over-read)
+  const int item_bytes = (a.nblk < 8 * gl ? a.nblk : 8 * gl) * bb;
+  a.cdma = (item_bytes + 19 + 1023) / 1024;
+  a.sbuf = a.cdma * 1024;
+  // waves: as many as the variant allows (a multiple of W) unless the tuning asks for fewer
+  int nw = g_qmv_tuning.waves < 1 ? 1 : g_qmv_tuning.waves;
+  if (nw > max_waves) nw = max_waves;
+  if (a.W > max_waves) return hipErrorInvalidValue;
+  if (nw < a.W) nw = a.W;
+  a.slots = nw / a.W;
+  nw = a.slots * a.W;
+  int grid = num_cus * wpc;
   if (N < grid) grid = (int)N;
   a.rows_per_wg = (int)((N + grid - 1) / grid);
-  const int Ua = (U + gl - 1) / gl;
-  // the per-row partials must fit in LDS next to the tables and a ring of >= 2-row steps
-  const int ring_min = 3 * (2 * a.row_bytes + 64);
-  int max_rows = (160 * 1024 - a.tbl_bytes - ring_min - 64) / (mr * Ua * 4);
-  if (max_rows < 1) max_rows = 1;
-  if (a.rows_per_wg > max_rows) a.rows_per_wg = max_rows;
   grid = (int)((N + a.rows_per_wg - 1) / a.rows_per_wg);
-  a.red_bytes = ((a.rows_per_wg * mr * Ua * 4) + 15) & ~15;
-  a.red_tpr = Ua >= 256 ? 16 : (Ua >= 64 ? 8 : 4);
-  const int budget = 160 * 1024 - a.tbl_bytes - a.red_bytes - 64;
-  int J = (budget / 3 - 48) / a.row_bytes;
-  if (J > a.rows_per_wg) J = a.rows_per_wg;
-  if (J > 2 * slots) J = 2 * slots;
-  if (J < 1) return hipErrorInvalidValue;
-  a.J = J;
-  a.buf_bytes = ((J * a.row_bytes + 48) + 15) & ~15;
-  a.slots = slots;
-  a.lanes_per_slot = Ls;
-  const size_t lds = (size_t)a.tbl_bytes + (size_t)a.red_bytes + 3 * (size_t)a.buf_bytes;
-  if (lds > 160 * 1024) return hipErrorInvalidValue;
-  const bool xs = xdt != DT_F16;
+  const int red_bytes = a.W > 1 ? ((a.rows_per_wg * mr * a.W * 4 + 15) & ~15) : 0;
+  // activations go to LDS only if the ring keeps at least 3 items per wave
+  a.x_lds = (a.tbl_bytes + a.x_bytes + red_bytes + nw * 3 * a.sbuf <= lds_cap) ? 1 : 0;
+  a.x_off = a.tbl_bytes;
+  a.red_off = a.x_off + (a.x_lds ? a.x_bytes : 0);
+  a.ring_off = a.red_off + red_bytes;
+  int nb = (lds_cap - a.ring_off) / (nw * a.sbuf);
+  // in-flight target per CU: nw * (nb - 1) items
+  const int want = 1 + (g_qmv_tuning.inflight_bytes * wpc / (item_bytes > 0 ? item_bytes : 1) + nw - 1) / nw;
+  if (nb > want) nb = want;
+  if (nb > kMaxRing) nb = kMaxRing;
+  while (nb > 2 && (nb - 2) * a.cdma > 31) --nb;  // exact vmcnt waits go up to 31
+  if (nb < 2) return hipErrorInvalidValue;
+  a.nb = nb;
+  const int threads = nw * 64;
+  const size_t lds = (size_t)a.ring_off + (size_t)nw * nb * a.sbuf;
+  if (lds > (size_t)lds_cap) return hipErrorInvalidValue;
   switch (qt) {
-    case Q2_K: return launch_qmv_type<Q2_K>(a, gl, mr, xs, grid, threads, lds, s);
-    case Q4_K: return launch_qmv_type<Q4_K>(a, gl, mr, xs, grid, threads, lds, s);
-    case Q6_K: return launch_qmv_type<Q6_K>(a, gl, mr, xs, grid, threads, lds, s);
-    case IQ4_XS: return launch_qmv_type<IQ4_XS>(a, gl, mr, xs, grid, threads, lds, s);
-    case IQ3_S: return launch_qmv_type<IQ3_S>(a, gl, mr, xs, grid, threads, lds, s);
-    case IQ3_XXS: return launch_qmv_type<IQ3_XXS>(a, gl, mr, xs, grid, threads, lds, s);
-    case IQ2_XXS: return launch_qmv_type<IQ2_XXS>(a, gl, mr, xs, grid, threads, lds, s);
-    case IQ2_XS: return launch_qmv_type<IQ2_XS>(a, gl, mr, xs, grid, threads, lds, s);
-    case IQ2_S: return launch_qmv_type<IQ2_S>(a, gl, mr, xs, grid, threads, lds, s);
-    case IQ1_S: return launch_qmv_type<IQ1_S>(a, gl, mr, xs, grid, threads, lds, s);
-    case IQ1_M: return launch_qmv_type<IQ1_M>(a, gl, mr, xs, grid, threads, lds, s);
+    case Q2_K: return launch_qmv_type<Q2_K>(a, mr, xs, grid, threads, lds, s);
+    case Q4_K: return launch_qmv_type<Q4_K>(a, mr, xs, grid, threads, lds, s);
+    case Q6_K: return launch_qmv_type<Q6_K>(a, mr, xs, grid, threads, lds, s);
+    case IQ4_XS: return launch_qmv_type<IQ4_XS>(a, mr, xs, grid, threads, lds, s);
+    case IQ3_S: return launch_qmv_type<IQ3_S>(a, mr, xs, grid, threads, lds, s);
+    case IQ3_XXS: return launch_qmv_type<IQ3_XXS>(a, mr, xs, grid, threads, lds, s);
+    case IQ2_XXS: return launch_qmv_type<IQ2_XXS>(a, mr, xs, grid, threads, lds, s);
+    case IQ2_XS: return launch_qmv_type<IQ2_XS>(a, mr, xs, grid, threads, lds, s);
+    case IQ2_S: return launch_qmv_type<IQ2_S>(a, mr, xs, grid, threads, lds, s);
+    case IQ1_S: return launch_qmv_type<IQ1_S>(a, mr, xs, grid, threads, lds, s);
+    case IQ1_M: return launch_qmv_type<IQ1_M>(a, mr, xs, grid, threads, lds, s);
     default: return hipErrorInvalidValue;
   }
+}
+
+// y[M, N] = x[M, K] W^T: activation rows go out in launches of up to 4 (2 for fp32/bf16).
+hipError_t launch_qmv(int qt, const uint8_t* packed, const void* x, int xdt, void* y, int ydt, int64_t M, int64_t N,
+                      int K, const DevTables& tb, int num_cus, hipStream_t s) {
+  const int chunk = qmv_rows_per_launch(xdt);
+  const size_t xe = xdt == DT_F32 ? 4 : 2, ye = ydt == DT_F32 ? 4 : 2;
+  for (int64_t r = 0; r < M; r += chunk) {
+    const int mrow = (int)((M - r) < chunk ? (M - r) : chunk);
+    const int mr = mrow <= 1 ? 1 : (mrow <= 2 ? 2 : 4);
+    const void* xr = static_cast<const char*>(x) + r * K * xe;
+    void* yr = static_cast<char*>(y) + r * N * ye;
+    hipError_t e = launch_qmv_rows(qt, packed, xr, xdt, yr, ydt, mr, mrow, N, K, tb, num_cus, s);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 }  // namespace gsq

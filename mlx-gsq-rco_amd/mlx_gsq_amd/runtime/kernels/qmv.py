@@ -47,7 +47,10 @@ def quantized_matvec(x, packed, *, qtype: str, out_features: int, in_features: i
     original = x.shape[:-1]
     rows = x.numel() // in_features
     flat = x.reshape(rows, in_features)
-    if rows >= QMM_MIN_ROWS or in_features > 65536:
+    # the fused QMV keeps a row's activations in registers: K <= 65536 for fp16 activations,
+    # K <= 32768 for fp32/bf16 (split into two fp16 parts); wider rows go to the tiled QMM
+    max_k = 65536 if x.dtype == torch.float16 else 32768
+    if rows >= QMM_MIN_ROWS or in_features > max_k:
         return quantized_matmul(flat, packed, qtype=qtype, out_features=out_features,
                                 in_features=in_features, out_dtype=out_dtype).reshape(*original, out_features)
     if qtype not in QTYPES:

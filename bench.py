@@ -3,24 +3,34 @@
 Workload: fused QMV at M=1 over all 11 types on the 27B layer
 shapes N x K in {5120x5120, 1024x5120, 17408x5120, 5120x17408}. One step = one pass over
 the 44 (type, shape) products with seeded random packed weights resident in HBM (about
-0.9 GB of distinct weights, larger than the 256 MB MALL, so every launch streams from HBM).
+0.9 GB of distinct weights, well beyond the 256 MB MALL, so every launch streams its weights
+from HBM). The step is captured once in a HIP graph and replayed; the eager (one launch call
+per product) step time is reported beside it.
 
-Printed JSON line:
-  value      whole-step HBM throughput: algorithmic bytes of the 44 launches / step time
-  roofline   the dominant QMV kernel (largest share of step time): its algorithmic bytes
-             per launch / its average launch time from HIP events on the launch stream,
-             against the 8 TB/s HBM peak
-  per_type   per-type GB/s and fraction of peak over its 4 shapes
-  qmm        tiled QMM at M=512 (configs[2] subset): TFLOP/s and fraction of dense fp16 peak
+Printed JSON line (one, on stdout):
+  value         whole-step throughput: algorithmic bytes of the 44 launches / graph step time
+  roofline      the dominant QMV launch (largest share of kernel time): its algorithmic bytes
+                / its median duration from HIP events around that launch on the launch
+                stream, against the 8 TB/s HBM peak; `traffic` comes from the committed
+                rocprofv3 counter summary (profiles/qmv_traffic.json) when it covers the
+                same kernel and shape, else null
+  per_type      per-type GB/s and fraction of peak over its 4 shapes (kernel time)
+  per_launch_us median kernel time of every (type, shape)
+  qmm           tiled QMM at M=512 (configs[2] subset): TFLOP/s and fraction of dense fp16 peak
   cpu_baseline  the numpy oracle (dequant + float32 matmul, one thread) on a bounded sample
 
 Algorithmic bytes per QMV launch = N*(K/256)*block_bytes + M*K*2 (x fp16) + M*N*4 (y fp32).
+
+Extra modes for counter collection (rocprofv3 --pmc runs):
+  --profile-case Q6_K:17408x5120   only launches of that product (rotating 8 weight copies)
+  --copy-bytes N                   only a plain device-to-device copy of N bytes
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -31,6 +41,7 @@ HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
 SHAPES = ((5120, 5120), (1024, 5120), (17408, 5120), (5120, 17408))
 METRIC = "QMV GB/s & % HBM peak (M=1); QMM TFLOPS & % MFMA peak (M=512); per type"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qmv_traffic.json")
 
 
 def log(*a):
@@ -98,69 +109,84 @@ def cpu_baseline(budget_s: float = 12.0):
             "matmul_only_s_per_pass": round(mm_t / reps, 4), "host_cpus": os.cpu_count()}
 
 
-def run_qmv_sweep(steps, warmup, device):
+class QmvCases:
+    """The 44 (type, shape) products of one step, resident on the device."""
+
+    def __init__(self, device):
+        import torch
+        from mlx_gsq_amd import _lib, tables
+        from mlx_gsq_amd.formats import QTYPES, TYPE_IDS
+        self.lib = _lib.lib()
+        self.torch = torch
+        tables.set_tables(tables.synthetic_tables(0))
+        self.cases = []
+        for ti, q in enumerate(QTYPES):
+            _lib.ensure_tables(q, device)
+            for si, (n, k) in enumerate(SHAPES):
+                packed = make_device_packed(q, n, k, seed=1000 + 10 * ti + si, device=device)
+                x = torch.randn(1, k, device=device, generator=torch.Generator(device=device).manual_seed(si)).half()
+                y = torch.empty(1, n, device=device, dtype=torch.float32)
+                self.cases.append((q, TYPE_IDS[q], n, k, packed, x, y))
+        torch.cuda.synchronize()
+        log(f"resident packed weights: {sum(c[4].numel() for c in self.cases) / 1e9:.3f} GB in {len(self.cases)} matrices")
+
+    def launch(self, c, stream):
+        q, tid, n, k, packed, x, y = c
+        rc = self.lib.gsq_qmv(tid, packed.data_ptr(), x.data_ptr(), 1, y.data_ptr(), 0, 1, n, k, stream)
+        if rc:
+            raise RuntimeError(self.lib.gsq_last_error().decode())
+
+    def step_bytes(self):
+        return sum(qmv_bytes(c[0], c[2], c[3]) for c in self.cases)
+
+
+def run_qmv(steps, warmup, device):
     import torch
-    from mlx_gsq_amd import _lib, tables
-    from mlx_gsq_amd.formats import QTYPES, TYPE_IDS
-    lib = _lib.lib()
-    tables.set_tables(tables.synthetic_tables(0))
-    cases = []
-    for ti, q in enumerate(QTYPES):
-        _lib.ensure_tables(q, device)
-        for si, (n, k) in enumerate(SHAPES):
-            packed = make_device_packed(q, n, k, seed=1000 + 10 * ti + si, device=device)
-            x = torch.randn(1, k, device=device, generator=torch.Generator(device=device).manual_seed(si)).half()
-            y = torch.empty(1, n, device=device, dtype=torch.float32)
-            cases.append((q, n, k, packed, x, y))
-    torch.cuda.synchronize()
-    log(f"resident packed weights: {sum(c[3].numel() for c in cases) / 1e9:.3f} GB in {len(cases)} matrices")
+    qc = QmvCases(device)
     stream = torch.cuda.current_stream(device)
     sh = stream.cuda_stream
-
-    def launch(c):
-        q, n, k, packed, x, y = c
-        rc = lib.gsq_qmv(TYPE_IDS[q], packed.data_ptr(), x.data_ptr(), 1, y.data_ptr(), 0, 1, n, k, sh)
-        if rc:
-            raise RuntimeError(lib.gsq_last_error().decode())
-
     for _ in range(warmup):
-        for c in cases:
-            launch(c)
+        for c in qc.cases:
+            qc.launch(c, sh)
     torch.cuda.synchronize()
-    # per-type event brackets (launches of one type are contiguous in `cases`)
-    ntypes = len(QTYPES)
-    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(ntypes)]
+    # eager pass with an event pair around every launch: per-launch kernel time
+    nc = len(qc.cases)
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(nc)]
            for _ in range(steps)]
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record(stream)
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
     for s in range(steps):
-        for ti in range(ntypes):
-            evs[s][ti][0].record(stream)
-            for c in cases[4 * ti: 4 * ti + 4]:
-                launch(c)
-            evs[s][ti][1].record(stream)
-    stop.record(stream)
+        for i, c in enumerate(qc.cases):
+            evs[s][i][0].record(stream)
+            qc.launch(c, sh)
+            evs[s][i][1].record(stream)
+    t1.record(stream)
     torch.cuda.synchronize()
-    total_ms = start.elapsed_time(stop)
-    type_ms = [sum(evs[s][ti][0].elapsed_time(evs[s][ti][1]) for s in range(steps)) for ti in range(ntypes)]
-    step_bytes = sum(qmv_bytes(c[0], c[1], c[2]) for c in cases)
-    per_type = {}
-    for ti, q in enumerate(QTYPES):
-        b = sum(qmv_bytes(q, n, k) for (n, k) in SHAPES)
-        gbs = b * steps / (type_ms[ti] * 1e-3) / 1e9
-        per_type[q] = {"GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
-                       "us_per_launch": round(type_ms[ti] * 1e3 / steps / 4, 2)}
-    dom = max(range(ntypes), key=lambda i: type_ms[i])
-    dq = QTYPES[dom]
-    dom_bytes = sum(qmv_bytes(dq, n, k) for (n, k) in SHAPES) / 4
-    dom_us = type_ms[dom] * 1e3 / steps / 4
-    return {
-        "total_ms": total_ms, "step_bytes": step_bytes, "per_type": per_type,
-        "dominant": {"kernel": f"qmv_kernel<{dq}> (type id {TYPE_IDS[dq]})", "qtype": dq,
-                     "bytes_per_launch": dom_bytes, "us_per_launch": dom_us},
-        "mean_type_frac": sum(v["frac"] for v in per_type.values()) / ntypes,
-    }
+    eager_ms = t0.elapsed_time(t1) / steps
+    per_launch = [statistics.median(evs[s][i][0].elapsed_time(evs[s][i][1]) for s in range(steps)) * 1e3
+                  for i in range(nc)]
+    # graph: one step captured once, replayed `steps` times
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream(device)
+    cap.wait_stream(stream)
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(graph, stream=cap):
+            for c in qc.cases:
+                qc.launch(c, torch.cuda.current_stream(device).cuda_stream)
+    stream.wait_stream(cap)
+    for _ in range(max(1, warmup)):
+        graph.replay()
+    torch.cuda.synchronize()
+    g0 = torch.cuda.Event(enable_timing=True)
+    g1 = torch.cuda.Event(enable_timing=True)
+    g0.record(stream)
+    for _ in range(steps):
+        graph.replay()
+    g1.record(stream)
+    torch.cuda.synchronize()
+    graph_ms = g0.elapsed_time(g1) / steps
+    return qc, per_launch, eager_ms, graph_ms
 
 
 def run_qmm(device, reps=10):
@@ -171,6 +197,7 @@ def run_qmm(device, reps=10):
     out = {}
     stream = torch.cuda.current_stream(device)
     for q in ("IQ3_S", "Q6_K"):
+        _lib.ensure_tables(q, device)
         for (n, k) in ((17408, 5120), (5120, 17408)):
             m = 512
             packed = make_device_packed(q, n, k, seed=77, device=device)
@@ -193,13 +220,59 @@ def run_qmm(device, reps=10):
     return out
 
 
+def profile_case(spec, reps, device):
+    """Launch one (type, shape) product `reps` times over 8 rotating weight copies."""
+    import torch
+    from mlx_gsq_amd import _lib, tables
+    from mlx_gsq_amd.formats import TYPE_IDS
+    q, shape = spec.split(":")
+    n, k = (int(v) for v in shape.split("x"))
+    tables.set_tables(tables.synthetic_tables(0))
+    _lib.ensure_tables(q, device)
+    lib = _lib.lib()
+    copies = [make_device_packed(q, n, k, seed=500 + i, device=device) for i in range(8)]
+    x = torch.randn(1, k, device=device).half()
+    y = torch.empty(1, n, device=device, dtype=torch.float32)
+    sh = torch.cuda.current_stream(device).cuda_stream
+    for i in range(reps):
+        rc = lib.gsq_qmv(TYPE_IDS[q], copies[i % 8].data_ptr(), x.data_ptr(), 1, y.data_ptr(), 0, 1, n, k, sh)
+        assert rc == 0, lib.gsq_last_error()
+    torch.cuda.synchronize()
+    print(json.dumps({"profile_case": spec, "reps": reps, "bytes_per_launch": qmv_bytes(q, n, k)}), flush=True)
+
+
+def copy_case(nbytes, reps, device):
+    """Plain device-to-device copy of `nbytes` (the counter scale reference)."""
+    import torch
+    src = torch.randint(0, 255, (nbytes,), dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": nbytes, "reps": reps}), flush=True)
+
+
+def load_traffic(kernel_case):
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if t.get("case") != kernel_case:
+        return None
+    return t.get("hbm_bytes_per_launch")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-qmm", action="store_true")
+    ap.add_argument("--profile-case", default=None, help="TYPE:NxK, launch only that product")
+    ap.add_argument("--copy-bytes", type=int, default=0, help="run only a plain copy of this many bytes")
+    ap.add_argument("--reps", type=int, default=20)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this path has no multi-GPU mode "
@@ -208,25 +281,50 @@ def main():
     import torch
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
-    res = run_qmv_sweep(args.steps, args.warmup, device)
+    if args.copy_bytes:
+        copy_case(args.copy_bytes, args.reps, device)
+        return
+    if args.profile_case:
+        profile_case(args.profile_case, args.reps, device)
+        return
+    qc, per_launch, eager_ms, graph_ms = run_qmv(args.steps, args.warmup, device)
     qmm = {} if args.no_qmm else run_qmm(device)
     cpu = None if args.no_cpu else cpu_baseline()
-    ms_per_step = res["total_ms"] / args.steps
-    value = res["step_bytes"] / (ms_per_step * 1e-3) / 1e9
-    dom = res["dominant"]
-    achieved = dom["bytes_per_launch"] / (dom["us_per_launch"] * 1e-6) / 1e9
+    from mlx_gsq_amd.formats import QTYPES
+    step_bytes = qc.step_bytes()
+    value = step_bytes / (graph_ms * 1e-3) / 1e9
+    per_type = {}
+    launches = {}
+    for i, c in enumerate(qc.cases):
+        launches[f"{c[0]} {c[2]}x{c[3]}"] = round(per_launch[i], 2)
+    for ti, q in enumerate(QTYPES):
+        idx = range(4 * ti, 4 * ti + 4)
+        b = sum(qmv_bytes(qc.cases[i][0], qc.cases[i][2], qc.cases[i][3]) for i in idx)
+        us = sum(per_launch[i] for i in idx)
+        gbs = b / (us * 1e-6) / 1e9
+        per_type[q] = {"GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    dom = max(range(len(qc.cases)), key=lambda i: per_launch[i])
+    dq, _, dn, dk = qc.cases[dom][:4]
+    dom_case = f"{dq} {dn}x{dk}"
+    dom_bytes = qmv_bytes(dq, dn, dk)
+    achieved = dom_bytes / (per_launch[dom] * 1e-6) / 1e9
+    kernel_time = sum(per_launch) * 1e-6
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+        "warmup": args.warmup, "ms_per_step": round(graph_ms, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
         "config": {"workload": "configs[1]: QMV M=1, 11 types x NxK {5120x5120,1024x5120,17408x5120,5120x17408}",
-                   "global_batch": 1, "launches_per_step": 44, "x": "fp16", "y": "fp32"},
+                   "global_batch": 1, "launches_per_step": len(qc.cases), "x": "fp16", "y": "fp32",
+                   "step": "one HIP graph of the 44 launches"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": dom["kernel"], "bytes_per_launch": int(dom["bytes_per_launch"]),
-                     "us_per_launch": round(dom["us_per_launch"], 3)},
-        "mean_type_frac": round(res["mean_type_frac"], 4),
-        "per_type": res["per_type"],
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(dom_case),
+                     "kernel": f"qmv_kernel<{dq}> M=1", "case": dom_case, "bytes_per_launch": int(dom_bytes),
+                     "us_per_launch": round(per_launch[dom], 3)},
+        "eager_ms_per_step": round(eager_ms, 4),
+        "kernel_time_GBs": round(step_bytes / kernel_time / 1e9, 1),
+        "mean_type_frac": round(sum(v["frac"] for v in per_type.values()) / len(per_type), 4),
+        "per_type": per_type,
+        "per_launch_us": launches,
         "qmm": qmm,
         "cpu_baseline": cpu,
     }

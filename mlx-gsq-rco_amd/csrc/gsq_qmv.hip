@@ -851,7 +851,7 @@ static constexpr int kLdsBytes = 160 * 1024;
 
 // Launch-plan parameters: waves per workgroup, in-flight bytes per CU the ring depth aims
 // for, and workgroups per CU.
-QmvTuning g_qmv_tuning = {16, 96 * 1024, 1};
+QmvTuning g_qmv_tuning = {12, 96 * 1024, 1};
 
 // Activation rows per launch: up to 4 for fp16 activations, 2 for fp32/bf16.
 static int qmv_rows_per_launch(int xdt) { return xdt == DT_F16 ? 4 : 2; }

@@ -192,3 +192,40 @@ def test_deterministic_repeat():
     a = quantized_matvec(x, packed, qtype="IQ3_XXS", out_features=N, in_features=K, out_dtype=torch.float32)
     b = quantized_matvec(x, packed, qtype="IQ3_XXS", out_features=N, in_features=K, out_dtype=torch.float32)
     assert torch.equal(a, b)
+
+
+def test_qmv_hip_graph_replays_match_eager():
+    """The QMV launches captured in a HIP graph reproduce the eager results on every replay."""
+    from mlx_gsq_amd import _lib
+    from mlx_gsq_amd.formats import TYPE_IDS
+    lib = _lib.lib()
+    cases = []
+    for i, qtype in enumerate(("Q4_K", "IQ2_S", "IQ1_M", "Q6_K")):
+        N, K = 777, 1280
+        packed = dev(synth.make_packed(qtype, N, K, seed=60 + i))
+        x = dev(synth.make_x(1, K, seed=70 + i, dtype=np.float16))
+        _lib.ensure_tables(qtype, packed.device)
+        cases.append((TYPE_IDS[qtype], packed, x, torch.empty(1, N, device="cuda"), N, K))
+
+    def launch_all(stream):
+        for tid, packed, x, y, N, K in cases:
+            assert lib.gsq_qmv(tid, packed.data_ptr(), x.data_ptr(), 1, y.data_ptr(), 0, 1, N, K, stream) == 0
+
+    launch_all(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    eager = [c[3].clone() for c in cases]
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(graph, stream=cap):
+            launch_all(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.current_stream().wait_stream(cap)
+    for rep in range(4):
+        for c in cases:
+            c[3].fill_(float("nan"))          # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for c, e in zip(cases, eager):
+            assert torch.equal(c[3], e), f"replay {rep} differs"

@@ -93,21 +93,31 @@ __device__ __forceinline__ uint32_t gu32(const uint8_t* p, int i) {
   return (uint32_t)p[i] | ((uint32_t)p[i + 1] << 8) | ((uint32_t)p[i + 2] << 16) | ((uint32_t)p[i + 3] << 24);
 }
 
-// LDS: N consecutive 32-bit words starting at an even byte offset (blocks are only
-// 2-byte aligned). Reads N+1 aligned words and funnel-shifts them into place.
-template <int N>
+// LDS: N consecutive 32-bit words starting at an even byte offset (superblocks are only
+// 2-byte aligned). A4 = the offset is known to be a multiple of 4: plain dword loads.
+// Otherwise N+1 aligned dwords are read and funnel-shifted into place: gfx950 LDS does serve
+// ds_read_b32/b64/b128 at 2-byte aligned addresses, but such reads stall the LDS pipeline
+// (SQ_LDS_UNALIGNED_STALL), which costs more than one v_alignbyte per word.
+template <int N, bool A4 = false>
 __device__ __forceinline__ void lds_words(const uint8_t* base, uint32_t off, uint32_t (&w)[N]) {
-  const uint32_t* p = reinterpret_cast<const uint32_t*>(base + (off & ~3u));
-  uint32_t sh = off & 3u;
-  uint32_t a[N + 1];
+  if constexpr (A4) {
+    const uint32_t* p = reinterpret_cast<const uint32_t*>(base + off);
 #pragma unroll
-  for (int i = 0; i <= N; ++i) a[i] = p[i];
+    for (int i = 0; i < N; ++i) w[i] = p[i];
+  } else {
+    const uint32_t* p = reinterpret_cast<const uint32_t*>(base + (off & ~3u));
+    const uint32_t sh = off & 3u;
+    uint32_t a[N + 1];
 #pragma unroll
-  for (int i = 0; i < N; ++i) w[i] = __builtin_amdgcn_alignbyte(a[i + 1], a[i], sh);
+    for (int i = 0; i <= N; ++i) a[i] = p[i];
+#pragma unroll
+    for (int i = 0; i < N; ++i) w[i] = __builtin_amdgcn_alignbyte(a[i + 1], a[i], sh);
+  }
 }
+template <bool A4 = false>
 __device__ __forceinline__ uint32_t lds_w32(const uint8_t* base, uint32_t off) {
   uint32_t w[1];
-  lds_words<1>(base, off, w);
+  lds_words<1, A4>(base, off, w);
   return w[0];
 }
 __device__ __forceinline__ uint32_t lds_u16(const uint8_t* base, uint32_t off) {

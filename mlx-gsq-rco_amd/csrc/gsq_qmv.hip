@@ -102,6 +102,30 @@ __device__ __forceinline__ uint32_t enc_codes(uint32_t codes) {
 template <bool XS>
 __device__ __forceinline__ constexpr float enc_scale() { return XS ? 1.f : kSub; }
 
+// Both 16-bit halves shifted right by 8 (v_pk_lshrrev_b16): bytes 1 and 3 move to 0 and 2.
+typedef unsigned short ushort2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pk_shr8(uint32_t v) {
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(ushort2_t, v) >> (ushort2_t){8, 8});
+}
+
+// Views of an LDS table of 8- or 16-byte entries read as scalar words (the compiler merges
+// them into ds_read_b64/b128). Vector-typed LDS loads would make the compiler drain every
+// in-flight LDS DMA before each table read.
+struct LdsV2 {
+  const uint8_t* p;
+  __device__ __forceinline__ uint2 operator[](uint32_t i) const {
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p + 8 * i);
+    return make_uint2(q[0], q[1]);
+  }
+};
+struct LdsV4 {
+  const uint8_t* p;
+  __device__ __forceinline__ uint4 operator[](uint32_t i) const {
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p + 16 * i);
+    return make_uint4(q[0], q[1], q[2], q[3]);
+  }
+};
+
 // ---- per-type decode + dot -----------------------------------------------------------
 // Qmv<T>::kTbl is the size of the type's LDS table: an exact byte image prepared on the host
 // (build_qmv_table below) and copied into LDS with DMA at kernel start. Codebooks are fp16;
@@ -112,30 +136,31 @@ template <> struct Qmv<Q4_K> {
   static constexpr int kPair = PAIR_K;
   static constexpr int kSums = 1;
   static constexpr int kTbl = 0;
-  template <int MR, bool XS>
+  template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t*, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
     uint32_t h[4];
-    lds_words<4>(buf, off, h);
+    lds_words<4, A4>(buf, off, h);  // d, dmin, 12 scale bytes (k_decode.py:38-46)
     const float d = h2f(h[0] & 0xFFFFu), dmin = h2f(h[0] >> 16);
     const uint32_t j8 = 8u * (g & 3);
     const uint32_t A = bfe(h[1], j8, 8), B = bfe(h[2], j8, 8), C = bfe(h[3], j8, 8);
-    uint32_t sc, mn;
-    if (g < 4) { sc = A & 63u; mn = B & 63u; }
-    else { sc = (C & 15u) | ((A >> 6) << 4); mn = (C >> 4) | ((B >> 6) << 4); }
+    const bool lo = g < 4;
+    const uint32_t sc = lo ? (A & 63u) : ((C & 15u) | ((A >> 6) << 4));
+    const uint32_t mn = lo ? (B & 63u) : ((C >> 4) | ((B >> 6) << 4));
     uint32_t q[8];
-    lds_words<8>(buf, off + 16 + 32 * (g >> 1), q);
-    const uint32_t sh = 4u * (g & 1);
+    lds_words<8, A4>(buf, off + 16 + 32 * (g >> 1), q);
+    // odd groups use the high nibbles: mask them in place (value x 16, folded into the scale)
+    const bool odd = g & 1;
+    const uint32_t M = odd ? 0x00F000F0u : 0x000F000Fu;
     float acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = 0.f;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const uint32_t v = q[k] >> sh;
-      dacc<MR, XS>(enc_codes<XS>(v & 0x000F000Fu), x, 2 * k, acc);
-      dacc<MR, XS>(enc_codes<XS>((v >> 8) & 0x000F000Fu), x, 2 * k + 1, acc);
+      dacc<MR, XS>(enc_codes<XS>(q[k] & M), x, 2 * k, acc);
+      dacc<MR, XS>(enc_codes<XS>(pk_shr8(q[k]) & M), x, 2 * k + 1, acc);
     }
-    const float s = d * (float)sc * enc_scale<XS>();
+    const float s = d * (float)sc * (odd ? enc_scale<XS>() * 0.0625f : enc_scale<XS>());
     const float o = -(dmin * (float)mn);
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
@@ -149,14 +174,14 @@ template <> struct Qmv<Q2_K> {
   static constexpr int kPair = PAIR_K;
   static constexpr int kSums = 2;
   static constexpr int kTbl = 0;
-  template <int MR, bool XS>
+  template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t*, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
     const uint32_t sm = lds_u16(buf, off + 2 * g);
-    const uint32_t dd = lds_w32(buf, off + 80);
+    const uint32_t dd = lds_w32<A4>(buf, off + 80);
     const float d = h2f(dd & 0xFFFFu), dmin = h2f(dd >> 16);
     uint32_t q[8];
-    lds_words<8>(buf, off + 16 + 32 * (g >> 2), q);
+    lds_words<8, A4>(buf, off + 16 + 32 * (g >> 2), q);
     const uint32_t sh = 2u * (g & 3);
     float a0[MR], a1[MR];
 #pragma unroll
@@ -184,13 +209,13 @@ template <> struct Qmv<Q6_K> {
   static constexpr int kPair = PAIR_K;
   static constexpr int kSums = 2;
   static constexpr int kTbl = 0;
-  template <int MR, bool XS>
+  template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t*, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
     const int chunk = g >> 2, plane = g & 3;
     uint32_t ql[8], qh[8];
-    lds_words<8>(buf, off + 64 * chunk + 32 * (plane & 1), ql);
-    lds_words<8>(buf, off + 128 + 32 * chunk, qh);
+    lds_words<8, A4>(buf, off + 64 * chunk + 32 * (plane & 1), ql);
+    lds_words<8, A4>(buf, off + 128 + 32 * chunk, qh);
     const uint32_t sc2 = lds_u16(buf, off + 192 + 2 * g);
     const float d = h2f(lds_u16(buf, off + 208));
     const uint32_t ls = 4u * (plane >> 1), hs = 2u * plane;
@@ -217,16 +242,16 @@ template <> struct Qmv<IQ4_XS> {
   static constexpr int kPair = PAIR_16;
   static constexpr int kSums = 0;
   static constexpr int kTbl = 1024;  // 256 fp16 pairs (kvalues[lo nibble], kvalues[hi nibble])
-  template <int MR, bool XS>
+  template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
-    const uint32_t hd = lds_w32(buf, off);
+    const uint32_t hd = lds_w32<A4>(buf, off);
     const float d = h2f(hd & 0xFFFFu);
     const uint32_t low = (lds_u8(buf, off + 4 + (g >> 1)) >> (4 * (g & 1))) & 15u;
     const uint32_t high = ((hd >> 16) >> (2 * g)) & 3u;
     const int scale = (int)(low | (high << 4)) - 32;
     uint32_t q[4];
-    lds_words<4>(buf, off + 8 + 16 * g, q);
+    lds_words<4, A4>(buf, off + 8 + 16 * g, q);
     const uint32_t* t = reinterpret_cast<const uint32_t*>(tbl);
     float acc[MR];
 #pragma unroll
@@ -247,18 +272,18 @@ template <> struct Qmv<IQ3_S> {
   static constexpr int kSums = 0;
   static constexpr int kGridB = 512 * 4 * 2;
   static constexpr int kTbl = kGridB + 16 * 8;  // grid + 16 nibble sign masks
-  template <int MR, bool XS>
+  template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
     const float d = h2f(lds_u16(buf, off));
     const uint32_t snib = (lds_u8(buf, off + 106 + (g >> 1)) >> (4 * (g & 1))) & 15u;
     const float db = d * (float)(1u + 2u * snib);
     uint32_t q[2];
-    lds_words<2>(buf, off + 2 + 8 * g, q);
+    lds_words<2, A4>(buf, off + 2 + 8 * g, q);
     const uint32_t qh = lds_u8(buf, off + 66 + g);
-    const uint32_t sg = lds_w32(buf, off + 74 + 4 * g);
-    const uint2* grid = reinterpret_cast<const uint2*>(tbl);
-    const uint2* sm = reinterpret_cast<const uint2*>(tbl + kGridB);
+    const uint32_t sg = lds_w32<A4>(buf, off + 74 + 4 * g);
+    const LdsV2 grid{tbl};
+    const LdsV2 sm{tbl + kGridB};
     float acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = 0.f;
@@ -280,16 +305,16 @@ template <> struct Qmv<IQ3_XXS> {
   static constexpr int kSums = 0;
   static constexpr int kGridB = 256 * 4 * 2;
   static constexpr int kTbl = kGridB + 128 * 16;
-  template <int MR, bool XS>
+  template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
     const float dh = h2f(lds_u16(buf, off));
     uint32_t q[2];
-    lds_words<2>(buf, off + 2 + 8 * g, q);
-    const uint32_t u = lds_w32(buf, off + 66 + 4 * g);
+    lds_words<2, A4>(buf, off + 2 + 8 * g, q);
+    const uint32_t u = lds_w32<A4>(buf, off + 66 + 4 * g);
     const float d = dh * (0.5f + (float)(u >> 28)) * 0.5f;
-    const uint2* grid = reinterpret_cast<const uint2*>(tbl);
-    const uint4* km = reinterpret_cast<const uint4*>(tbl + kGridB);
+    const LdsV2 grid{tbl};
+    const LdsV4 km{tbl + kGridB};
     float acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = 0.f;
@@ -313,16 +338,16 @@ template <> struct Qmv<IQ2_XXS> {
   static constexpr int kSums = 0;
   static constexpr int kGridB = 256 * 8 * 2;
   static constexpr int kTbl = kGridB + 128 * 16;
-  template <int MR, bool XS>
+  template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
     const float dh = h2f(lds_u16(buf, off));
     uint32_t q[2];
-    lds_words<2>(buf, off + 2 + 8 * g, q);
+    lds_words<2, A4>(buf, off + 2 + 8 * g, q);
     const uint32_t u = q[1];
     const float d = dh * (0.5f + (float)(u >> 28)) * 0.25f;
-    const uint4* grid = reinterpret_cast<const uint4*>(tbl);
-    const uint4* km = reinterpret_cast<const uint4*>(tbl + kGridB);
+    const LdsV4 grid{tbl};
+    const LdsV4 km{tbl + kGridB};
     float acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = 0.f;
@@ -345,15 +370,15 @@ template <> struct Qmv<IQ2_XS> {
   static constexpr int kSums = 0;
   static constexpr int kGridB = 512 * 8 * 2;
   static constexpr int kTbl = kGridB + 128 * 16;
-  template <int MR, bool XS>
+  template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
     const float dh = h2f(lds_u16(buf, off));
     uint32_t q[2];
-    lds_words<2>(buf, off + 2 + 8 * g, q);
+    lds_words<2, A4>(buf, off + 2 + 8 * g, q);
     const uint32_t sb = lds_u8(buf, off + 66 + g);
-    const uint4* grid = reinterpret_cast<const uint4*>(tbl);
-    const uint4* km = reinterpret_cast<const uint4*>(tbl + kGridB);
+    const LdsV4 grid{tbl};
+    const LdsV4 km{tbl + kGridB};
     float a0[MR], a1[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) { a0[m] = 0.f; a1[m] = 0.f; }
@@ -381,16 +406,16 @@ template <> struct Qmv<IQ2_S> {
   static constexpr int kSums = 0;
   static constexpr int kGridB = 1024 * 8 * 2;
   static constexpr int kTbl = kGridB + 256 * 16;  // grid + 256 byte sign masks
-  template <int MR, bool XS>
+  template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
     const float dh = h2f(lds_u16(buf, off));
-    const uint32_t qs = lds_w32(buf, off + 2 + 4 * g);
-    const uint32_t sg = lds_w32(buf, off + 34 + 4 * g);
+    const uint32_t qs = lds_w32<A4>(buf, off + 2 + 4 * g);
+    const uint32_t sg = lds_w32<A4>(buf, off + 34 + 4 * g);
     const uint32_t qh = lds_u8(buf, off + 66 + g);
     const uint32_t sb = lds_u8(buf, off + 74 + g);
-    const uint4* grid = reinterpret_cast<const uint4*>(tbl);
-    const uint4* bm = reinterpret_cast<const uint4*>(tbl + kGridB);
+    const LdsV4 grid{tbl};
+    const LdsV4 bm{tbl + kGridB};
     float a0[MR], a1[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) { a0[m] = 0.f; a1[m] = 0.f; }
@@ -417,15 +442,15 @@ template <> struct Qmv<IQ1_S> {
   static constexpr int kPair = PAIR_NAT;
   static constexpr int kSums = 1;
   static constexpr int kTbl = 2048 * 8 * 2;
-  template <int MR, bool XS>
+  template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
     const float dh = h2f(lds_u16(buf, off));
-    const uint32_t qs = lds_w32(buf, off + 2 + 4 * g);
+    const uint32_t qs = lds_w32<A4>(buf, off + 2 + 4 * g);
     const uint32_t h = lds_u16(buf, off + 34 + 2 * g);
     const float d = dh * (float)(2u * ((h >> 12) & 7u) + 1u);
     const float delta = (h & 0x8000u) ? -0.125f : 0.125f;
-    const uint4* grid = reinterpret_cast<const uint4*>(tbl);
+    const LdsV4 grid{tbl};
     float acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = 0.f;
@@ -447,13 +472,13 @@ template <> struct Qmv<IQ1_M> {
   static constexpr int kPair = PAIR_NAT;
   static constexpr int kSums = 4;
   static constexpr int kTbl = 2048 * 8 * 2;
-  template <int MR, bool XS>
+  template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
-    const uint32_t qs = lds_w32(buf, off + 4 * g);
+    const uint32_t qs = lds_w32<A4>(buf, off + 4 * g);
     const uint32_t qh = lds_u16(buf, off + 32 + 2 * g);
     uint32_t w[2];
-    lds_words<2>(buf, off + 48, w);
+    lds_words<2, A4>(buf, off + 48, w);
     const uint32_t w0 = w[0] & 0xFFFFu, w1 = w[0] >> 16, w2 = w[1] & 0xFFFFu, w3 = w[1] >> 16;
     const uint32_t dbits = ((w0 & 61440u) >> 12) | ((w1 & 61440u) >> 8) | ((w2 & 61440u) >> 4) | (w3 & 61440u);
     const float d = h2f(dbits);
@@ -461,7 +486,7 @@ template <> struct Qmv<IQ1_M> {
     const uint32_t sh0 = 3u * ((2 * g) & 3);
     const float d0 = d * (float)(2u * ((ww >> sh0) & 7u) + 1u);
     const float d1 = d * (float)(2u * ((ww >> (sh0 + 3)) & 7u) + 1u);
-    const uint4* grid = reinterpret_cast<const uint4*>(tbl);
+    const LdsV4 grid{tbl};
     float a[4][MR];
 #pragma unroll
     for (int l = 0; l < 4; ++l)
@@ -650,7 +675,7 @@ __device__ __forceinline__ void qmv_load_x1(XReg<MR, XS, Qmv<T>::kSums>& xr, boo
   }
 }
 
-template <int T, int MR, bool XS, int GL>
+template <int T, int MR, bool XS, int GL, bool A4>
 __global__ void __launch_bounds__(QmvBounds<qmv_weight(MR, GL, XS)>::v) qmv_kernel(QmvArgs a) {
   using P = Qmv<T>;
   constexpr int BB = BlockBytes<T>::v;
@@ -663,30 +688,27 @@ __global__ void __launch_bounds__(QmvBounds<qmv_weight(MR, GL, XS)>::v) qmv_kern
 
   const int64_t r0 = (int64_t)blockIdx.x * a.rows_per_wg;
   const int64_t r1 = min(a.N, r0 + (int64_t)a.rows_per_wg);
-  // row slot of this wave and its K range (slices sl0 .. sl0 + nq - 1)
+  // row slot of this wave and its K range (slices sl0 .. sl0 + nq - 1). Slot s takes rows
+  // r0 + s, r0 + s + slots, ...: at any time the waves of a workgroup read neighbouring rows,
+  // one contiguous span of the packed matrix.
   const int slot = wave / a.W, ws = wave - slot * a.W;
-  const bool live = slot < a.slots && r0 < r1;
-  int64_t sr0 = r1, sr1 = r1;
-  if (live) {
-    const int64_t nrows = r1 - r0;
-    const int64_t per = (nrows + a.slots - 1) / a.slots;
-    sr0 = min(r1, r0 + (int64_t)slot * per);
-    sr1 = min(r1, sr0 + per);
-  }
+  const bool live = slot < a.slots && r0 + slot < r1;
   const int sl0 = ws * GL;
   const int nq = live ? max(0, min(GL, a.nslices - sl0)) : 0;
   const int nbk = min(8 * GL, a.nblk - sl0 * 8);             // superblocks per item
   const int item_bytes = nbk * BB;
-  const int nitems = nq > 0 ? (int)(sr1 - sr0) : 0;
-  // item t = K range of row sr0 + t
-  const uintptr_t base = reinterpret_cast<uintptr_t>(a.packed) + (uintptr_t)(sr0 * a.row_bytes + (int64_t)sl0 * 8 * BB);
+  const int nitems = nq > 0 ? (int)((r1 - r0 - slot + a.slots - 1) / a.slots) : 0;
+  // item t = K range of row r0 + slot + t * slots
+  const int64_t row0 = r0 + slot;
+  const uintptr_t base = reinterpret_cast<uintptr_t>(a.packed) + (uintptr_t)(row0 * a.row_bytes + (int64_t)sl0 * 8 * BB);
+  const uintptr_t stride = (uintptr_t)a.row_bytes * (uintptr_t)a.slots;
 
   // ---- prologue: table + activations (once per workgroup), then this wave's first items ----
   if constexpr (P::kTbl > 0) dma_copy(a.tb.qmv_tbl, P::kTbl, tbl, wave, nw, lane);
   if (a.x_lds) dma_copy(a.x, a.x_bytes, xst, wave, nw, lane);
   const int pre = min(a.nb - 1, nitems);
   for (int i = 0; i < pre; ++i)
-    dma_item(base + (uintptr_t)i * a.row_bytes, item_bytes, a.cdma, ring + i * a.sbuf, lane);
+    dma_item(base + (uintptr_t)i * stride, item_bytes, a.cdma, ring + i * a.sbuf, lane);
   wait_vmcnt(pre * a.cdma);  // this wave's share of the table and activations has landed
   __syncthreads();           // ... and every other wave's share
 
@@ -706,10 +728,10 @@ __global__ void __launch_bounds__(QmvBounds<qmv_weight(MR, GL, XS)>::v) qmv_kern
     if (t + a.nb - 1 < nitems) {
       int nbuf = buf + a.nb - 1;
       if (nbuf >= a.nb) nbuf -= a.nb;
-      dma_item(base + (uintptr_t)(t + a.nb - 1) * a.row_bytes, item_bytes, a.cdma, ring + nbuf * a.sbuf, lane);
+      dma_item(base + (uintptr_t)(t + a.nb - 1) * stride, item_bytes, a.cdma, ring + nbuf * a.sbuf, lane);
     }
-    const int64_t row = sr0 + t;
-    const uint32_t delta = (uint32_t)((base + (uintptr_t)t * a.row_bytes) & 15u);
+    const int64_t row = row0 + (int64_t)t * a.slots;
+    const uint32_t delta = (uint32_t)((base + (uintptr_t)t * stride) & 15u);
     const uint8_t* b = ring + buf * a.sbuf;
     float acc[MR];
 #pragma unroll
@@ -723,7 +745,7 @@ __global__ void __launch_bounds__(QmvBounds<qmv_weight(MR, GL, XS)>::v) qmv_kern
         float part[MR];
 #pragma unroll
         for (int m = 0; m < MR; ++m) part[m] = 0.f;
-        P::template dot<MR, XS>(b, delta + (uint32_t)((ok ? blk : 0) * BB), lane & 7, tbl, xr[q], part);
+        P::template dot<MR, XS, A4>(b, delta + (uint32_t)((ok ? blk : 0) * BB), lane & 7, tbl, xr[q], part);
 #pragma unroll
         for (int m = 0; m < MR; ++m) acc[m] += ok ? part[m] : 0.f;
       }
@@ -754,9 +776,9 @@ __global__ void __launch_bounds__(QmvBounds<qmv_weight(MR, GL, XS)>::v) qmv_kern
   }
 }
 
-template <int T, int MR, bool XS, int GL>
+template <int T, int MR, bool XS, int GL, bool A4>
 static hipError_t launch_qmv_t(const QmvArgs& a, int grid, int threads, size_t lds, hipStream_t s) {
-  auto k = qmv_kernel<T, MR, XS, GL>;
+  auto k = qmv_kernel<T, MR, XS, GL, A4>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
@@ -778,13 +800,25 @@ static int qmv_gl(int mr, bool xs) {
   return 1;
 }
 
+template <int T, bool A4>
+static hipError_t launch_qmv_variant(const QmvArgs& a, int mr, bool xs, int grid, int threads, size_t lds,
+                                     hipStream_t s) {
+  if (mr == 1) return xs ? launch_qmv_t<T, 1, true, 1, A4>(a, grid, threads, lds, s) : launch_qmv_t<T, 1, false, 3, A4>(a, grid, threads, lds, s);
+  if (mr == 2) return xs ? launch_qmv_t<T, 2, true, 1, A4>(a, grid, threads, lds, s) : launch_qmv_t<T, 2, false, 1, A4>(a, grid, threads, lds, s);
+  if (mr == 4 && !xs) return launch_qmv_t<T, 4, false, 1, A4>(a, grid, threads, lds, s);
+  return hipErrorInvalidValue;
+}
+
+// Types whose superblock size is a multiple of 4 read their fields with plain dword loads when
+// the packed matrix is 4-byte aligned (every superblock then is); the rest funnel-shift.
 template <int T>
 static hipError_t launch_qmv_type(const QmvArgs& a, int mr, bool xs, int grid, int threads, size_t lds,
                                   hipStream_t s) {
-  if (mr == 1) return xs ? launch_qmv_t<T, 1, true, 1>(a, grid, threads, lds, s) : launch_qmv_t<T, 1, false, 3>(a, grid, threads, lds, s);
-  if (mr == 2) return xs ? launch_qmv_t<T, 2, true, 1>(a, grid, threads, lds, s) : launch_qmv_t<T, 2, false, 1>(a, grid, threads, lds, s);
-  if (mr == 4 && !xs) return launch_qmv_t<T, 4, false, 1>(a, grid, threads, lds, s);
-  return hipErrorInvalidValue;
+  if constexpr (BlockBytes<T>::v % 4 == 0) {
+    if ((reinterpret_cast<uintptr_t>(a.packed) & 3) == 0)
+      return launch_qmv_variant<T, true>(a, mr, xs, grid, threads, lds, s);
+  }
+  return launch_qmv_variant<T, false>(a, mr, xs, grid, threads, lds, s);
 }
 
 int qmv_table_bytes(int qt) {

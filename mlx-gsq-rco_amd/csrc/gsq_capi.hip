@@ -18,7 +18,7 @@ hipError_t launch_dequant(int qt, const uint8_t* packed, int64_t nblocks, float*
 hipError_t launch_qmv(int qt, const uint8_t* packed, const void* x, int xdt, void* y, int ydt, int64_t M, int64_t N,
                       int K, const DevTables& tb, int num_cus, hipStream_t s);
 hipError_t launch_qmm(int qt, const uint8_t* packed, const void* x, int xdt, void* y, int ydt, int64_t M, int64_t N,
-                      int K, const DevTables& tb, hipStream_t s);
+                      int K, const DevTables& tb, int num_cus, const QmmWorkspace& ws, hipStream_t s);
 int qmv_table_bytes(int qt);
 bool build_qmv_table(int qt, const uint16_t* grid16, const uint8_t* ksigns, std::vector<uint8_t>& out);
 }  // namespace gsq
@@ -62,6 +62,7 @@ struct DevState {
   std::map<int, uint8_t*> qmv_tbls;   // per type with a QMV LDS table
   uint8_t* ksigns = nullptr;
   int num_cus = 0;
+  QmmWorkspace qmm_ws = {nullptr, nullptr, 0};
 };
 
 // Upload (or refresh) the QMV LDS table image of `qt` on the current device; caller holds g_mu.
@@ -115,6 +116,38 @@ int resolve(int qt, DevTables* tb, int* num_cus) {
   }
   auto tt = st.qmv_tbls.find(qt);
   if (tt != st.qmv_tbls.end()) tb->qmv_tbl = tt->second;
+  return GSQ_OK;
+}
+
+// The QMM workspace of the current device, allocated on the first QMM call there (a fixed
+// size: 2 partial slots of 256 x 256 floats and one counter per CU); counters start at zero.
+int qmm_workspace(QmmWorkspace* ws) {
+  int dev;
+  if (int rc = current_device(&dev)) return rc;
+  std::lock_guard<std::mutex> lk(g_mu);
+  DevState& st = g_dev[dev];
+  if (!st.qmm_ws.part) {
+    if (st.num_cus == 0) {
+      hipError_t e = hipDeviceGetAttribute(&st.num_cus, hipDeviceAttributeMultiprocessorCount, dev);
+      if (e != hipSuccess) return fail(GSQ_E_HIP, "hipDeviceGetAttribute: %s", hipGetErrorString(e));
+    }
+    const int groups = st.num_cus;
+    const size_t part_bytes = (size_t)2 * groups * 256 * 256 * sizeof(float);
+    float* part = nullptr;
+    int* cnt = nullptr;
+    hipError_t e = hipMalloc(&part, part_bytes);
+    if (e != hipSuccess) return fail(GSQ_E_HIP, "hipMalloc(QMM workspace): %s", hipGetErrorString(e));
+    e = hipMalloc(&cnt, (size_t)groups * sizeof(int));
+    if (e == hipSuccess) e = hipMemset(cnt, 0, (size_t)groups * sizeof(int));
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+      hipFree(part);
+      if (cnt) hipFree(cnt);
+      return fail(GSQ_E_HIP, "QMM workspace setup: %s", hipGetErrorString(e));
+    }
+    st.qmm_ws = {part, cnt, groups};
+  }
+  *ws = st.qmm_ws;
   return GSQ_OK;
 }
 
@@ -244,7 +277,9 @@ int gsq_qmm(int qt, const void* packed, const void* x, int xdt, void* y, int ydt
   DevTables tb;
   int cus;
   if (int rc = resolve(qt, &tb, &cus)) return rc;
-  hipError_t e = launch_qmm(qt, static_cast<const uint8_t*>(packed), x, xdt, y, ydt, M, N, (int)K, tb,
+  QmmWorkspace ws;
+  if (int rc = qmm_workspace(&ws)) return rc;
+  hipError_t e = launch_qmm(qt, static_cast<const uint8_t*>(packed), x, xdt, y, ydt, M, N, (int)K, tb, cus, ws,
                             static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(GSQ_E_HIP, "qmm launch: %s", hipGetErrorString(e));
   return GSQ_OK;

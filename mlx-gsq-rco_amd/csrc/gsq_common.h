@@ -66,6 +66,22 @@ struct QmvTuning {
   int wg_per_cu;
 };
 
+// Launch-plan overrides of the QMM kernel: activation tile height in 16-row blocks (0 = by
+// M) and the largest activation ring depth.
+struct QmmTuning {
+  int mf;
+  int lx_max;
+};
+
+// Per-device QMM workspace, allocated once: fp32 partial tiles of workgroups that share an
+// output tile (2 slots of 256 x 256 floats per workgroup) and one arrival counter per
+// workgroup, kept at zero between launches.
+struct QmmWorkspace {
+  float* part;
+  int* cnt;
+  int max_groups;
+};
+
 // Non-linear IQ4_XS values (k_decode.py:77).
 __device__ __constant__ static const int8_t kIQ4Values[16] = {
     -127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
@@ -127,6 +143,38 @@ __device__ __forceinline__ uint32_t lds_u8(const uint8_t* base, uint32_t off) { 
 
 __device__ __forceinline__ uint32_t bfe(uint32_t v, uint32_t off, uint32_t width) {
   return __builtin_amdgcn_ubfe(v, off, width);
+}
+
+// ---- LDS DMA -------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Cooperative DMA of a 16-byte aligned buffer of `bytes` (a multiple of 16) by all waves of
+// the workgroup; returns the instructions this wave issued.
+__device__ __forceinline__ int dma_copy(const void* src, int bytes, uint8_t* dst, int wave, int nw, int lane) {
+  const int ngran = bytes >> 4, per_wave = 64;
+  int issued = 0;
+  for (int c0 = wave * per_wave; c0 < ngran; c0 += nw * per_wave) {
+    const int c = c0 + lane;
+    if (c < ngran)
+      __builtin_amdgcn_global_load_lds(static_cast<const uint8_t*>(src) + (size_t)c * 16,
+                                       (lds_ptr_t)(dst + c0 * 16), 16, 0, 0);
+    ++issued;
+  }
+  return issued;
+}
+
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding: vmcnt bits 3:0 and
+// 15:14); n above 63 waits for vmcnt(63), and a smaller immediate only waits longer.
+__device__ __forceinline__ void wait_vmcnt(int n) {
+#define GSQ_VMW(k) case k: __builtin_amdgcn_s_waitcnt(0x0F70 | ((k) & 15) | (((k) >> 4) << 14)); break;
+#define GSQ_VMW8(k) GSQ_VMW(k) GSQ_VMW(k + 1) GSQ_VMW(k + 2) GSQ_VMW(k + 3) GSQ_VMW(k + 4) GSQ_VMW(k + 5) \
+  GSQ_VMW(k + 6) GSQ_VMW(k + 7)
+  switch (n < 0 ? 0 : n) {
+    GSQ_VMW8(0) GSQ_VMW8(8) GSQ_VMW8(16) GSQ_VMW8(24) GSQ_VMW8(32) GSQ_VMW8(40) GSQ_VMW8(48) GSQ_VMW8(56)
+    default: __builtin_amdgcn_s_waitcnt(0x0F70 | 15 | (3 << 14)); break;
+  }
+#undef GSQ_VMW8
+#undef GSQ_VMW
 }
 
 }  // namespace gsq

@@ -1,0 +1,269 @@
+// fp16 decode of one MFMA B-operand fragment slice: eight consecutive weights (octet
+// kq = 0..3 of group g = 0..7) of one superblock held in LDS, as four fp16 pairs.
+//
+// Each weight is the reference decoder's value (mlx_gsq/runtime/kernels/k_decode.py:18-80,
+// iq_lookup_decode.py:6-39, iq3_s_decode.py:16-40) rounded to fp16 (the reference QMM's
+// decoded tile is half, qmm.py:181). One v_fma_mix per weight forms scale * code + offset
+// exactly and rounds it once to fp16 (round to nearest even):
+//  * K-quant and IQ4_XS codes enter as fp16 subnormals (bits = the code, value code * 2^-24)
+//    against a scale multiplied by 2^24, so the product is the exact integer multiple;
+//  * codebook types read the fp16 codebook entries directly and flip signs with XOR masks
+//    of fp16 pairs, from the same LDS table image as the QMV kernel.
+// For Q6_K, IQ4_XS and every product of the real codebooks the float32 value is exact, so
+// this is the reference's fp16 tile bit for bit; where the reference's float32 expression
+// rounds (Q2_K / Q4_K's d*sc*q - dmin*m, products with arbitrary codebook values) the
+// single rounding can differ from its float32-then-fp16 double rounding by one fp16 ulp when
+// the float32 value falls on an fp16 tie.
+//
+// `sb` points at the superblock in LDS (2-byte aligned; A4: 4-byte aligned), `tbl` at the
+// type's table image: fp16 codebook (entries x coords) followed by its sign masks.
+#pragma once
+#include "gsq_common.h"
+
+namespace gsq {
+
+// fp16 pair {fma(a, h.lo, c), fma(a, h.hi, c)} with h an fp16 pair and a, c float: each result
+// is computed exactly and rounded once (v_fma_mixlo_f16 / v_fma_mixhi_f16)
+// (the host pass never runs this device-only function; the VGPR asm constraints exist only in
+// the device compilation)
+__device__ __forceinline__ uint32_t mix2(float a, uint32_t h, float c) {
+  uint32_t r = 0;
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(h), "v"(c));
+  asm("v_fma_mixhi_f16 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "+v"(r) : "v"(a), "v"(h), "v"(c));
+#endif
+  return r;
+}
+
+// bytes 0,1 (lo) or 2,3 (hi) of q as the two halves of a word (fp16 subnormal codes)
+__device__ __forceinline__ uint32_t spread_lo(uint32_t q) { return __builtin_amdgcn_perm(0u, q, 0x0c010c00u); }
+__device__ __forceinline__ uint32_t spread_hi(uint32_t q) { return __builtin_amdgcn_perm(0u, q, 0x0c030c02u); }
+
+constexpr float kCode = 16777216.f;  // 2^24: an fp16 subnormal with bits q has value q * 2^-24
+
+// eight byte codes (two words) -> fp16 of a * code + c (a24 = a * 2^24)
+__device__ __forceinline__ void codes8(const uint32_t (&q)[2], float a24, float c, uint32_t (&o)[4]) {
+  o[0] = mix2(a24, spread_lo(q[0]), c);
+  o[1] = mix2(a24, spread_hi(q[0]), c);
+  o[2] = mix2(a24, spread_lo(q[1]), c);
+  o[3] = mix2(a24, spread_hi(q[1]), c);
+}
+
+__device__ __forceinline__ const uint32_t* tbl_words(const uint8_t* tbl, uint32_t byte_off) {
+  return reinterpret_cast<const uint32_t*>(tbl + byte_off);
+}
+
+template <int T, bool A4>
+struct QmmDec;
+
+// Q2_K (k_decode.py:18-30): w = d*(sm&15)*q - dmin*(sm>>4)
+template <bool A4>
+struct QmmDec<Q2_K, A4> {
+  __device__ static void run(const uint8_t* sb, const uint8_t*, int g, int kq, uint32_t (&o)[4]) {
+    uint32_t q[2];
+    lds_words<2, A4>(sb, 16 + (g >> 2) * 32 + 8 * kq, q);
+    const int sh = 2 * (g & 3);
+    q[0] = (q[0] >> sh) & 0x03030303u;
+    q[1] = (q[1] >> sh) & 0x03030303u;
+    const uint32_t dd = lds_w32<A4>(sb, 80);
+    const uint32_t sm = lds_u8(sb, 2 * g + (kq >> 1));
+    const float a = h2f(dd & 0xFFFFu) * (float)(sm & 15u);
+    const float b = h2f(dd >> 16) * (float)(sm >> 4);
+    codes8(q, a * kCode, -b, o);
+  }
+};
+
+// Q4_K (k_decode.py:31-50): w = d*sc*q - dmin*mn with 6-bit scales/mins
+template <bool A4>
+struct QmmDec<Q4_K, A4> {
+  __device__ static void run(const uint8_t* sb, const uint8_t*, int g, int kq, uint32_t (&o)[4]) {
+    uint32_t q[2];
+    lds_words<2, A4>(sb, 16 + (g >> 1) * 32 + 8 * kq, q);
+    const int sh = 4 * (g & 1);
+    q[0] = (q[0] >> sh) & 0x0F0F0F0Fu;
+    q[1] = (q[1] >> sh) & 0x0F0F0F0Fu;
+    uint32_t s[3];
+    lds_words<3, A4>(sb, 4, s);
+    const uint32_t dd = lds_w32<A4>(sb, 0);
+    uint32_t sc, mn;
+    const int gg = g & 3;
+    if (g < 4) {
+      sc = bfe(s[0], 8 * gg, 6);
+      mn = bfe(s[1], 8 * gg, 6);
+    } else {
+      const uint32_t lo = bfe(s[2], 8 * gg, 8);
+      sc = (lo & 15u) | (bfe(s[0], 8 * gg + 6, 2) << 4);
+      mn = (lo >> 4) | (bfe(s[1], 8 * gg + 6, 2) << 4);
+    }
+    const float a = h2f(dd & 0xFFFFu) * (float)sc;
+    const float b = h2f(dd >> 16) * (float)mn;
+    codes8(q, a * kCode, -b, o);
+  }
+};
+
+// Q6_K (k_decode.py:51-65): w = d*scale*(q - 32), q = low nibble | 2 high bits << 4
+template <bool A4>
+struct QmmDec<Q6_K, A4> {
+  __device__ static void run(const uint8_t* sb, const uint8_t*, int g, int kq, uint32_t (&o)[4]) {
+    const int h = g >> 2, pl = g & 3;
+    uint32_t ql[2], qh[2];
+    lds_words<2, A4>(sb, h * 64 + (pl & 1) * 32 + 8 * kq, ql);
+    lds_words<2, A4>(sb, 128 + h * 32 + 8 * kq, qh);
+    const int shl = 4 * (pl >> 1), shh = 2 * pl;
+    uint32_t q[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) q[i] = ((ql[i] >> shl) & 0x0F0F0F0Fu) | (((qh[i] >> shh) & 0x03030303u) << 4);
+    const int sc = (int)(int8_t)lds_u8(sb, 192 + 2 * g + (kq >> 1));
+    const float a = h2f(lds_u16(sb, 208)) * (float)sc;
+    codes8(q, a * kCode, -32.f * a, o);
+  }
+};
+
+// IQ4_XS (k_decode.py:66-80): w = d*scale*kvalues[q]; kvalues + 128 looked up as bytes
+template <bool A4>
+struct QmmDec<IQ4_XS, A4> {
+  __device__ static void run(const uint8_t* sb, const uint8_t*, int g, int kq, uint32_t (&o)[4]) {
+    uint32_t q[2];
+    lds_words<2, A4>(sb, 8 + 16 * g + 8 * (kq & 1), q);
+    const int sh = 4 * (kq >> 1);
+    const uint32_t dw = lds_w32<A4>(sb, 0);
+    const uint32_t low = (lds_u8(sb, 4 + g / 2) >> (4 * (g & 1))) & 15u;
+    const uint32_t high = ((dw >> 16) >> (2 * g)) & 3u;
+    const float a = h2f(dw & 0xFFFFu) * (float)((int)(low | (high << 4)) - 32);
+    // kvalues + 128 = {1,24,45,63,79,93,106,118,129,141,153,166,181,197,217,241}
+    constexpr uint32_t T0 = 0x3F2D1801u, T1 = 0x766A5D4Fu, T2 = 0xA6998D81u, T3 = 0xF1D9C5B5u;
+    uint32_t u[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t c = (q[i] >> sh) & 0x0F0F0F0Fu;
+      const uint32_t sel = c & 0x07070707u;
+      const uint32_t lo = __builtin_amdgcn_perm(T1, T0, sel);
+      const uint32_t hi = __builtin_amdgcn_perm(T3, T2, sel);
+      const uint32_t m = ((c >> 3) & 0x01010101u) * 0xFFu;
+      u[i] = (hi & m) | (lo & ~m);
+    }
+    codes8(u, a * kCode, -128.f * a, o);
+  }
+};
+
+// IQ3_S (iq3_s_decode.py:16-40): w = +-d*(1+2*s)*grid[gi][c], 9-bit grid index; sign masks
+// per nibble (two pairs) after the codebook
+template <bool A4>
+struct QmmDec<IQ3_S, A4> {
+  static constexpr uint32_t kGridB = 512 * 4 * 2;
+  __device__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+    const float d = h2f(lds_u16(sb, 0));
+    const uint32_t sbyte = lds_u8(sb, 106 + (g >> 1));
+    const float db = d * (float)(1u + 2u * ((sbyte >> (4 * (g & 1))) & 15u));
+    const uint32_t qh = lds_u8(sb, 66 + g);
+    const uint32_t qq = lds_u16(sb, 2 + 8 * g + 2 * kq);
+    const uint32_t i0 = (qq & 0xFFu) | ((qh << (8 - 2 * kq)) & 256u);
+    const uint32_t i1 = (qq >> 8) | ((qh << (7 - 2 * kq)) & 256u);
+    const uint32_t signs = lds_u8(sb, 74 + 4 * g + kq);
+    const uint32_t* e0 = tbl_words(tbl, i0 * 8);
+    const uint32_t* e1 = tbl_words(tbl, i1 * 8);
+    const uint32_t* m0 = tbl_words(tbl, kGridB + (signs & 15u) * 8);
+    const uint32_t* m1 = tbl_words(tbl, kGridB + (signs >> 4) * 8);
+    o[0] = mix2(db, e0[0], 0.f) ^ m0[0];
+    o[1] = mix2(db, e0[1], 0.f) ^ m0[1];
+    o[2] = mix2(db, e1[0], 0.f) ^ m1[0];
+    o[3] = mix2(db, e1[1], 0.f) ^ m1[1];
+  }
+};
+
+// one 8-wide codebook entry times d, with four sign-mask pairs
+__device__ __forceinline__ void grid8(const uint8_t* tbl, uint32_t qi, float d, float c, const uint32_t* m,
+                                      uint32_t (&o)[4]) {
+  const uint32_t* e = tbl_words(tbl, qi * 16);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = mix2(d, e[i], c) ^ (m ? m[i] : 0u);
+}
+
+// IQ3_XXS (iq_lookup_decode.py:7-12): w = +-d*(0.5+s)*0.5*grid[qi][c], ksigns masks
+template <bool A4>
+struct QmmDec<IQ3_XXS, A4> {
+  static constexpr uint32_t kGridB = 256 * 4 * 2;
+  __device__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+    const uint32_t u = lds_w32<A4>(sb, 66 + 4 * g);
+    const float d = h2f(lds_u16(sb, 0)) * (0.5f + (float)(u >> 28)) * 0.5f;
+    const uint32_t* m = tbl_words(tbl, kGridB + ((u >> (7 * kq)) & 127u) * 16);
+    const uint32_t qq = lds_u16(sb, 2 + 8 * g + 2 * kq);
+    const uint32_t* e0 = tbl_words(tbl, (qq & 0xFFu) * 8);
+    const uint32_t* e1 = tbl_words(tbl, (qq >> 8) * 8);
+    o[0] = mix2(d, e0[0], 0.f) ^ m[0];
+    o[1] = mix2(d, e0[1], 0.f) ^ m[1];
+    o[2] = mix2(d, e1[0], 0.f) ^ m[2];
+    o[3] = mix2(d, e1[1], 0.f) ^ m[3];
+  }
+};
+
+// IQ2_XXS (iq_lookup_decode.py:23-26)
+template <bool A4>
+struct QmmDec<IQ2_XXS, A4> {
+  static constexpr uint32_t kGridB = 256 * 8 * 2;
+  __device__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+    const uint32_t u = lds_w32<A4>(sb, 2 + 8 * g + 4);
+    const float d = h2f(lds_u16(sb, 0)) * (0.5f + (float)(u >> 28)) * 0.25f;
+    grid8(tbl, lds_u8(sb, 2 + 8 * g + kq), d, 0.f, tbl_words(tbl, kGridB + ((u >> (7 * kq)) & 127u) * 16), o);
+  }
+};
+
+// IQ2_XS (iq_lookup_decode.py:13-17)
+template <bool A4>
+struct QmmDec<IQ2_XS, A4> {
+  static constexpr uint32_t kGridB = 512 * 8 * 2;
+  __device__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+    const uint32_t q = lds_u16(sb, 2 + 2 * (4 * g + kq));
+    const uint32_t sc = (lds_u8(sb, 66 + g) >> (4 * (kq >> 1))) & 15u;
+    const float d = h2f(lds_u16(sb, 0)) * (0.5f + (float)sc) * 0.25f;
+    grid8(tbl, q & 511u, d, 0.f, tbl_words(tbl, kGridB + (q >> 9) * 16), o);
+  }
+};
+
+// IQ2_S (iq_lookup_decode.py:18-22): sign byte masks after the codebook
+template <bool A4>
+struct QmmDec<IQ2_S, A4> {
+  static constexpr uint32_t kGridB = 1024 * 8 * 2;
+  __device__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+    const int oo = 4 * g + kq;
+    const uint32_t hi = (lds_u8(sb, 66 + g) >> (2 * kq)) & 3u;
+    const uint32_t qi = lds_u8(sb, 2 + oo) | (hi << 8);
+    const uint32_t sc = (lds_u8(sb, 74 + g) >> (4 * (kq >> 1))) & 15u;
+    const float d = h2f(lds_u16(sb, 0)) * (0.5f + (float)sc) * 0.25f;
+    grid8(tbl, qi, d, 0.f, tbl_words(tbl, kGridB + lds_u8(sb, 34 + oo) * 16), o);
+  }
+};
+
+// IQ1_S (iq_lookup_decode.py:27-30): w = d*(2*s+1)*(grid[qi][c] + delta) = fma(d, grid, d*delta)
+template <bool A4>
+struct QmmDec<IQ1_S, A4> {
+  __device__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+    const uint32_t h = lds_u16(sb, 34 + 2 * g);
+    const float d = h2f(lds_u16(sb, 0)) * (float)(2u * ((h >> 12) & 7u) + 1u);
+    const float dd = (h & 32768u) ? -0.125f * d : 0.125f * d;
+    const uint32_t qi = lds_u8(sb, 2 + 4 * g + kq) | (((h >> (3 * kq)) & 7u) << 8);
+    grid8(tbl, qi, d, dd, nullptr, o);
+  }
+};
+
+// IQ1_M (iq_lookup_decode.py:31-37): w = d*(2*sc+1)*(grid[qi][c] + delta), d from the four
+// scale words' top nibbles
+template <bool A4>
+struct QmmDec<IQ1_M, A4> {
+  __device__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+    uint32_t w[2];
+    lds_words<2, A4>(sb, 48, w);
+    const uint32_t w0 = w[0] & 0xFFFFu, w1 = w[0] >> 16, w2 = w[1] & 0xFFFFu, w3 = w[1] >> 16;
+    const uint32_t dbits = ((w0 & 61440u) >> 12) | ((w1 & 61440u) >> 8) | ((w2 & 61440u) >> 4) | (w3 & 61440u);
+    const int oo = 4 * g + kq;
+    const uint32_t hn = (lds_u8(sb, 32 + oo / 2) >> (4 * (oo & 1))) & 15u;
+    const uint32_t qi = lds_u8(sb, oo) | ((hn & 7u) << 8);
+    const int sci = 2 * g + (kq >> 1);
+    const uint32_t ww = (sci >> 2) == 0 ? w0 : ((sci >> 2) == 1 ? w1 : ((sci >> 2) == 2 ? w2 : w3));
+    const uint32_t sc = (ww >> (3 * (sci & 3))) & 7u;
+    const float d = h2f(dbits) * (float)(2u * sc + 1u);
+    grid8(tbl, qi, d, (hn & 8u) ? -0.125f * d : 0.125f * d, nullptr, o);
+  }
+};
+
+}  // namespace gsq

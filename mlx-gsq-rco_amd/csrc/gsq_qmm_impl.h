@@ -1,0 +1,561 @@
+// Tiled quantized matrix-matrix product (QMM) for prefill: y[M,N] = x[M,K] * W[N,K]^T.
+//
+// Counterpart of the reference's tiled decode-once kernel
+// (mlx_gsq/runtime/kernels/qmm.py:252-325, dispatched by quantized_matmul qmm.py:559-594):
+// every weight is decoded once per activation tile into fp16 (the reference's decoded tile is
+// half, qmm.py:181), activations are staged as fp16 (qmm.py:150-165) and products accumulate
+// in fp32.
+//
+// gfx950 kernel (fp16 activations), one 256-thread workgroup per CU:
+//  * output tile = BM activation rows x 256 weight rows; wave w owns weight rows
+//    [64w, 64w + 64) and all BM rows, so its weights are private to it: the wave decodes them
+//    straight into v_mfma_f32_16x16x32_f16 B operands (lane l: row l%16 of a 16-row block,
+//    weights 8(l/16)..+7 of the 32-weight group) and they never pass through LDS as fp16.
+//  * the wave's 64 superblocks of the current 256-wide K column sit in a private
+//    two-column LDS ring, filled by global_load_lds DMA one column ahead; each row has a
+//    16-byte aligned slot holding the granules that cover its (2-byte aligned) superblock.
+//  * activations: a ring of `lx` K32 stages of BM x 32 fp16 shared by the four waves, filled
+//    by DMA lx-1 stages ahead into a layout whose 16-byte octets are XOR-swizzled per row
+//    (octet o of row m at position o ^ ((m >> 2) & 3)) so that the ds_read_b128 A-operand
+//    reads of a wave are free of bank conflicts.
+//  * all DMA waits are exact s_waitcnt vmcnt counts derived from the fixed issue order; one
+//    s_barrier per K32 stage guards the shared activation ring.
+//  * stream-K work split: the (tile, K column) iterations are divided evenly over as many
+//    workgroups as there are CUs, so shapes whose tile count is not a multiple of the CU count
+//    (17408 = 17 * 1024 rows) still fill the chip. A tile split between workgroups is
+//    finished by the last one to arrive (per-tile arrival counter), which sums the fp32
+//    partials in a fixed order (deterministic) and writes y.
+//  * workgroups are renumbered so that consecutive work (same weight rows, neighbouring
+//    activation tiles and K ranges) lands on one XCD and shares its L2.
+// fp32 / bf16 activations use the generic kernel below.
+#pragma once
+#include "gsq_decode.h"
+#include "gsq_qmm_decode.h"
+
+namespace gsq {
+
+enum { QDT_F32 = 0, QDT_F16 = 1, QDT_BF16 = 2 };
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void qmm_store_y(void* y, int dt, int64_t i, float v) {
+  if (dt == QDT_F16) reinterpret_cast<_Float16*>(y)[i] = (_Float16)v;
+  else if (dt == QDT_BF16) {
+    uint32_t b = __builtin_bit_cast(uint32_t, v);
+    b += 0x7FFFu + ((b >> 16) & 1u);
+    reinterpret_cast<uint16_t*>(y)[i] = (uint16_t)(b >> 16);
+  } else reinterpret_cast<float*>(y)[i] = v;
+}
+
+// ---- MFMA kernel ----------------------------------------------------------------------
+constexpr int kQWaves = 4;                  // waves per workgroup
+constexpr int kQWRows = 64;                 // weight rows per wave
+constexpr int kQBN = kQWaves * kQWRows;     // weight rows per tile
+constexpr int kQLds = 160 * 1024;
+constexpr int kQSlotFloats = 256 * kQBN;    // one partial-sum slot (BM <= 256)
+
+template <int T>
+struct QmmGeo {
+  static constexpr int kBB = BlockBytes<T>::v;
+  // granules per row slot (= DMA instructions per column): enough for a superblock at any
+  // 2-byte offset within its first granule, rounded up to an odd count so that the sixteen
+  // rows a wave reads at once fall into distinct LDS bank groups
+  static constexpr int kGran = ((kBB + 15) / 16 + 1) | 1;
+  static constexpr int kSlot = kGran * 16;
+  static constexpr int kRing = 2 * kQWRows * kSlot;  // per wave: two columns
+};
+
+struct QmmMfmaArgs {
+  const uint8_t* packed;
+  const _Float16* x;
+  void* y;
+  int M, N, K;
+  int y_dtype;
+  int nblk;              // superblocks per row (K / 256)
+  long long row_bytes;
+  int mt;                // activation tiles
+  int units;             // tiles * nblk
+  int G;                 // workgroups
+  int xcd_remap;         // G is a multiple of 8
+  int lx;                // activation ring depth (K32 stages)
+  const uint8_t* tbl;    // the type's table image (codebook + sign masks), or null
+  int tbl_bytes;         // multiple of 16
+  int x_off, w_off, bc_off;  // LDS layout
+  float* part;           // 2 * G partial slots of kQSlotFloats
+  int* cnt;              // per-tile arrival counters, indexed by the tile's first workgroup
+};
+
+// workgroup whose range holds column u: ranges are [floor(w*units/G), floor((w+1)*units/G))
+__device__ __forceinline__ int qmm_owner(int u, int units, int G) {
+  return (int)(((long long)(u + 1) * G + units - 1) / units) - 1;
+}
+__device__ __forceinline__ int qmm_first_col(int w, int units, int G) {
+  return (int)((long long)w * units / G);
+}
+
+template <int MF>
+__device__ __forceinline__ void qmm_store_tile(const QmmMfmaArgs& a, const float4_t (&acc)[MF][4], int m0, int n0,
+                                               int lane) {
+#pragma unroll
+  for (int i = 0; i < MF; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = n0 + 16 * j + (lane & 15);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = m0 + 16 * i + 4 * (lane >> 4) + e;
+        if (m < a.M && n < a.N) qmm_store_y(a.y, a.y_dtype, (int64_t)m * a.N + n, acc[i][j][e]);
+      }
+    }
+}
+
+// Issues the activation stages of one workgroup in order: stage q (ring slot b) of tile t,
+// column c; row[i] = this lane's source row (clamped to the matrix) and octet for DMA
+// instruction i, laid out for the XOR-swizzled ring (octet o of row m at o ^ ((m >> 2) & 3)).
+template <int NX, int BM>
+struct QmmXIter {
+  int q, t, c, b;
+  const _Float16* row[NX];
+  __device__ void rows(const QmmMfmaArgs& a, int wave, int lane) {
+    const int m0 = (t % a.mt) * BM;
+#pragma unroll
+    for (int i = 0; i < NX; ++i) {
+      const int s = (wave * NX + i) * 64 + lane;
+      const int m = s >> 2;
+      const int o = (s & 3) ^ ((m >> 2) & 3);
+      row[i] = a.x + (long long)min(m0 + m, a.M - 1) * a.K + 8 * o;
+    }
+  }
+  __device__ void init(const QmmMfmaArgs& a, int ub, int wave, int lane) {
+    q = 0;
+    b = 0;
+    t = ub / a.nblk;
+    c = ub - t * a.nblk;
+    rows(a, wave, lane);
+  }
+  __device__ void issue(const QmmMfmaArgs& a, uint8_t* xring, int wave, int lane) {
+    const int kk = c * 256 + (q & 7) * 32;
+    uint8_t* buf = xring + b * (BM * 64) + wave * NX * 1024;
+#pragma unroll
+    for (int i = 0; i < NX; ++i)
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(row[i] + kk), (lds_ptr_t)(buf + i * 1024), 16, 0, 0);
+    ++q;
+    if (++b == a.lx) b = 0;
+    if ((q & 7) == 0 && ++c == a.nblk) {
+      c = 0;
+      ++t;
+      rows(a, wave, lane);
+    }
+  }
+};
+
+template <int T, int MF, bool A4>
+__global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs a) {
+  using Geo = QmmGeo<T>;
+  constexpr int BB = Geo::kBB, GW = Geo::kGran, S = Geo::kSlot;
+  constexpr int BM = 16 * MF, NX = MF / 4;  // NX: activation DMA instructions per wave per stage
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int bid = blockIdx.x;
+  const int w = a.xcd_remap ? (bid & 7) * (a.G >> 3) + (bid >> 3) : bid;
+  const int ub = qmm_first_col(w, a.units, a.G), ue = qmm_first_col(w + 1, a.units, a.G);
+  const int ncols = ue - ub;  // >= 1: G <= units
+  const int Q = 8 * ncols;    // K32 stages of this workgroup
+  const int lx = a.lx;
+  uint8_t* xring = lds + a.x_off;
+  uint8_t* wring = lds + a.w_off + wave * Geo::kRing;
+  const uint8_t* tbl = lds;
+
+  // the type's table image first in this wave's DMA order: the first wait covers it
+  if (a.tbl_bytes) dma_copy(a.tbl, a.tbl_bytes, lds, wave, kQWaves, lane);
+
+  // activation stages are issued in order by an iterator
+  QmmXIter<NX, BM> xi;
+  xi.init(a, ub, wave, lane);
+  // weight column cl (local index): the wave's 64 superblocks, granule e of the column at
+  // slot byte 16e (row e / GW, granule e % GW of that row); granules past a row's last one
+  // reload its last granule so every lane stays active and the count stays fixed
+  auto issue_w = [&](int cl) {
+    const int u = ub + cl;
+    const int tile = u / a.nblk, c = u - tile * a.nblk;
+    const int n0 = (tile / a.mt) * kQBN + wave * kQWRows;
+    uint8_t* buf = wring + (cl & 1) * (kQWRows * S);
+#pragma unroll
+    for (int i = 0; i < GW; ++i) {
+      const int e = i * 64 + lane;
+      const int r = e / GW, qg = e - r * GW;
+      const int n = min(n0 + r, a.N - 1);
+      const uintptr_t p = reinterpret_cast<uintptr_t>(a.packed) + (uintptr_t)((long long)n * a.row_bytes) +
+                          (uintptr_t)c * BB;
+      const uintptr_t a0 = p & ~(uintptr_t)15;
+      const int ng = (int)((p + BB + 15 - a0) >> 4);
+      const uintptr_t src = a0 + (uintptr_t)(qg < ng ? qg : ng - 1) * 16;
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src), (lds_ptr_t)(buf + i * 1024), 16, 0, 0);
+    }
+  };
+
+  // DMA instructions this wave has issued before the issues of stage q (the table copy
+  // precedes everything and cancels out of every difference below)
+  const int P = min(lx - 1, Q);
+  auto issued_before = [&](int q) {
+    return GW + NX * P + NX * max(0, min(q, Q - lx + 1)) + GW * min((q + 7) >> 3, ncols - 1);
+  };
+  auto end_x = [&](int k) { return k < P ? GW + NX * (k + 1) : issued_before(k - lx + 1) + NX; };
+  auto end_w = [&](int c) {
+    if (c == 0) return GW;
+    const int qp = 8 * (c - 1);
+    return issued_before(qp) + (qp + lx - 1 < Q ? NX : 0) + GW;
+  };
+
+  // B operands of stage q: the four 16-row blocks of the wave's weight rows, group q % 8 of
+  // column q / 8; dl = the low address bits of the lane's four superblocks in that column
+  auto decode = [&](int q, const uint32_t (&dl)[4], half8_t (&bf)[4]) {
+    const uint8_t* wb = wring + ((q >> 3) & 1) * (kQWRows * S);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t o[4];
+      QmmDec<T, A4>::run(wb + (16 * j + (lane & 15)) * S + dl[j], tbl, q & 7, lane >> 4, o);
+      bf[j] = __builtin_bit_cast(half8_t, o);
+    }
+  };
+  auto col_delta = [&](int q, uint32_t (&dl)[4]) {
+    const int u = ub + (q >> 3);
+    const int tl = u / a.nblk, c = u - tl * a.nblk;
+    const int n0 = (tl / a.mt) * kQBN + wave * kQWRows;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = min(n0 + 16 * j + (lane & 15), a.N - 1);
+      dl[j] = (uint32_t)((reinterpret_cast<uintptr_t>(a.packed) + (uintptr_t)((long long)n * a.row_bytes) +
+                          (uintptr_t)c * BB) & 15u);
+    }
+  };
+  // A operands of a stage: MF 16-row blocks (row l % 16, octet l / 16, swizzled)
+  const int xoff = (lane & 15) * 64 + (((lane >> 4) ^ ((lane >> 2) & 3)) << 4);
+  int* bc = reinterpret_cast<int*>(lds + a.bc_off);
+
+  // prologue: table, column 0 and the first activation stages in flight; stage 0's weights
+  issue_w(0);
+  for (int q = 0; q < P; ++q) xi.issue(a, xring, wave, lane);
+  wait_vmcnt(NX * (P - 1));  // table, column 0 and stage 0 (this wave's share)
+  __syncthreads();
+  uint32_t dl[4];
+  col_delta(0, dl);
+  half8_t bcur[4];
+  decode(0, dl, bcur);
+  int rb = 0;  // ring slot of the stage being multiplied
+
+  // one segment = this workgroup's columns of one tile; stage q multiplies its activations
+  // with weights decoded during stage q - 1 and decodes the weights of stage q + 1
+  for (int q0 = 0; q0 < Q;) {
+    const int u0 = ub + (q0 >> 3);
+    const int tile = u0 / a.nblk;
+    const int q1 = q0 + 8 * (min(ue, (tile + 1) * a.nblk) - u0);
+    const int m0 = (tile % a.mt) * BM, n0 = (tile / a.mt) * kQBN + wave * kQWRows;
+    float4_t acc[MF][4];
+#pragma unroll
+    for (int i = 0; i < MF; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = (float4_t){0.f, 0.f, 0.f, 0.f};
+
+    for (int q = q0; q < q1; ++q) {
+      const int cl = q >> 3;
+      {  // stage q's activations and the column of stage q + 1 have landed (this wave's DMAs)
+        int need = end_x(q);
+        if (q + 1 < Q) need = max(need, end_w((q + 1) >> 3));
+        const int n = issued_before(q) - need;
+        wait_vmcnt(n > 63 ? 63 : n);
+      }
+      // every wave's DMAs of stage q are in; every wave is done with stage q - 1's buffer
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      if (q + lx - 1 < Q) xi.issue(a, xring, wave, lane);
+      if ((q & 7) == 0 && cl + 1 < ncols) issue_w(cl + 1);
+      half8_t af[MF];
+      {
+        const uint32_t* xb = reinterpret_cast<const uint32_t*>(xring + rb * (BM * 64) + xoff);
+#pragma unroll
+        for (int i = 0; i < MF; ++i) {
+          const uint32_t* p = xb + i * 256;
+          const uint32_t aw[4] = {p[0], p[1], p[2], p[3]};
+          af[i] = __builtin_bit_cast(half8_t, aw);
+        }
+      }
+      if (++rb == lx) rb = 0;
+      // weights of stage q + 1 (after the last stage they come from stale, in-bounds LDS and
+      // are not used): unconditional, in one scheduling region with the MFMAs
+      if (((q + 1) & 7) == 0) col_delta(q + 1, dl);
+      half8_t bnext[4];
+      decode(q + 1, dl, bnext);
+#pragma unroll
+      for (int i = 0; i < MF; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bcur[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bcur[j] = bnext[j];
+    }
+
+    // end of this workgroup's part of `tile`
+    const int wf = qmm_owner(tile * a.nblk, a.units, a.G);
+    const int wl = qmm_owner(tile * a.nblk + a.nblk - 1, a.units, a.G);
+    if (wf == wl) {
+      qmm_store_tile<MF>(a, acc, m0, n0, lane);
+    } else {
+      // slot 2w: the tile this workgroup starts in; slot 2w + 1: the tile it ends in
+      const int slot = 2 * w + (q0 == 0 ? 0 : 1);
+      float4_t* ps = reinterpret_cast<float4_t*>(a.part + (size_t)slot * kQSlotFloats);
+#pragma unroll
+      for (int i = 0; i < MF; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ps[(i * 4 + j) * 256 + tid] = acc[i][j];
+      __threadfence();
+      __syncthreads();
+      if (tid == 0) bc[0] = atomicAdd(&a.cnt[wf], 1);
+      __syncthreads();
+      const int arrived = bc[0];
+      if (arrived == wl - wf) {  // last to arrive: sum the partials in workgroup order
+        __threadfence();
+        const int mb = m0 + 4 * (lane >> 4), nb = n0 + (lane & 15);
+        constexpr int CH = 8;  // output blocks per batch of loads
+#pragma unroll 1
+        for (int ij0 = 0; ij0 < MF * 4; ij0 += CH) {
+          float4_t sum[CH];
+#pragma unroll
+          for (int t = 0; t < CH; ++t) sum[t] = (float4_t){0.f, 0.f, 0.f, 0.f};
+          for (int v = wf; v <= wl; ++v) {
+            const int vs = 2 * v + (tile == qmm_first_col(v, a.units, a.G) / a.nblk ? 0 : 1);
+            const float4_t* pv = reinterpret_cast<const float4_t*>(a.part + (size_t)vs * kQSlotFloats) + ij0 * 256 + tid;
+            float4_t ld[CH];
+#pragma unroll
+            for (int t = 0; t < CH; ++t) ld[t] = pv[t * 256];
+#pragma unroll
+            for (int t = 0; t < CH; ++t) sum[t] += ld[t];
+          }
+#pragma unroll
+          for (int t = 0; t < CH; ++t) {
+            const int ij = ij0 + t;
+            const int n = nb + 16 * (ij & 3);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int m = mb + 16 * (ij >> 2) + e;
+              if (m < a.M && n < a.N) qmm_store_y(a.y, a.y_dtype, (int64_t)m * a.N + n, sum[t][e]);
+            }
+          }
+        }
+        if (tid == 0) a.cnt[wf] = 0;
+      }
+      __syncthreads();
+    }
+    q0 = q1;
+  }
+}
+
+// ---- generic kernel (fp32 / bf16 activations) ------------------------------------------
+// 64 x 64 output tile per 256 threads over K steps of 64: half of the threads decode 64 rows x
+// two groups of weights (exact fp32 -> fp16), the other half stage the activations as fp16
+// (qmm.py:160-165 converts fp32 activations to half the same way); each wave multiplies a
+// 32 x 32 sub-tile with v_mfma_f32_16x16x32_f16.
+constexpr int kGBM = 64, kGBN = 64, kGKS = 64, kGStride = kGKS + 8;
+
+struct QmmArgs {
+  const uint8_t* packed;
+  const void* x;
+  void* y;
+  int64_t M, N;
+  int K, x_dtype, y_dtype;
+  DevTables tb;
+};
+
+__device__ __forceinline__ float qmm_load_x(const void* x, int dt, int64_t i) {
+  if (dt == QDT_F16) return (float)reinterpret_cast<const _Float16*>(x)[i];
+  if (dt == QDT_BF16) return __builtin_bit_cast(float, (uint32_t)reinterpret_cast<const uint16_t*>(x)[i] << 16);
+  return reinterpret_cast<const float*>(x)[i];
+}
+
+template <int T>
+__global__ void __launch_bounds__(256) qmm_generic_kernel(QmmArgs a) {
+  constexpr int BB = BlockBytes<T>::v;
+  __shared__ __attribute__((aligned(16))) _Float16 wt[kGBN * kGStride];
+  __shared__ __attribute__((aligned(16))) _Float16 xt[kGBM * kGStride];
+  const int tid = threadIdx.x;
+  const int64_t n0 = (int64_t)blockIdx.x * kGBN;
+  const int64_t m0 = (int64_t)blockIdx.y * kGBM;
+  const int nb = a.K / 256;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  float4_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = (float4_t){0.f, 0.f, 0.f, 0.f};
+
+  for (int k0 = 0; k0 < a.K; k0 += kGKS) {
+    if (tid < 128) {
+      const int r = tid >> 1, kg = tid & 1;
+      const int64_t n = n0 + r;
+      _Float16* dst = wt + r * kGStride + 32 * kg;
+      if (n < a.N) {
+        const int gidx = (k0 >> 5) + kg;
+        const uint8_t* blk = a.packed + (n * nb + (gidx >> 3)) * BB;
+        float v[32];
+        dq_group<T>(blk, gidx & 7, a.tb, v);
+#pragma unroll
+        for (int i = 0; i < 32; ++i) dst[i] = (_Float16)v[i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) dst[i] = (_Float16)0.f;
+      }
+    } else {
+      const int t = tid - 128, r = t >> 1, half = t & 1;
+      const int64_t m = m0 + r;
+      _Float16* dst = xt + r * kGStride + 32 * half;
+      if (m < a.M) {
+        const int64_t base = m * a.K + k0 + 32 * half;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) dst[i] = (_Float16)qmm_load_x(a.x, a.x_dtype, base + i);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) dst[i] = (_Float16)0.f;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < kGKS; kk += 32) {
+      half8_t af[2], bf[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        af[i] = *reinterpret_cast<const half8_t*>(xt + (wm * 32 + i * 16 + (lane & 15)) * kGStride + kk + 8 * (lane >> 4));
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        bf[j] = *reinterpret_cast<const half8_t*>(wt + (wn * 32 + j * 16 + (lane & 15)) * kGStride + kk + 8 * (lane >> 4));
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    __syncthreads();
+  }
+  // C layout: lane holds rows 4*(lane/16)+e (e=0..3) of column lane%16 of each 16x16 tile
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t n = n0 + wn * 32 + j * 16 + (lane & 15);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t m = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + e;
+        if (m < a.M && n < a.N) qmm_store_y(a.y, a.y_dtype, m * a.N + n, acc[i][j][e]);
+      }
+    }
+}
+
+// ---- host side --------------------------------------------------------------------------
+extern QmmTuning g_qmm_tuning;
+
+int qmv_table_bytes(int qt);  // the LDS table image of a type (gsq_qmv.hip)
+static bool qmm_grid_type(int qt) {
+  return qt == IQ1_S || qt == IQ1_M || qt == IQ2_XXS || qt == IQ2_XS || qt == IQ2_S || qt == IQ3_XXS || qt == IQ3_S;
+}
+
+template <int T, int MF, bool A4>
+static hipError_t launch_mfma_t(const QmmMfmaArgs& a, size_t lds, hipStream_t s) {
+  auto k = qmm_mfma_kernel<T, MF, A4>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, kQLds);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(k, dim3(a.G), dim3(256), lds, s, a);
+  return hipGetLastError();
+}
+
+template <int T, int MF>
+static hipError_t launch_mfma_mf(QmmMfmaArgs& a, size_t lds, bool a4, hipStream_t s) {
+  if constexpr (BlockBytes<T>::v % 4 == 0) {
+    if (a4) return launch_mfma_t<T, MF, true>(a, lds, s);
+  }
+  return launch_mfma_t<T, MF, false>(a, lds, s);
+}
+
+// Plan and launch the MFMA kernel for type T: activation tile height (MF 16-row blocks) from M,
+// ring depth from the LDS left after the tables and the weight rings.
+template <int T>
+static hipError_t launch_mfma(QmmMfmaArgs& a, int num_cus, const QmmWorkspace& ws, hipStream_t s) {
+  using Geo = QmmGeo<T>;
+  const int tbl = a.tbl_bytes;
+  const int wbytes = kQWaves * Geo::kRing;
+  auto ring_depth = [&](int mf) {
+    const int avail = kQLds - tbl - wbytes - 32;
+    int lx = avail / (16 * mf * 64);
+    return lx < g_qmm_tuning.lx_max ? lx : g_qmm_tuning.lx_max;
+  };
+  int mf = g_qmm_tuning.mf;
+  if (mf == 0) {
+    mf = a.M <= 64 ? 4 : (a.M <= 128 ? 8 : 16);
+    if (mf == 16 && ring_depth(16) < 3) mf = 8;
+  }
+  if (mf != 4 && mf != 8 && mf != 16) return hipErrorInvalidValue;
+  // stage q is read while stages up to q + lx - 1 load: at least two stages
+  const int lx = ring_depth(mf);
+  if (lx < 2) return hipErrorInvalidValue;
+  const int bm = 16 * mf;
+  a.lx = lx;
+  a.mt = (a.M + bm - 1) / bm;
+  const long long nt = ((long long)a.N + kQBN - 1) / kQBN;
+  const long long units = (long long)a.mt * nt * a.nblk;
+  if (units >= (1ll << 31)) return hipErrorInvalidValue;
+  a.units = (int)units;
+  a.G = num_cus < a.units ? num_cus : a.units;
+  if (a.G > ws.max_groups) a.G = ws.max_groups;
+  a.xcd_remap = (a.G % 8 == 0) ? 1 : 0;
+  a.x_off = (tbl + 15) & ~15;
+  a.w_off = a.x_off + lx * bm * 64;
+  a.bc_off = a.w_off + wbytes;
+  a.part = ws.part;
+  a.cnt = ws.cnt;
+  const size_t lds = (size_t)a.bc_off + 32;
+  const bool a4 = (reinterpret_cast<uintptr_t>(a.packed) & 3) == 0;
+  switch (mf) {
+    case 4: return launch_mfma_mf<T, 4>(a, lds, a4, s);
+    case 8: return launch_mfma_mf<T, 8>(a, lds, a4, s);
+    default: return launch_mfma_mf<T, 16>(a, lds, a4, s);
+  }
+}
+
+template <int T>
+static hipError_t launch_generic_t(const QmmArgs& a, hipStream_t s) {
+  dim3 grid((unsigned)((a.N + kGBN - 1) / kGBN), (unsigned)((a.M + kGBM - 1) / kGBM));
+  hipLaunchKernelGGL(qmm_generic_kernel<T>, grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+template <int T>
+static hipError_t launch_qmm_type(const uint8_t* packed, const void* x, int xdt, void* y, int ydt, int64_t M,
+                                  int64_t N, int K, const DevTables& tb, int num_cus, const QmmWorkspace& ws,
+                                  hipStream_t s) {
+  if (xdt == QDT_F16 && ws.part && M < (1ll << 31) && N < (1ll << 31)) {
+    QmmMfmaArgs a{};
+    a.packed = packed;
+    a.x = static_cast<const _Float16*>(x);
+    a.y = y;
+    a.M = (int)M;
+    a.N = (int)N;
+    a.K = K;
+    a.y_dtype = ydt;
+    a.nblk = K / 256;
+    a.row_bytes = (long long)a.nblk * BlockBytes<T>::v;
+    if (qmm_grid_type(T)) {
+      if (!tb.qmv_tbl) return hipErrorInvalidValue;
+      a.tbl = tb.qmv_tbl;
+      a.tbl_bytes = qmv_table_bytes(T);
+    }
+    return launch_mfma<T>(a, num_cus, ws, s);
+  }
+  QmmArgs a;
+  a.packed = packed; a.x = x; a.y = y; a.M = M; a.N = N; a.K = K; a.x_dtype = xdt; a.y_dtype = ydt; a.tb = tb;
+  return launch_generic_t<T>(a, s);
+}
+
+}  // namespace gsq

@@ -525,34 +525,6 @@ __device__ __forceinline__ void dma_item(uintptr_t start, int bytes, int n, uint
   }
 }
 
-// Cooperative DMA of a 16-byte aligned buffer of `bytes` (a multiple of 16) by all waves of
-// the workgroup; returns the instructions this wave issued.
-__device__ __forceinline__ int dma_copy(const void* src, int bytes, uint8_t* dst, int wave, int nw, int lane) {
-  const int ngran = bytes >> 4, per_wave = 64;
-  int issued = 0;
-  for (int c0 = wave * per_wave; c0 < ngran; c0 += nw * per_wave) {
-    const int c = c0 + lane;
-    if (c < ngran)
-      __builtin_amdgcn_global_load_lds(static_cast<const uint8_t*>(src) + (size_t)c * 16,
-                                       (__attribute__((address_space(3))) void*)(dst + c0 * 16), 16, 0, 0);
-    ++issued;
-  }
-  return issued;
-}
-
-// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding); n above 31 waits for
-// vmcnt(31), and a smaller immediate only waits longer.
-__device__ __forceinline__ void wait_vmcnt(int n) {
-#define GSQ_VMW(k) case k: __builtin_amdgcn_s_waitcnt(0x0F70 | ((k) & 15) | (((k) >> 4) << 14)); break;
-  switch (n < 0 ? 0 : n) {
-    GSQ_VMW(0) GSQ_VMW(1) GSQ_VMW(2) GSQ_VMW(3) GSQ_VMW(4) GSQ_VMW(5) GSQ_VMW(6) GSQ_VMW(7)
-    GSQ_VMW(8) GSQ_VMW(9) GSQ_VMW(10) GSQ_VMW(11) GSQ_VMW(12) GSQ_VMW(13) GSQ_VMW(14) GSQ_VMW(15)
-    GSQ_VMW(16) GSQ_VMW(17) GSQ_VMW(18) GSQ_VMW(19) GSQ_VMW(20) GSQ_VMW(21) GSQ_VMW(22) GSQ_VMW(23)
-    GSQ_VMW(24) GSQ_VMW(25) GSQ_VMW(26) GSQ_VMW(27) GSQ_VMW(28) GSQ_VMW(29) GSQ_VMW(30) GSQ_VMW(31)
-    default: __builtin_amdgcn_s_waitcnt(0x0F70 | 15 | (1 << 14)); break;
-  }
-#undef GSQ_VMW
-}
 
 __device__ __forceinline__ float load_x(const void* x, int dt, int64_t i) {
   if (dt == DT_F16) return (float)reinterpret_cast<const _Float16*>(x)[i];

@@ -136,6 +136,52 @@ def test_qmm_matches_oracle(qtype, rows):
     np.testing.assert_allclose(y, want, rtol=2e-3, atol=2e-3 * scale)  # reference test_all_qmm.py:38-39
 
 
+# Multi-tile shapes: several 256-row weight tiles, several activation tiles, and K split over
+# workgroups (stream-K), including tiles whose partial sums come from many workgroups.
+QMM_SHAPES = [
+    (300, 520, 2048),   # two 256-row activation tiles (or 128-row), ragged weight tile
+    (64, 1000, 1024),   # 64-row activation tiles, four weight tiles
+    (512, 2048, 4096),  # 16 tiles x 16 columns: one column per workgroup, 16 partials per tile
+    (200, 1536, 5120),  # 20 columns per tile over 6 tiles
+]
+
+
+@pytest.mark.parametrize("qtype", ["Q4_K", "Q6_K", "IQ3_S", "IQ1_M", "IQ2_XS", "IQ4_XS"])
+@pytest.mark.parametrize("shape", QMM_SHAPES)
+def test_qmm_multi_tile_shapes(qtype, shape):
+    from mlx_gsq_amd.runtime.kernels.qmm import quantized_matmul
+    M, N, K = shape
+    print(f"qmm {qtype} M={M} N={N} K={K}", flush=True)
+    packed = synth.make_packed(qtype, N, K, seed=17)
+    x = synth.make_x(M, K, seed=5, dtype=np.float16)
+    y = quantized_matmul(dev(x), dev(packed), qtype=qtype, out_features=N, in_features=K,
+                         out_dtype=torch.float32).cpu().numpy()
+    want = O.matmul_reference(x, packed, qtype, N, K, TABLES.get(qtype))
+    assert rel_l2(y, want) <= 1e-3, rel_l2(y, want)
+    scale = np.abs(want).max()
+    np.testing.assert_allclose(y, want, rtol=2e-3, atol=2e-3 * scale)
+
+
+@pytest.mark.parametrize("qtype", QTYPES)
+def test_qmm_unaligned_packed_view_deterministic(qtype):
+    """A 2-byte aligned packed view (no 4-byte word reads, superblocks at every offset within
+    their 16-byte granules); two launches give bit-identical results (fixed partial-sum order)."""
+    from mlx_gsq_amd.runtime.kernels.qmm import quantized_matmul
+    M, N, K = 96, 300, 3072
+    print(f"qmm unaligned {qtype}", flush=True)
+    packed = synth.make_packed(qtype, N, K, seed=23)
+    big = torch.zeros(packed.size + 64, dtype=torch.uint8, device="cuda")
+    big[6:6 + packed.size] = dev(packed)
+    view = big[6:6 + packed.size]
+    x = synth.make_x(M, K, seed=9, dtype=np.float16)
+    xd = dev(x)
+    y1 = quantized_matmul(xd, view, qtype=qtype, out_features=N, in_features=K, out_dtype=torch.float32)
+    y2 = quantized_matmul(xd, view, qtype=qtype, out_features=N, in_features=K, out_dtype=torch.float32)
+    assert torch.equal(y1, y2)
+    want = O.matmul_reference(x, packed, qtype, N, K, TABLES.get(qtype))
+    assert rel_l2(y1.cpu().numpy(), want) <= 1e-3, rel_l2(y1.cpu().numpy(), want)
+
+
 @pytest.mark.parametrize("qtype", ["Q4_K", "IQ3_S", "Q6_K"])
 def test_qmm_fp16_output_and_fp32_input(qtype):
     from mlx_gsq_amd.runtime.kernels.qmm import quantized_matmul

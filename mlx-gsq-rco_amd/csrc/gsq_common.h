@@ -70,7 +70,7 @@ struct QmvTuning {
 // M) and the largest activation ring depth.
 struct QmmTuning {
   int mf;
-  int lx_max;
+  int reserved;
 };
 
 // Per-device QMM workspace, allocated once: fp32 partial tiles of workgroups that share an

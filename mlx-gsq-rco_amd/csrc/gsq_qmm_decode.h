@@ -59,7 +59,7 @@ struct QmmDec;
 // Q2_K (k_decode.py:18-30): w = d*(sm&15)*q - dmin*(sm>>4)
 template <bool A4>
 struct QmmDec<Q2_K, A4> {
-  __device__ static void run(const uint8_t* sb, const uint8_t*, int g, int kq, uint32_t (&o)[4]) {
+  __device__ __forceinline__ static void run(const uint8_t* sb, const uint8_t*, int g, int kq, uint32_t (&o)[4]) {
     uint32_t q[2];
     lds_words<2, A4>(sb, 16 + (g >> 2) * 32 + 8 * kq, q);
     const int sh = 2 * (g & 3);
@@ -76,7 +76,7 @@ struct QmmDec<Q2_K, A4> {
 // Q4_K (k_decode.py:31-50): w = d*sc*q - dmin*mn with 6-bit scales/mins
 template <bool A4>
 struct QmmDec<Q4_K, A4> {
-  __device__ static void run(const uint8_t* sb, const uint8_t*, int g, int kq, uint32_t (&o)[4]) {
+  __device__ __forceinline__ static void run(const uint8_t* sb, const uint8_t*, int g, int kq, uint32_t (&o)[4]) {
     uint32_t q[2];
     lds_words<2, A4>(sb, 16 + (g >> 1) * 32 + 8 * kq, q);
     const int sh = 4 * (g & 1);
@@ -104,7 +104,7 @@ struct QmmDec<Q4_K, A4> {
 // Q6_K (k_decode.py:51-65): w = d*scale*(q - 32), q = low nibble | 2 high bits << 4
 template <bool A4>
 struct QmmDec<Q6_K, A4> {
-  __device__ static void run(const uint8_t* sb, const uint8_t*, int g, int kq, uint32_t (&o)[4]) {
+  __device__ __forceinline__ static void run(const uint8_t* sb, const uint8_t*, int g, int kq, uint32_t (&o)[4]) {
     const int h = g >> 2, pl = g & 3;
     uint32_t ql[2], qh[2];
     lds_words<2, A4>(sb, h * 64 + (pl & 1) * 32 + 8 * kq, ql);
@@ -122,7 +122,7 @@ struct QmmDec<Q6_K, A4> {
 // IQ4_XS (k_decode.py:66-80): w = d*scale*kvalues[q]; kvalues + 128 looked up as bytes
 template <bool A4>
 struct QmmDec<IQ4_XS, A4> {
-  __device__ static void run(const uint8_t* sb, const uint8_t*, int g, int kq, uint32_t (&o)[4]) {
+  __device__ __forceinline__ static void run(const uint8_t* sb, const uint8_t*, int g, int kq, uint32_t (&o)[4]) {
     uint32_t q[2];
     lds_words<2, A4>(sb, 8 + 16 * g + 8 * (kq & 1), q);
     const int sh = 4 * (kq >> 1);
@@ -151,7 +151,7 @@ struct QmmDec<IQ4_XS, A4> {
 template <bool A4>
 struct QmmDec<IQ3_S, A4> {
   static constexpr uint32_t kGridB = 512 * 4 * 2;
-  __device__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+  __device__ __forceinline__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
     const float d = h2f(lds_u16(sb, 0));
     const uint32_t sbyte = lds_u8(sb, 106 + (g >> 1));
     const float db = d * (float)(1u + 2u * ((sbyte >> (4 * (g & 1))) & 15u));
@@ -183,7 +183,7 @@ __device__ __forceinline__ void grid8(const uint8_t* tbl, uint32_t qi, float d, 
 template <bool A4>
 struct QmmDec<IQ3_XXS, A4> {
   static constexpr uint32_t kGridB = 256 * 4 * 2;
-  __device__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+  __device__ __forceinline__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
     const uint32_t u = lds_w32<A4>(sb, 66 + 4 * g);
     const float d = h2f(lds_u16(sb, 0)) * (0.5f + (float)(u >> 28)) * 0.5f;
     const uint32_t* m = tbl_words(tbl, kGridB + ((u >> (7 * kq)) & 127u) * 16);
@@ -201,7 +201,7 @@ struct QmmDec<IQ3_XXS, A4> {
 template <bool A4>
 struct QmmDec<IQ2_XXS, A4> {
   static constexpr uint32_t kGridB = 256 * 8 * 2;
-  __device__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+  __device__ __forceinline__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
     const uint32_t u = lds_w32<A4>(sb, 2 + 8 * g + 4);
     const float d = h2f(lds_u16(sb, 0)) * (0.5f + (float)(u >> 28)) * 0.25f;
     grid8(tbl, lds_u8(sb, 2 + 8 * g + kq), d, 0.f, tbl_words(tbl, kGridB + ((u >> (7 * kq)) & 127u) * 16), o);
@@ -212,7 +212,7 @@ struct QmmDec<IQ2_XXS, A4> {
 template <bool A4>
 struct QmmDec<IQ2_XS, A4> {
   static constexpr uint32_t kGridB = 512 * 8 * 2;
-  __device__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+  __device__ __forceinline__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
     const uint32_t q = lds_u16(sb, 2 + 2 * (4 * g + kq));
     const uint32_t sc = (lds_u8(sb, 66 + g) >> (4 * (kq >> 1))) & 15u;
     const float d = h2f(lds_u16(sb, 0)) * (0.5f + (float)sc) * 0.25f;
@@ -224,7 +224,7 @@ struct QmmDec<IQ2_XS, A4> {
 template <bool A4>
 struct QmmDec<IQ2_S, A4> {
   static constexpr uint32_t kGridB = 1024 * 8 * 2;
-  __device__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+  __device__ __forceinline__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
     const int oo = 4 * g + kq;
     const uint32_t hi = (lds_u8(sb, 66 + g) >> (2 * kq)) & 3u;
     const uint32_t qi = lds_u8(sb, 2 + oo) | (hi << 8);
@@ -237,7 +237,7 @@ struct QmmDec<IQ2_S, A4> {
 // IQ1_S (iq_lookup_decode.py:27-30): w = d*(2*s+1)*(grid[qi][c] + delta) = fma(d, grid, d*delta)
 template <bool A4>
 struct QmmDec<IQ1_S, A4> {
-  __device__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+  __device__ __forceinline__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
     const uint32_t h = lds_u16(sb, 34 + 2 * g);
     const float d = h2f(lds_u16(sb, 0)) * (float)(2u * ((h >> 12) & 7u) + 1u);
     const float dd = (h & 32768u) ? -0.125f * d : 0.125f * d;
@@ -250,7 +250,7 @@ struct QmmDec<IQ1_S, A4> {
 // scale words' top nibbles
 template <bool A4>
 struct QmmDec<IQ1_M, A4> {
-  __device__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+  __device__ __forceinline__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
     uint32_t w[2];
     lds_words<2, A4>(sb, 48, w);
     const uint32_t w0 = w[0] & 0xFFFFu, w1 = w[0] >> 16, w2 = w[1] & 0xFFFFu, w3 = w[1] >> 16;

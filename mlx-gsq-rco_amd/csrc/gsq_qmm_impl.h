@@ -66,6 +66,105 @@ struct QmmGeo {
   static constexpr int kRing = 2 * kQWRows * kSlot;  // per wave: two columns
 };
 
+// Byte size of a type's LDS table image (the QMV kernel's image: fp16 codebook followed by
+// the sign masks); checked against the host-built image at launch.
+template <int T>
+constexpr int qmm_tbl_bytes() {
+  return T == IQ1_S || T == IQ1_M ? 2048 * 8 * 2
+       : T == IQ2_XXS            ? 256 * 8 * 2 + 128 * 16
+       : T == IQ2_XS             ? 512 * 8 * 2 + 128 * 16
+       : T == IQ2_S              ? 1024 * 8 * 2 + 256 * 16
+       : T == IQ3_XXS            ? 256 * 4 * 2 + 128 * 16
+       : T == IQ3_S              ? 512 * 4 * 2 + 16 * 8
+                                 : 0;
+}
+
+// LDS plan of (type, activation tile height MF x 16 rows): table image, activation ring of
+// kLx K32 stages (as deep as the LDS left over allows, up to 8), the four waves' weight rings
+// and a small broadcast slot.
+template <int T, int MF>
+struct QmmPlan {
+  static constexpr int kTbl = qmm_tbl_bytes<T>();
+  static constexpr int kW = kQWaves * QmmGeo<T>::kRing;
+  static constexpr int kLx0 = (kQLds - kTbl - kW - 32) / (16 * MF * 64);
+  static constexpr int kLx = kLx0 > 8 ? 8 : kLx0;
+  static constexpr int kXOff = kTbl;
+  static constexpr int kWOff = kXOff + kLx * 16 * MF * 64;
+  static constexpr int kBcOff = kWOff + kW;
+  static constexpr int kLds = kBcOff + 32;
+  static constexpr bool kValid = kLx >= 2;
+};
+
+// The DMA schedule of one wave (per K32 stage q of Q): the table copy, then column 0 and
+// activation stages 0 .. min(LX-1, Q)-1; stage q issues activation stage q + LX - 1 (NX
+// instructions, while it exists) and, at a column start, the next column (GW instructions).
+// Stage q needs activation stage q and the column of stage q + 1. qmm_wait_n is the number of
+// this wave's instructions that may still be in flight at that point (vmcnt is in order).
+constexpr int qmm_issued_before(int q, int Q, int LX, int NX, int GW) {
+  const int P = LX - 1 < Q ? LX - 1 : Q;
+  const int x = q < Q - LX + 1 ? q : Q - LX + 1;
+  const int cols = (q + 7) / 8 < Q / 8 - 1 ? (q + 7) / 8 : Q / 8 - 1;
+  return GW + NX * P + NX * (x > 0 ? x : 0) + GW * cols;
+}
+constexpr int qmm_wait_n(int q, int Q, int LX, int NX, int GW) {
+  const int P = LX - 1 < Q ? LX - 1 : Q;
+  int need = q < P ? GW + NX * (q + 1) : qmm_issued_before(q - LX + 1, Q, LX, NX, GW) + NX;
+  if (q + 1 < Q) {
+    const int c = (q + 1) / 8;
+    int ew = GW;
+    if (c > 0) {
+      const int qp = 8 * (c - 1);
+      ew = qmm_issued_before(qp, Q, LX, NX, GW) + (qp + LX - 1 < Q ? NX : 0) + GW;
+    }
+    need = need > ew ? need : ew;
+  }
+  return qmm_issued_before(q, Q, LX, NX, GW) - need;
+}
+// Every count the schedule produces (column counts 1..40 cover the start, steady state and
+// end of any range), distinct, in descending order.
+struct QmmWaitSet {
+  int v[64];
+  int n;
+};
+template <int LX, int NX, int GW>
+constexpr QmmWaitSet qmm_wait_set() {
+  QmmWaitSet w{};
+  w.n = 0;
+  for (int cols = 1; cols <= 40; ++cols)
+    for (int q = 0; q < 8 * cols; ++q) {
+      int c = qmm_wait_n(q, 8 * cols, LX, NX, GW);
+      if (c > 63) c = 63;
+      bool seen = false;
+      for (int i = 0; i < w.n; ++i) seen = seen || w.v[i] == c;
+      if (!seen && w.n < 64) w.v[w.n++] = c;
+    }
+  for (int i = 0; i < w.n; ++i)
+    for (int j = i + 1; j < w.n; ++j)
+      if (w.v[j] > w.v[i]) {
+        const int t = w.v[i];
+        w.v[i] = w.v[j];
+        w.v[j] = t;
+      }
+  return w;
+}
+template <int N>
+__device__ __forceinline__ void wait_vm_imm() {
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+// s_waitcnt vmcnt(c) for the largest schedule count c <= n: a short chain of compile-time
+// immediates, largest (steady-state) counts first
+template <int LX, int NX, int GW, int K = 0>
+__device__ __forceinline__ void qmm_wait(int n) {
+  constexpr QmmWaitSet W = qmm_wait_set<LX, NX, GW>();
+  if constexpr (K >= W.n) {
+    wait_vm_imm<0>();
+  } else {
+    constexpr int c = W.v[K];
+    if (n >= c) wait_vm_imm<c>();
+    else qmm_wait<LX, NX, GW, K + 1>(n);
+  }
+}
+
 struct QmmMfmaArgs {
   const uint8_t* packed;
   const _Float16* x;
@@ -78,13 +177,27 @@ struct QmmMfmaArgs {
   int units;             // tiles * nblk
   int G;                 // workgroups
   int xcd_remap;         // G is a multiple of 8
-  int lx;                // activation ring depth (K32 stages)
   const uint8_t* tbl;    // the type's table image (codebook + sign masks), or null
   int tbl_bytes;         // multiple of 16
-  int x_off, w_off, bc_off;  // LDS layout
   float* part;           // 2 * G partial slots of kQSlotFloats
   int* cnt;              // per-tile arrival counters, indexed by the tile's first workgroup
 };
+
+// Partial tiles travel between workgroups (possibly on different XCDs, whose L2 caches are
+// not coherent with each other) as whole 16-byte buffer stores written through to the
+// device-coherent level (sc1) and buffer loads that bypass the caches (sc0 sc1): no L2
+// write-back or invalidate of unrelated data, and full cache lines per wave instruction.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+constexpr int kQSlotBytes = kQSlotFloats * 4;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t qmm_slot_rsrc(float* part, int slot) {
+  return __builtin_amdgcn_make_buffer_rsrc(part + (size_t)slot * kQSlotFloats, 0, kQSlotBytes, 0x00020000);
+}
+__device__ __forceinline__ void qmm_st_coherent(__amdgpu_buffer_rsrc_t r, int off, float4_t v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, off, 0, 16 /* sc1 */);
+}
+__device__ __forceinline__ float4_t qmm_ld_coherent(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 17 /* sc0 sc1 */));
+}
 
 // workgroup whose range holds column u: ranges are [floor(w*units/G), floor((w+1)*units/G))
 __device__ __forceinline__ int qmm_owner(int u, int units, int G) {
@@ -95,8 +208,8 @@ __device__ __forceinline__ int qmm_first_col(int w, int units, int G) {
 }
 
 template <int MF>
-__device__ __forceinline__ void qmm_store_tile(const QmmMfmaArgs& a, const float4_t (&acc)[MF][4], int m0, int n0,
-                                               int lane) {
+__device__ __forceinline__ void qmm_store_tile(void* y, int ydt, int M, int N, const float4_t (&acc)[MF][4], int m0,
+                                               int n0, int lane) {
 #pragma unroll
   for (int i = 0; i < MF; ++i)
 #pragma unroll
@@ -105,7 +218,7 @@ __device__ __forceinline__ void qmm_store_tile(const QmmMfmaArgs& a, const float
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int m = m0 + 16 * i + 4 * (lane >> 4) + e;
-        if (m < a.M && n < a.N) qmm_store_y(a.y, a.y_dtype, (int64_t)m * a.N + n, acc[i][j][e]);
+        if (m < M && n < N) qmm_store_y(y, ydt, (int64_t)m * N + n, acc[i][j][e]);
       }
     }
 }
@@ -113,80 +226,101 @@ __device__ __forceinline__ void qmm_store_tile(const QmmMfmaArgs& a, const float
 // Issues the activation stages of one workgroup in order: stage q (ring slot b) of tile t,
 // column c; row[i] = this lane's source row (clamped to the matrix) and octet for DMA
 // instruction i, laid out for the XOR-swizzled ring (octet o of row m at o ^ ((m >> 2) & 3)).
-template <int NX, int BM>
+template <int NX, int BM, int LX>
 struct QmmXIter {
+  const _Float16* x;
+  int M, K, mt, nblk;
   int q, t, c, b;
   const _Float16* row[NX];
-  __device__ void rows(const QmmMfmaArgs& a, int wave, int lane) {
-    const int m0 = (t % a.mt) * BM;
+  __device__ __forceinline__ void rows(int wave, int lane) {
+    const int m0 = (t % mt) * BM;
 #pragma unroll
     for (int i = 0; i < NX; ++i) {
       const int s = (wave * NX + i) * 64 + lane;
       const int m = s >> 2;
       const int o = (s & 3) ^ ((m >> 2) & 3);
-      row[i] = a.x + (long long)min(m0 + m, a.M - 1) * a.K + 8 * o;
+      row[i] = x + (long long)min(m0 + m, M - 1) * K + 8 * o;
     }
   }
-  __device__ void init(const QmmMfmaArgs& a, int ub, int wave, int lane) {
+  __device__ __forceinline__ void init(const _Float16* x_, int M_, int K_, int mt_, int nblk_, int ub, int wave, int lane) {
+    x = x_;
+    M = M_;
+    K = K_;
+    mt = mt_;
+    nblk = nblk_;
     q = 0;
     b = 0;
-    t = ub / a.nblk;
-    c = ub - t * a.nblk;
-    rows(a, wave, lane);
+    t = ub / nblk;
+    c = ub - t * nblk;
+    rows(wave, lane);
   }
-  __device__ void issue(const QmmMfmaArgs& a, uint8_t* xring, int wave, int lane) {
+  __device__ __forceinline__ void issue(uint8_t* xring, int wave, int lane) {
     const int kk = c * 256 + (q & 7) * 32;
     uint8_t* buf = xring + b * (BM * 64) + wave * NX * 1024;
 #pragma unroll
     for (int i = 0; i < NX; ++i)
       __builtin_amdgcn_global_load_lds(static_cast<const void*>(row[i] + kk), (lds_ptr_t)(buf + i * 1024), 16, 0, 0);
     ++q;
-    if (++b == a.lx) b = 0;
-    if ((q & 7) == 0 && ++c == a.nblk) {
+    if (++b == LX) b = 0;
+    if ((q & 7) == 0 && ++c == nblk) {
       c = 0;
       ++t;
-      rows(a, wave, lane);
+      rows(wave, lane);
     }
   }
 };
 
 template <int T, int MF, bool A4>
-__global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs a) {
+__global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs args) {
+  // the arguments as plain values (no reference to the argument block escapes, so it is never
+  // copied to scratch memory, whose loads would wait on the DMA counter)
+  const uint8_t* const packed = args.packed;
+  const _Float16* const xg = args.x;
+  void* const yg = args.y;
+  const int M = args.M, N = args.N, K = args.K, ydt = args.y_dtype, nblk = args.nblk, mt = args.mt;
+  const int units = args.units, G = args.G, xcd = args.xcd_remap, tbl_bytes = args.tbl_bytes;
+  const long long row_bytes = args.row_bytes;
+  const uint8_t* const tblg = args.tbl;
+  float* const part = args.part;
+  int* const cnt = args.cnt;
   using Geo = QmmGeo<T>;
   constexpr int BB = Geo::kBB, GW = Geo::kGran, S = Geo::kSlot;
   constexpr int BM = 16 * MF, NX = MF / 4;  // NX: activation DMA instructions per wave per stage
+  using Plan = QmmPlan<T, MF>;
+  constexpr int LX = Plan::kLx;
+  static_assert(Plan::kValid, "activation ring needs two stages");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int bid = blockIdx.x;
-  const int w = a.xcd_remap ? (bid & 7) * (a.G >> 3) + (bid >> 3) : bid;
-  const int ub = qmm_first_col(w, a.units, a.G), ue = qmm_first_col(w + 1, a.units, a.G);
+  const int w = xcd ? (bid & 7) * (G >> 3) + (bid >> 3) : bid;
+  const int ub = qmm_first_col(w, units, G), ue = qmm_first_col(w + 1, units, G);
   const int ncols = ue - ub;  // >= 1: G <= units
   const int Q = 8 * ncols;    // K32 stages of this workgroup
-  const int lx = a.lx;
-  uint8_t* xring = lds + a.x_off;
-  uint8_t* wring = lds + a.w_off + wave * Geo::kRing;
+  constexpr int lx = LX;
+  uint8_t* xring = lds + Plan::kXOff;
+  uint8_t* wring = lds + Plan::kWOff + wave * Geo::kRing;
   const uint8_t* tbl = lds;
 
   // the type's table image first in this wave's DMA order: the first wait covers it
-  if (a.tbl_bytes) dma_copy(a.tbl, a.tbl_bytes, lds, wave, kQWaves, lane);
+  if (tbl_bytes) dma_copy(tblg, tbl_bytes, lds, wave, kQWaves, lane);
 
   // activation stages are issued in order by an iterator
-  QmmXIter<NX, BM> xi;
-  xi.init(a, ub, wave, lane);
+  QmmXIter<NX, BM, LX> xi;
+  xi.init(xg, M, K, mt, nblk, ub, wave, lane);
   // weight column cl (local index): the wave's 64 superblocks, granule e of the column at
   // slot byte 16e (row e / GW, granule e % GW of that row); granules past a row's last one
   // reload its last granule so every lane stays active and the count stays fixed
   auto issue_w = [&](int cl) {
     const int u = ub + cl;
-    const int tile = u / a.nblk, c = u - tile * a.nblk;
-    const int n0 = (tile / a.mt) * kQBN + wave * kQWRows;
+    const int tile = u / nblk, c = u - tile * nblk;
+    const int n0 = (tile / mt) * kQBN + wave * kQWRows;
     uint8_t* buf = wring + (cl & 1) * (kQWRows * S);
 #pragma unroll
     for (int i = 0; i < GW; ++i) {
       const int e = i * 64 + lane;
       const int r = e / GW, qg = e - r * GW;
-      const int n = min(n0 + r, a.N - 1);
-      const uintptr_t p = reinterpret_cast<uintptr_t>(a.packed) + (uintptr_t)((long long)n * a.row_bytes) +
+      const int n = min(n0 + r, N - 1);
+      const uintptr_t p = reinterpret_cast<uintptr_t>(packed) + (uintptr_t)((long long)n * row_bytes) +
                           (uintptr_t)c * BB;
       const uintptr_t a0 = p & ~(uintptr_t)15;
       const int ng = (int)((p + BB + 15 - a0) >> 4);
@@ -221,23 +355,23 @@ __global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs a) {
   };
   auto col_delta = [&](int q, uint32_t (&dl)[4]) {
     const int u = ub + (q >> 3);
-    const int tl = u / a.nblk, c = u - tl * a.nblk;
-    const int n0 = (tl / a.mt) * kQBN + wave * kQWRows;
+    const int tl = u / nblk, c = u - tl * nblk;
+    const int n0 = (tl / mt) * kQBN + wave * kQWRows;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int n = min(n0 + 16 * j + (lane & 15), a.N - 1);
-      dl[j] = (uint32_t)((reinterpret_cast<uintptr_t>(a.packed) + (uintptr_t)((long long)n * a.row_bytes) +
+      const int n = min(n0 + 16 * j + (lane & 15), N - 1);
+      dl[j] = (uint32_t)((reinterpret_cast<uintptr_t>(packed) + (uintptr_t)((long long)n * row_bytes) +
                           (uintptr_t)c * BB) & 15u);
     }
   };
   // A operands of a stage: MF 16-row blocks (row l % 16, octet l / 16, swizzled)
   const int xoff = (lane & 15) * 64 + (((lane >> 4) ^ ((lane >> 2) & 3)) << 4);
-  int* bc = reinterpret_cast<int*>(lds + a.bc_off);
+  int* bc = reinterpret_cast<int*>(lds + Plan::kBcOff);
 
   // prologue: table, column 0 and the first activation stages in flight; stage 0's weights
   issue_w(0);
-  for (int q = 0; q < P; ++q) xi.issue(a, xring, wave, lane);
-  wait_vmcnt(NX * (P - 1));  // table, column 0 and stage 0 (this wave's share)
+  for (int q = 0; q < P; ++q) xi.issue(xring, wave, lane);
+  qmm_wait<LX, NX, GW>(NX * (P - 1));  // table, column 0 and stage 0 (this wave's share)
   __syncthreads();
   uint32_t dl[4];
   col_delta(0, dl);
@@ -249,9 +383,9 @@ __global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs a) {
   // with weights decoded during stage q - 1 and decodes the weights of stage q + 1
   for (int q0 = 0; q0 < Q;) {
     const int u0 = ub + (q0 >> 3);
-    const int tile = u0 / a.nblk;
-    const int q1 = q0 + 8 * (min(ue, (tile + 1) * a.nblk) - u0);
-    const int m0 = (tile % a.mt) * BM, n0 = (tile / a.mt) * kQBN + wave * kQWRows;
+    const int tile = u0 / nblk;
+    const int q1 = q0 + 8 * (min(ue, (tile + 1) * nblk) - u0);
+    const int m0 = (tile % mt) * BM, n0 = (tile / mt) * kQBN + wave * kQWRows;
     float4_t acc[MF][4];
 #pragma unroll
     for (int i = 0; i < MF; ++i)
@@ -263,12 +397,11 @@ __global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs a) {
       {  // stage q's activations and the column of stage q + 1 have landed (this wave's DMAs)
         int need = end_x(q);
         if (q + 1 < Q) need = max(need, end_w((q + 1) >> 3));
-        const int n = issued_before(q) - need;
-        wait_vmcnt(n > 63 ? 63 : n);
+        qmm_wait<LX, NX, GW>(issued_before(q) - need);
       }
       // every wave's DMAs of stage q are in; every wave is done with stage q - 1's buffer
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      if (q + lx - 1 < Q) xi.issue(a, xring, wave, lane);
+      if (q + lx - 1 < Q) xi.issue(xring, wave, lane);
       if ((q & 7) == 0 && cl + 1 < ncols) issue_w(cl + 1);
       half8_t af[MF];
       {
@@ -296,25 +429,25 @@ __global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs a) {
     }
 
     // end of this workgroup's part of `tile`
-    const int wf = qmm_owner(tile * a.nblk, a.units, a.G);
-    const int wl = qmm_owner(tile * a.nblk + a.nblk - 1, a.units, a.G);
+    const int wf = qmm_owner(tile * nblk, units, G);
+    const int wl = qmm_owner(tile * nblk + nblk - 1, units, G);
     if (wf == wl) {
-      qmm_store_tile<MF>(a, acc, m0, n0, lane);
+      qmm_store_tile<MF>(yg, ydt, M, N, acc, m0, n0, lane);
     } else {
       // slot 2w: the tile this workgroup starts in; slot 2w + 1: the tile it ends in
       const int slot = 2 * w + (q0 == 0 ? 0 : 1);
-      float4_t* ps = reinterpret_cast<float4_t*>(a.part + (size_t)slot * kQSlotFloats);
+      const __amdgpu_buffer_rsrc_t ps = qmm_slot_rsrc(part, slot);
+      // every store has completed (device-coherent) before the arrival count is incremented
 #pragma unroll
       for (int i = 0; i < MF; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) ps[(i * 4 + j) * 256 + tid] = acc[i][j];
-      __threadfence();
+        for (int j = 0; j < 4; ++j) qmm_st_coherent(ps, ((i * 4 + j) * 256 + tid) * 16, acc[i][j]);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
-      if (tid == 0) bc[0] = atomicAdd(&a.cnt[wf], 1);
+      if (tid == 0) bc[0] = __hip_atomic_fetch_add(&cnt[wf], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __syncthreads();
       const int arrived = bc[0];
       if (arrived == wl - wf) {  // last to arrive: sum the partials in workgroup order
-        __threadfence();
         const int mb = m0 + 4 * (lane >> 4), nb = n0 + (lane & 15);
         constexpr int CH = 8;  // output blocks per batch of loads
 #pragma unroll 1
@@ -323,11 +456,11 @@ __global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs a) {
 #pragma unroll
           for (int t = 0; t < CH; ++t) sum[t] = (float4_t){0.f, 0.f, 0.f, 0.f};
           for (int v = wf; v <= wl; ++v) {
-            const int vs = 2 * v + (tile == qmm_first_col(v, a.units, a.G) / a.nblk ? 0 : 1);
-            const float4_t* pv = reinterpret_cast<const float4_t*>(a.part + (size_t)vs * kQSlotFloats) + ij0 * 256 + tid;
+            const int vs = 2 * v + (tile == qmm_first_col(v, units, G) / nblk ? 0 : 1);
+            const __amdgpu_buffer_rsrc_t pv = qmm_slot_rsrc(part, vs);
             float4_t ld[CH];
 #pragma unroll
-            for (int t = 0; t < CH; ++t) ld[t] = pv[t * 256];
+            for (int t = 0; t < CH; ++t) ld[t] = qmm_ld_coherent(pv, ((ij0 + t) * 256 + tid) * 16);
 #pragma unroll
             for (int t = 0; t < CH; ++t) sum[t] += ld[t];
           }
@@ -338,11 +471,11 @@ __global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs a) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const int m = mb + 16 * (ij >> 2) + e;
-              if (m < a.M && n < a.N) qmm_store_y(a.y, a.y_dtype, (int64_t)m * a.N + n, sum[t][e]);
+              if (m < M && n < N) qmm_store_y(yg, ydt, (int64_t)m * N + n, sum[t][e]);
             }
           }
         }
-        if (tid == 0) a.cnt[wf] = 0;
+        if (tid == 0) __hip_atomic_store(&cnt[wf], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       __syncthreads();
     }
@@ -459,68 +592,55 @@ static bool qmm_grid_type(int qt) {
 }
 
 template <int T, int MF, bool A4>
-static hipError_t launch_mfma_t(const QmmMfmaArgs& a, size_t lds, hipStream_t s) {
-  auto k = qmm_mfma_kernel<T, MF, A4>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, kQLds);
-    if (e != hipSuccess) return e;
-    attr_set = true;
+static hipError_t launch_mfma_t(const QmmMfmaArgs& a, hipStream_t s) {
+  if constexpr (!QmmPlan<T, MF>::kValid) {
+    return hipErrorInvalidValue;
+  } else {
+    auto k = qmm_mfma_kernel<T, MF, A4>;
+    static bool attr_set = false;
+    if (!attr_set) {
+      hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, kQLds);
+      if (e != hipSuccess) return e;
+      attr_set = true;
+    }
+    constexpr size_t lds = QmmPlan<T, MF>::kLds;
+    hipLaunchKernelGGL(k, dim3(a.G), dim3(256), lds, s, a);
+    return hipGetLastError();
   }
-  hipLaunchKernelGGL(k, dim3(a.G), dim3(256), lds, s, a);
-  return hipGetLastError();
 }
 
 template <int T, int MF>
-static hipError_t launch_mfma_mf(QmmMfmaArgs& a, size_t lds, bool a4, hipStream_t s) {
+static hipError_t launch_mfma_mf(const QmmMfmaArgs& a, bool a4, hipStream_t s) {
   if constexpr (BlockBytes<T>::v % 4 == 0) {
-    if (a4) return launch_mfma_t<T, MF, true>(a, lds, s);
+    if (a4) return launch_mfma_t<T, MF, true>(a, s);
   }
-  return launch_mfma_t<T, MF, false>(a, lds, s);
+  return launch_mfma_t<T, MF, false>(a, s);
 }
 
-// Plan and launch the MFMA kernel for type T: activation tile height (MF 16-row blocks) from M,
-// ring depth from the LDS left after the tables and the weight rings.
+// Plan and launch the MFMA kernel for type T: activation tile height (MF 16-row blocks) from M
+// (64 rows up to 64, 128 up to 192, else 256), then the stream-K grid:
+// one workgroup per CU, at most one per (tile, K column) unit.
 template <int T>
 static hipError_t launch_mfma(QmmMfmaArgs& a, int num_cus, const QmmWorkspace& ws, hipStream_t s) {
-  using Geo = QmmGeo<T>;
-  const int tbl = a.tbl_bytes;
-  const int wbytes = kQWaves * Geo::kRing;
-  auto ring_depth = [&](int mf) {
-    const int avail = kQLds - tbl - wbytes - 32;
-    int lx = avail / (16 * mf * 64);
-    return lx < g_qmm_tuning.lx_max ? lx : g_qmm_tuning.lx_max;
-  };
+  if (a.tbl_bytes != QmmPlan<T, 4>::kTbl) return hipErrorInvalidValue;
   int mf = g_qmm_tuning.mf;
-  if (mf == 0) {
-    mf = a.M <= 64 ? 4 : (a.M <= 128 ? 8 : 16);
-    if (mf == 16 && ring_depth(16) < 3) mf = 8;
-  }
+  if (mf == 0) mf = a.M <= 64 ? 4 : (a.M <= 192 ? 8 : 16);
   if (mf != 4 && mf != 8 && mf != 16) return hipErrorInvalidValue;
-  // stage q is read while stages up to q + lx - 1 load: at least two stages
-  const int lx = ring_depth(mf);
-  if (lx < 2) return hipErrorInvalidValue;
   const int bm = 16 * mf;
-  a.lx = lx;
   a.mt = (a.M + bm - 1) / bm;
-  const long long nt = ((long long)a.N + kQBN - 1) / kQBN;
-  const long long units = (long long)a.mt * nt * a.nblk;
+  const long long units = (long long)a.mt * (((long long)a.N + kQBN - 1) / kQBN) * a.nblk;
   if (units >= (1ll << 31)) return hipErrorInvalidValue;
   a.units = (int)units;
   a.G = num_cus < a.units ? num_cus : a.units;
   if (a.G > ws.max_groups) a.G = ws.max_groups;
   a.xcd_remap = (a.G % 8 == 0) ? 1 : 0;
-  a.x_off = (tbl + 15) & ~15;
-  a.w_off = a.x_off + lx * bm * 64;
-  a.bc_off = a.w_off + wbytes;
   a.part = ws.part;
   a.cnt = ws.cnt;
-  const size_t lds = (size_t)a.bc_off + 32;
   const bool a4 = (reinterpret_cast<uintptr_t>(a.packed) & 3) == 0;
   switch (mf) {
-    case 4: return launch_mfma_mf<T, 4>(a, lds, a4, s);
-    case 8: return launch_mfma_mf<T, 8>(a, lds, a4, s);
-    default: return launch_mfma_mf<T, 16>(a, lds, a4, s);
+    case 4: return launch_mfma_mf<T, 4>(a, a4, s);
+    case 8: return launch_mfma_mf<T, 8>(a, a4, s);
+    default: return launch_mfma_mf<T, 16>(a, a4, s);
   }
 }
 

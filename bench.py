@@ -16,7 +16,10 @@ Printed JSON line (one, on stdout):
                 same kernel and shape, else null
   per_type      per-type GB/s and fraction of peak over its 4 shapes (kernel time)
   per_launch_us median kernel time of every (type, shape)
-  qmm           tiled QMM at M=512 (configs[2] subset): TFLOP/s and fraction of dense fp16 peak
+  qmm           tiled QMM (configs[2]: IQ3_S and Q6_K, both shapes, M in {182, 512, 2048}):
+                TFLOP/s and fraction of the 2.5 PFLOP/s dense fp16 MFMA peak per case
+  layer_crossover  configs[3]: QMV vs QMM time per projection of the mixed layer, M in 1..16
+  decode_stack  configs[4]: 448 GEMVs (64 layers, 8.34 GB) in one HIP graph: GB/s, tokens/s
   cpu_baseline  the numpy oracle (dequant + float32 matmul, one thread) on a bounded sample
 
 Algorithmic bytes per QMV launch = N*(K/256)*block_bytes + M*K*2 (x fp16) + M*N*4 (y fp32).
@@ -24,6 +27,7 @@ Algorithmic bytes per QMV launch = N*(K/256)*block_bytes + M*K*2 (x fp16) + M*N*
 Extra modes for counter collection (rocprofv3 --pmc runs):
   --profile-case Q6_K:17408x5120   only launches of that product (rotating 8 weight copies)
   --copy-bytes N                   only a plain device-to-device copy of N bytes
+  --qmm-profile-case IQ3_S:512x17408x5120   only launches of that QMM product
 """
 from __future__ import annotations
 
@@ -189,35 +193,180 @@ def run_qmv(steps, warmup, device):
     return qc, per_launch, eager_ms, graph_ms
 
 
+QMM_TYPES = ("IQ3_S", "Q6_K")
+QMM_SHAPES = ((17408, 5120), (5120, 17408))
+QMM_ROWS = (182, 512, 2048)
+
+
 def run_qmm(device, reps=10):
+    """QMM for IQ3_S and Q6_K at both 27B shapes, M in {182, 512, 2048} rows of fp16
+    activations, fp32 output; time per launch from HIP events on the launch stream."""
     import torch
     from mlx_gsq_amd import _lib
     from mlx_gsq_amd.formats import TYPE_IDS
     lib = _lib.lib()
     out = {}
     stream = torch.cuda.current_stream(device)
-    for q in ("IQ3_S", "Q6_K"):
+    for q in QMM_TYPES:
         _lib.ensure_tables(q, device)
-        for (n, k) in ((17408, 5120), (5120, 17408)):
-            m = 512
+        for (n, k) in QMM_SHAPES:
             packed = make_device_packed(q, n, k, seed=77, device=device)
+            for m in QMM_ROWS:
+                x = torch.randn(m, k, device=device).half()
+                y = torch.empty(m, n, device=device, dtype=torch.float32)
+                args = (TYPE_IDS[q], packed.data_ptr(), x.data_ptr(), 1, y.data_ptr(), 0, m, n, k, stream.cuda_stream)
+                assert lib.gsq_qmm(*args) == 0, lib.gsq_last_error()
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for _ in range(reps):
+                    lib.gsq_qmm(*args)
+                e1.record(stream)
+                torch.cuda.synchronize()
+                ms = e0.elapsed_time(e1) / reps
+                tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+                out[f"{q} {n}x{k} M={m}"] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1),
+                                              "frac": round(tf / FP16_PEAK_TFLOPS, 4)}
+                del x, y
+            del packed
+    m512 = [v["frac"] for kk, v in out.items() if kk.endswith("M=512")]
+    out["mean_frac_M512"] = round(sum(m512) / len(m512), 4)
+    return out
+
+
+# configs[3]/[4]: the mixed-type decoder layer (name, type, N, K)
+LAYER = (("q", "IQ2_XS", 5120, 5120), ("k", "IQ2_XS", 1024, 5120), ("v", "IQ4_XS", 1024, 5120),
+         ("o", "IQ3_S", 5120, 5120), ("gate", "IQ2_S", 17408, 5120), ("up", "IQ2_S", 17408, 5120),
+         ("down", "Q4_K", 5120, 17408))
+CROSS_ROWS = (1, 2, 4, 8, 16)
+
+
+def _time_launches(fn, stream, reps):
+    """Mean time of `reps` launches of fn (HIP events); None if the library refuses the call."""
+    import torch
+    if fn() != 0:
+        return None
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps * 1e3  # us
+
+
+def run_crossover(device, reps=20):
+    """per projection of the mixed layer and M in {1,2,4,8,16}, QMV vs QMM time (HIP
+    events, weights resident); the crossover is the smallest M at which QMM is faster."""
+    import torch
+    from mlx_gsq_amd import _lib
+    from mlx_gsq_amd.formats import TYPE_IDS
+    lib = _lib.lib()
+    stream = torch.cuda.current_stream(device)
+    sh = stream.cuda_stream
+    out = {}
+    for (name, q, n, k) in LAYER:
+        _lib.ensure_tables(q, device)
+        packed = make_device_packed(q, n, k, seed=300, device=device)
+        row = {}
+        for m in CROSS_ROWS:
             x = torch.randn(m, k, device=device).half()
             y = torch.empty(m, n, device=device, dtype=torch.float32)
-            args = (TYPE_IDS[q], packed.data_ptr(), x.data_ptr(), 1, y.data_ptr(), 0, m, n, k, stream.cuda_stream)
-            assert lib.gsq_qmm(*args) == 0, lib.gsq_last_error()
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            for _ in range(reps):
-                lib.gsq_qmm(*args)
-            e1.record(stream)
-            torch.cuda.synchronize()
-            ms = e0.elapsed_time(e1) / reps
-            tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-            out[f"{q} {n}x{k} M={m}"] = {"ms": round(ms, 3), "TFLOP/s": round(tf, 1),
-                                          "frac": round(tf / FP16_PEAK_TFLOPS, 4)}
-            del packed, x, y
-    return out
+            a = (TYPE_IDS[q], packed.data_ptr(), x.data_ptr(), 1, y.data_ptr(), 0, m, n, k, sh)
+            tv = _time_launches(lambda: lib.gsq_qmv(*a), stream, reps)
+            tm = _time_launches(lambda: lib.gsq_qmm(*a), stream, reps)
+            if tv is None:
+                from mlx_gsq_amd import _lib as L
+                note = L.lib().gsq_last_error().decode()
+            row[f"M={m}"] = {"qmv_us": None if tv is None else round(tv, 2), "qmm_us": round(tm, 2)}
+            if tv is None:
+                row[f"M={m}"]["qmv_refused"] = note
+        cross = next((m for m in CROSS_ROWS if row[f"M={m}"]["qmv_us"] is None
+                      or row[f"M={m}"]["qmm_us"] < row[f"M={m}"]["qmv_us"]), None)
+        out[f"{name} {q} {n}x{k}"] = {"rows": row, "qmm_faster_from_M": cross}
+        del packed
+    def best(r):  # the routed time: QMV where it runs and is faster, else QMM
+        return r["qmm_us"] if r["qmv_us"] is None else min(r["qmv_us"], r["qmm_us"])
+    totals = {f"M={m}": {"qmm_us": round(sum(v["rows"][f"M={m}"]["qmm_us"] for v in out.values()), 2),
+                         "best_us": round(sum(best(v["rows"][f"M={m}"]) for v in out.values()), 2)}
+              for m in CROSS_ROWS}
+    return {"per_projection": out, "layer_total": totals}
+
+
+def run_stack(device, layers=64, reps=10):
+    """one decode token of the 448 projection GEMVs (64 layers x the 7 projections of
+    the mixed layer, distinct random weights per layer, 8.34 GB resident) at M=1, captured in one
+    HIP graph and replayed; aggregate GB/s and implied linear-layer tokens/s."""
+    import torch
+    from mlx_gsq_amd import _lib
+    from mlx_gsq_amd.formats import TYPE_IDS
+    lib = _lib.lib()
+    stream = torch.cuda.current_stream(device)
+    mats, total = [], 0
+    xs = {k: torch.randn(1, k, device=device).half() for k in (5120, 17408)}
+    ys = {n: torch.empty(1, n, device=device, dtype=torch.float32) for n in (1024, 5120, 17408)}
+    for (_, q, _, _) in LAYER:
+        _lib.ensure_tables(q, device)
+    for layer in range(layers):
+        for (name, q, n, k) in LAYER:
+            p = make_device_packed(q, n, k, seed=5000 + len(mats), device=device)
+            mats.append((TYPE_IDS[q], p, n, k))
+            total += qmv_bytes(q, n, k)
+    torch.cuda.synchronize()
+
+    def step(sh):
+        for (tid, p, n, k) in mats:
+            rc = lib.gsq_qmv(tid, p.data_ptr(), xs[k].data_ptr(), 1, ys[n].data_ptr(), 0, 1, n, k, sh)
+            if rc:
+                raise RuntimeError(lib.gsq_last_error().decode())
+
+    step(stream.cuda_stream)
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream(device)
+    cap.wait_stream(stream)
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(graph, stream=cap):
+            step(torch.cuda.current_stream(device).cuda_stream)
+    stream.wait_stream(cap)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    gbs = total / (ms * 1e-3) / 1e9
+    res = {"gemvs": len(mats), "bytes": int(total), "ms_per_token": round(ms, 4), "GB/s": round(gbs, 1),
+           "frac": round(gbs / HBM_PEAK_GBS, 4), "linear_tokens_per_s": round(1e3 / ms, 1),
+           "mix": "per layer: q 5120x5120 IQ2_XS, k/v 1024x5120 IQ2_XS/IQ4_XS, o 5120x5120 IQ3_S, "
+                  "gate/up 17408x5120 IQ2_S, down 5120x17408 Q4_K"}
+    del mats
+    torch.cuda.empty_cache()
+    return res
+
+
+def qmm_profile_case(spec, reps, device):
+    """Launch one QMM product TYPE:MxNxK `reps` times (for rocprofv3 runs)."""
+    import torch
+    from mlx_gsq_amd import _lib, tables
+    from mlx_gsq_amd.formats import TYPE_IDS
+    q, shape = spec.split(":")
+    m, n, k = (int(v) for v in shape.split("x"))
+    tables.set_tables(tables.synthetic_tables(0))
+    _lib.ensure_tables(q, device)
+    lib = _lib.lib()
+    packed = make_device_packed(q, n, k, seed=77, device=device)
+    x = torch.randn(m, k, device=device).half()
+    y = torch.empty(m, n, device=device, dtype=torch.float32)
+    sh = torch.cuda.current_stream(device).cuda_stream
+    for _ in range(reps):
+        rc = lib.gsq_qmm(TYPE_IDS[q], packed.data_ptr(), x.data_ptr(), 1, y.data_ptr(), 0, m, n, k, sh)
+        assert rc == 0, lib.gsq_last_error()
+    torch.cuda.synchronize()
+    print(json.dumps({"qmm_profile_case": spec, "reps": reps, "flop_per_launch": 2 * m * n * k}), flush=True)
 
 
 def profile_case(spec, reps, device):
@@ -270,8 +419,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-qmm", action="store_true")
+    ap.add_argument("--no-layer", action="store_true", help="skip the mixed-layer crossover and 448-GEMV stack")
     ap.add_argument("--profile-case", default=None, help="TYPE:NxK, launch only that product")
     ap.add_argument("--copy-bytes", type=int, default=0, help="run only a plain copy of this many bytes")
+    ap.add_argument("--qmm-profile-case", default=None, help="TYPE:MxNxK, launch only that QMM product")
     ap.add_argument("--reps", type=int, default=20)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -287,8 +438,13 @@ def main():
     if args.profile_case:
         profile_case(args.profile_case, args.reps, device)
         return
+    if args.qmm_profile_case:
+        qmm_profile_case(args.qmm_profile_case, args.reps, device)
+        return
     qc, per_launch, eager_ms, graph_ms = run_qmv(args.steps, args.warmup, device)
     qmm = {} if args.no_qmm else run_qmm(device)
+    crossover = {} if args.no_layer else run_crossover(device)
+    stack = {} if args.no_layer else run_stack(device)
     cpu = None if args.no_cpu else cpu_baseline()
     from mlx_gsq_amd.formats import QTYPES
     step_bytes = qc.step_bytes()
@@ -326,6 +482,8 @@ def main():
         "per_type": per_type,
         "per_launch_us": launches,
         "qmm": qmm,
+        "layer_crossover": crossover,
+        "decode_stack": stack,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

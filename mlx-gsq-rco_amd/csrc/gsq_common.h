@@ -67,10 +67,10 @@ struct QmvTuning {
 };
 
 // Launch-plan overrides of the QMM kernel: activation tile height in 16-row blocks (0 = by
-// M) and the largest activation ring depth.
+// M) and the fewest K columns (256 wide) per workgroup (0 = default).
 struct QmmTuning {
   int mf;
-  int reserved;
+  int min_cols;
 };
 
 // Per-device QMM workspace, allocated once: fp32 partial tiles of workgroups that share an

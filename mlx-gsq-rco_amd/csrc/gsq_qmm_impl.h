@@ -631,7 +631,11 @@ static hipError_t launch_mfma(QmmMfmaArgs& a, int num_cus, const QmmWorkspace& w
   const long long units = (long long)a.mt * (((long long)a.N + kQBN - 1) / kQBN) * a.nblk;
   if (units >= (1ll << 31)) return hipErrorInvalidValue;
   a.units = (int)units;
-  a.G = num_cus < a.units ? num_cus : a.units;
+  // at least min_cols columns per workgroup: fewer workgroups share each tile when the
+  // problem is small, which bounds the partial-tile traffic
+  const int min_cols = g_qmm_tuning.min_cols > 0 ? g_qmm_tuning.min_cols : 2;
+  const int gmax = (a.units + min_cols - 1) / min_cols;
+  a.G = num_cus < gmax ? num_cus : gmax;
   if (a.G > ws.max_groups) a.G = ws.max_groups;
   a.xcd_remap = (a.G % 8 == 0) ? 1 : 0;
   a.part = ws.part;

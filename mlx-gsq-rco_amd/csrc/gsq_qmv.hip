@@ -932,7 +932,15 @@ static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, 
 // y[M, N] = x[M, K] W^T: activation rows go out in launches of up to 4 (2 for fp32/bf16).
 hipError_t launch_qmv(int qt, const uint8_t* packed, const void* x, int xdt, void* y, int ydt, int64_t M, int64_t N,
                       int K, const DevTables& tb, int num_cus, hipStream_t s) {
-  const int chunk = qmv_rows_per_launch(xdt);
+  // rows per launch: the widest variant whose waves per row (one per GL slices) fit a workgroup
+  int chunk = qmv_rows_per_launch(xdt);
+  const bool xs = xdt != DT_F16;
+  const int nslices = (K / 256 + 7) / 8;
+  auto fits = [&](int mr) {
+    const int gl = qmv_gl(mr, xs);
+    return (nslices + gl - 1) / gl <= qmv_max_threads(qmv_weight(mr, gl, xs)) / 64;
+  };
+  while (chunk > 1 && !fits(chunk)) chunk /= 2;
   const size_t xe = xdt == DT_F32 ? 4 : 2, ye = ydt == DT_F32 ? 4 : 2;
   for (int64_t r = 0; r < M; r += chunk) {
     const int mrow = (int)((M - r) < chunk ? (M - r) : chunk);

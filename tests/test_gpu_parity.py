@@ -104,6 +104,21 @@ def test_qmv_27b_row_widths(qtype, shape):
     assert rel_l2(y, want) <= 1e-4, rel_l2(y, want)
 
 
+@pytest.mark.parametrize("qtype", ["Q4_K", "IQ2_S", "IQ3_XXS"])
+@pytest.mark.parametrize("rows", [4, 7])
+def test_qmv_wide_rows_multi_row(qtype, rows):
+    """4..7 activation rows of the 17408-wide down projection: more waves per row than the
+    4-row variant holds, so the rows go out in 2-row launches."""
+    from mlx_gsq_amd.runtime.kernels.qmv import quantized_matvec
+    N, K = 160, 17408
+    packed = synth.make_packed(qtype, N, K, seed=12)
+    x = synth.make_x(rows, K, seed=13, dtype=np.float16)
+    y = quantized_matvec(dev(x), dev(packed), qtype=qtype, out_features=N, in_features=K,
+                         out_dtype=torch.float32).cpu().numpy()
+    want = O.matmul_reference(x, packed, qtype, N, K, TABLES.get(qtype))
+    assert rel_l2(y, want) <= 1e-4, rel_l2(y, want)
+
+
 def test_qmv_unaligned_packed_view_and_odd_rows():
     """A 2-byte (not 16-byte) aligned packed view and an odd N exercise the staged copy's edges."""
     from mlx_gsq_amd.runtime.kernels.qmv import quantized_matvec

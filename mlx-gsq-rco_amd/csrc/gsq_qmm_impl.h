@@ -290,7 +290,8 @@ __global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs args) {
   constexpr int LX = Plan::kLx;
   static_assert(Plan::kValid, "activation ring needs two stages");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int bid = blockIdx.x;
   const int w = xcd ? (bid & 7) * (G >> 3) + (bid >> 3) : bid;
   const int ub = qmm_first_col(w, units, G), ue = qmm_first_col(w + 1, units, G);

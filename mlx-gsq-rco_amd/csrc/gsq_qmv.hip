@@ -652,7 +652,10 @@ __global__ void __launch_bounds__(QmvBounds<qmv_weight(MR, GL, XS)>::v) qmv_kern
   using P = Qmv<T>;
   constexpr int BB = BlockBytes<T>::v;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+  // the wave index as a wave-uniform (scalar) value: everything derived from it (row slot,
+  // item count, DMA wait counts, loop bounds) then stays in scalar registers and branches
+  const int tid = threadIdx.x, lane = tid & 63, nw = blockDim.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   uint8_t* tbl = smem;
   uint8_t* xst = smem + a.x_off;
   float* red = reinterpret_cast<float*>(smem + a.red_off);   // [rows_per_wg][MR][W] (W > 1)

@@ -59,11 +59,12 @@ struct DevTables {
 };
 
 // Launch-plan parameters of the QMV kernel: waves per workgroup, target in-flight weight
-// bytes per CU, workgroups per CU.
+// bytes per CU, workgroups per CU, and whether rows of 2.5 wave slices may go in pairs.
 struct QmvTuning {
   int waves;
   int inflight_bytes;
   int wg_per_cu;
+  int pair;
 };
 
 // Launch-plan overrides of the QMM kernel: activation tile height in 16-row blocks (0 = by

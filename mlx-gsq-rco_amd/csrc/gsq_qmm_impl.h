@@ -98,17 +98,22 @@ struct QmmPlan {
 // The DMA schedule of one wave (per K32 stage q of Q): the table copy, then column 0 and
 // activation stages 0 .. min(LX-1, Q)-1; stage q issues activation stage q + LX - 1 (NX
 // instructions, while it exists) and, at a column start, the next column (GW instructions).
-// Stage q needs activation stage q and the column of stage q + 1. qmm_wait_n is the number of
-// this wave's instructions that may still be in flight at that point (vmcnt is in order).
+// Stage q needs the column of stage q + 1 and activation stage q + 1 when the ring has three
+// or more stages (the A operands are read one stage ahead), else activation stage q.
+// qmm_wait_n is the number of this wave's instructions that may still be in flight at that
+// point (vmcnt is in order).
 constexpr int qmm_issued_before(int q, int Q, int LX, int NX, int GW) {
   const int P = LX - 1 < Q ? LX - 1 : Q;
   const int x = q < Q - LX + 1 ? q : Q - LX + 1;
   const int cols = (q + 7) / 8 < Q / 8 - 1 ? (q + 7) / 8 : Q / 8 - 1;
   return GW + NX * P + NX * (x > 0 ? x : 0) + GW * cols;
 }
-constexpr int qmm_wait_n(int q, int Q, int LX, int NX, int GW) {
+constexpr int qmm_end_x(int k, int Q, int LX, int NX, int GW) {
   const int P = LX - 1 < Q ? LX - 1 : Q;
-  int need = q < P ? GW + NX * (q + 1) : qmm_issued_before(q - LX + 1, Q, LX, NX, GW) + NX;
+  return k < P ? GW + NX * (k + 1) : qmm_issued_before(k - LX + 1, Q, LX, NX, GW) + NX;
+}
+constexpr int qmm_wait_n(int q, int Q, int LX, int NX, int GW) {
+  int need = qmm_end_x(LX >= 3 && q + 1 < Q ? q + 1 : q, Q, LX, NX, GW);
   if (q + 1 < Q) {
     const int c = (q + 1) / 8;
     int ew = GW;
@@ -337,6 +342,9 @@ __global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs args) {
     return GW + NX * P + NX * max(0, min(q, Q - lx + 1)) + GW * min((q + 7) >> 3, ncols - 1);
   };
   auto end_x = [&](int k) { return k < P ? GW + NX * (k + 1) : issued_before(k - lx + 1) + NX; };
+  // A operands one stage ahead when the ring has a stage to spare: stage q reads stage q + 1's
+  // activations while its MFMAs run on the operands read during stage q - 1
+  constexpr bool PF = LX >= 3;
   auto end_w = [&](int c) {
     if (c == 0) return GW;
     const int qp = 8 * (c - 1);
@@ -367,6 +375,15 @@ __global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs args) {
   };
   // A operands of a stage: MF 16-row blocks (row l % 16, octet l / 16, swizzled)
   const int xoff = (lane & 15) * 64 + (((lane >> 4) ^ ((lane >> 2) & 3)) << 4);
+  auto load_a = [&](int slot, half8_t (&af)[MF]) {
+    const uint32_t* xb = reinterpret_cast<const uint32_t*>(xring + slot * (BM * 64) + xoff);
+#pragma unroll
+    for (int i = 0; i < MF; ++i) {
+      const uint32_t* p = xb + i * 256;
+      const uint32_t aw[4] = {p[0], p[1], p[2], p[3]};
+      af[i] = __builtin_bit_cast(half8_t, aw);
+    }
+  };
   int* bc = reinterpret_cast<int*>(lds + Plan::kBcOff);
 
   // prologue: table, column 0 and the first activation stages in flight; stage 0's weights
@@ -378,7 +395,9 @@ __global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs args) {
   col_delta(0, dl);
   half8_t bcur[4];
   decode(0, dl, bcur);
-  int rb = 0;  // ring slot of the stage being multiplied
+  half8_t acur[MF], anext[MF], bnext[4];
+  if constexpr (PF) load_a(0, acur);
+  int rb = PF ? 1 : 0;  // ring slot of the next activations read
 
   // one segment = this workgroup's columns of one tile; stage q multiplies its activations
   // with weights decoded during stage q - 1 and decodes the weights of stage q + 1
@@ -393,10 +412,14 @@ __global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs args) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = (float4_t){0.f, 0.f, 0.f, 0.f};
 
-    for (int q = q0; q < q1; ++q) {
+    // stage q: the operands (ua, ub_) were read and decoded during stage q - 1; this stage reads
+    // and decodes those of stage q + 1 into (na, nb). Two stages per iteration with the roles
+    // of the register sets swapped, so no operand is copied between stages.
+    auto stage = [&](int q, const half8_t (&ua)[MF], const half8_t (&ub_)[4], half8_t (&na)[MF],
+                     half8_t (&nb)[4]) __attribute__((always_inline)) {
       const int cl = q >> 3;
-      {  // stage q's activations and the column of stage q + 1 have landed (this wave's DMAs)
-        int need = end_x(q);
+      {  // the activations read now and the column of stage q + 1 have landed (this wave's DMAs)
+        int need = end_x(PF && q + 1 < Q ? q + 1 : q);
         if (q + 1 < Q) need = max(need, end_w((q + 1) >> 3));
         qmm_wait<LX, NX, GW>(issued_before(q) - need);
       }
@@ -404,29 +427,28 @@ __global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs args) {
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
       if (q + lx - 1 < Q) xi.issue(xring, wave, lane);
       if ((q & 7) == 0 && cl + 1 < ncols) issue_w(cl + 1);
-      half8_t af[MF];
-      {
-        const uint32_t* xb = reinterpret_cast<const uint32_t*>(xring + rb * (BM * 64) + xoff);
-#pragma unroll
-        for (int i = 0; i < MF; ++i) {
-          const uint32_t* p = xb + i * 256;
-          const uint32_t aw[4] = {p[0], p[1], p[2], p[3]};
-          af[i] = __builtin_bit_cast(half8_t, aw);
-        }
-      }
-      if (++rb == lx) rb = 0;
       // weights of stage q + 1 (after the last stage they come from stale, in-bounds LDS and
       // are not used): unconditional, in one scheduling region with the MFMAs
       if (((q + 1) & 7) == 0) col_delta(q + 1, dl);
-      half8_t bnext[4];
-      decode(q + 1, dl, bnext);
+      decode(q + 1, dl, nb);
+      // LDS reads stay in this order: the decode's table reads are waited for without waiting
+      // for the activation reads issued after them (LDS completes in order)
+      __builtin_amdgcn_sched_barrier(0x1 | 0x2 | 0x4 | 0x8);
+      // stage q + 1's activations (after the last stage: stale, in-bounds LDS, not used), or
+      // stage q's without the lookahead
+      load_a(rb, na);
+      if (++rb == lx) rb = 0;
 #pragma unroll
       for (int i = 0; i < MF; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bcur[j], acc[i][j], 0, 0, 0);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bcur[j] = bnext[j];
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(PF ? ua[i] : na[i], ub_[j], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);  // stages stay apart: two sets of operands at most
+    };
+    // a segment is whole columns: its stage count is a multiple of 8
+    for (int q = q0; q < q1; q += 2) {
+      stage(q, acur, bcur, anext, bnext);
+      stage(q + 1, anext, bnext, acur, bcur);
     }
 
     // end of this workgroup's part of `tile`

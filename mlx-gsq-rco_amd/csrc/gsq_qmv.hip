@@ -47,6 +47,7 @@ struct QmvArgs {
   int sbuf;         // bytes per ring buffer (cdma KB)
   int cdma;         // DMA instructions per item
   int tbl_bytes, x_off, x_bytes, x_lds, red_off, ring_off;  // LDS layout
+  int pair;         // rows go in pairs (see qmv_kernel)
   DevTables tb;
 };
 
@@ -209,24 +210,36 @@ template <> struct Qmv<Q6_K> {
   static constexpr int kPair = PAIR_K;
   static constexpr int kSums = 2;
   static constexpr int kTbl = 0;
+  // Group g = plane g % 4 of 128-weight chunk g / 4: weight e takes nibble plane / 2 of ql byte
+  // 64 chunk + 32 (plane % 2) + e and bits 2 plane of qh byte 128 + 32 chunk + e (k_decode.py:
+  // 51-64). Each word of 4 weights is one funnel shift out of the ql stream (nibble to bits
+  // 0-3 of every byte) and one out of the qh stream (2 bits to bits 4-5), which also absorbs
+  // the superblock's 2-byte alignment; the 6-bit codes then assemble bytewise and two byte
+  // permutes spread them into the fp16 code pairs (elements 0, 2 and 1, 3).
   template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t*, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
     const int chunk = g >> 2, plane = g & 3;
-    uint32_t ql[8], qh[8];
-    lds_words<8, A4>(buf, off + 64 * chunk + 32 * (plane & 1), ql);
-    lds_words<8, A4>(buf, off + 128 + 32 * chunk, qh);
+    const uint32_t lbit = 8u * (off + 64 * chunk + 32 * (plane & 1)) + 4u * (plane >> 1);
+    const uint32_t hbit = 8u * (off + 128 + 32 * chunk) + 2u * plane - 4u;  // bits 2 plane -> 4
+    const uint32_t* pl = reinterpret_cast<const uint32_t*>(buf + ((lbit >> 5) << 2));
+    const uint32_t* ph = reinterpret_cast<const uint32_t*>(buf + ((hbit >> 5) << 2));
+    const uint32_t nl = lbit & 31u, nh = hbit & 31u;
+    uint32_t wl[9], wh[9];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) { wl[i] = pl[i]; wh[i] = ph[i]; }
     const uint32_t sc2 = lds_u16(buf, off + 192 + 2 * g);
     const float d = h2f(lds_u16(buf, off + 208));
-    const uint32_t ls = 4u * (plane >> 1), hs = 2u * plane;
     float a0[MR], a1[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) { a0[m] = 0.f; a1[m] = 0.f; }
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const uint32_t L = ql[k] >> ls, H = qh[k] >> hs;
-      const uint32_t A = enc_codes<XS>((L & 0x000F000Fu) | ((H & 0x00030003u) << 4));
-      const uint32_t B = enc_codes<XS>(((L >> 8) & 0x000F000Fu) | (((H >> 8) & 0x00030003u) << 4));
+      const uint32_t L = __builtin_amdgcn_alignbit(wl[k + 1], wl[k], nl);
+      const uint32_t H = __builtin_amdgcn_alignbit(wh[k + 1], wh[k], nh);
+      const uint32_t C = (L & 0x0F0F0F0Fu) | (H & 0x30303030u);
+      const uint32_t A = enc_codes<XS>(__builtin_amdgcn_perm(0u, C, 0x0C020C00u));
+      const uint32_t B = enc_codes<XS>(__builtin_amdgcn_perm(0u, C, 0x0C030C01u));
       if (k < 4) { dacc<MR, XS>(A, x, 2 * k, a0); dacc<MR, XS>(B, x, 2 * k + 1, a0); }
       else { dacc<MR, XS>(A, x, 2 * k, a1); dacc<MR, XS>(B, x, 2 * k + 1, a1); }
     }
@@ -647,7 +660,12 @@ __device__ __forceinline__ void qmv_load_x1(XReg<MR, XS, Qmv<T>::kSums>& xr, boo
   }
 }
 
-template <int T, int MR, bool XS, int GL, bool A4>
+// PR2 (one fp16 activation row, K = 5120: 20 superblocks = 2.5 slices per row): an item is
+// two neighbouring rows A and B, decoded as five full slices per lane instead of 2 x 3 with
+// half of every third slice idle: slices 0 and 1 of A, slices 0 and 1 of B, and a shared
+// tail slice whose lanes 0-31 take A's last 4 superblocks and lanes 32-63 B's. Every row uses
+// the same activations, so the tail slice's activations are those of groups 128 + lane % 32.
+template <int T, int MR, bool XS, int GL, bool A4, bool PR2 = false>
 __global__ void __launch_bounds__(QmvBounds<qmv_weight(MR, GL, XS)>::v) qmv_kernel(QmvArgs a) {
   using P = Qmv<T>;
   constexpr int BB = BlockBytes<T>::v;
@@ -667,16 +685,18 @@ __global__ void __launch_bounds__(QmvBounds<qmv_weight(MR, GL, XS)>::v) qmv_kern
   // r0 + s, r0 + s + slots, ...: at any time the waves of a workgroup read neighbouring rows,
   // one contiguous span of the packed matrix.
   const int slot = wave / a.W, ws = wave - slot * a.W;
-  const bool live = slot < a.slots && r0 + slot < r1;
+  constexpr int RI = PR2 ? 2 : 1;  // rows per item
+  const int nrow_items = (int)((r1 - r0) / RI);
+  const bool live = slot < a.slots && slot < nrow_items;
   const int sl0 = ws * GL;
   const int nq = live ? max(0, min(GL, a.nslices - sl0)) : 0;
-  const int nbk = min(8 * GL, a.nblk - sl0 * 8);             // superblocks per item
-  const int item_bytes = nbk * BB;
-  const int nitems = nq > 0 ? (int)((r1 - r0 - slot + a.slots - 1) / a.slots) : 0;
-  // item t = K range of row r0 + slot + t * slots
-  const int64_t row0 = r0 + slot;
+  const int nbk = min(8 * GL, a.nblk - sl0 * 8);             // superblocks per item (per row)
+  const int item_bytes = PR2 ? 2 * a.row_bytes : nbk * BB;
+  const int nitems = nq > 0 ? (nrow_items - slot + a.slots - 1) / a.slots : 0;
+  // item t = K range of row(s) r0 + RI * (slot + t * slots)
+  const int64_t row0 = r0 + RI * slot;
   const uintptr_t base = reinterpret_cast<uintptr_t>(a.packed) + (uintptr_t)(row0 * a.row_bytes + (int64_t)sl0 * 8 * BB);
-  const uintptr_t stride = (uintptr_t)a.row_bytes * (uintptr_t)a.slots;
+  const uintptr_t stride = (uintptr_t)a.row_bytes * (uintptr_t)(RI * a.slots);
 
   // ---- prologue: table + activations (once per workgroup), then this wave's first items ----
   if constexpr (P::kTbl > 0) dma_copy(a.tb.qmv_tbl, P::kTbl, tbl, wave, nw, lane);
@@ -690,7 +710,7 @@ __global__ void __launch_bounds__(QmvBounds<qmv_weight(MR, GL, XS)>::v) qmv_kern
   XReg<MR, XS, P::kSums> xr[GL];
 #pragma unroll
   for (int q = 0; q < GL; ++q) {
-    const int u = (sl0 + q) * 64 + lane;
+    const int u = PR2 ? (q < 2 ? q * 64 + lane : 128 + (lane & 31)) : (sl0 + q) * 64 + lane;
     const bool act = q < nq && u < (a.K >> 5);
     if (a.x_lds) qmv_load_x1<T, MR, XS>(xr[q], act, act ? u : 0, xst, a.x_dtype, a.K, a.M);
     else qmv_load_x1<T, MR, XS>(xr[q], act, act ? u : 0, a.x, a.x_dtype, a.K, a.M);
@@ -705,9 +725,40 @@ __global__ void __launch_bounds__(QmvBounds<qmv_weight(MR, GL, XS)>::v) qmv_kern
       if (nbuf >= a.nb) nbuf -= a.nb;
       dma_item(base + (uintptr_t)(t + a.nb - 1) * stride, item_bytes, a.cdma, ring + nbuf * a.sbuf, lane);
     }
-    const int64_t row = row0 + (int64_t)t * a.slots;
+    const int64_t row = row0 + (int64_t)t * RI * a.slots;
     const uint32_t delta = (uint32_t)((base + (uintptr_t)t * stride) & 15u);
     const uint8_t* b = ring + buf * a.sbuf;
+    if constexpr (PR2) {
+      float accA[MR], accB[MR], pt[MR];
+#pragma unroll
+      for (int m = 0; m < MR; ++m) { accA[m] = 0.f; accB[m] = 0.f; pt[m] = 0.f; }
+      const uint32_t rb = (uint32_t)a.row_bytes;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const uint32_t off = delta + (uint32_t)((q * 8 + (lane >> 3)) * BB);
+        P::template dot<MR, XS, A4>(b, off, lane & 7, tbl, xr[q], accA);
+        P::template dot<MR, XS, A4>(b, off + rb, lane & 7, tbl, xr[q], accB);
+      }
+      const bool rowA = lane < 32;
+      P::template dot<MR, XS, A4>(b, delta + (rowA ? 0u : rb) + (uint32_t)((16 + ((lane & 31) >> 3)) * BB), lane & 7, tbl,
+                                  xr[2], pt);
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        accA[m] += rowA ? pt[m] : 0.f;
+        accB[m] += rowA ? 0.f : pt[m];
+      }
+      if (++buf == a.nb) buf = 0;
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        const float vA = wave_sum_to_lane63(accA[m]);
+        const float vB = wave_sum_to_lane63(accB[m]);
+        if (lane == 63 && m < a.M) {
+          store_y(a.y, a.y_dtype, (int64_t)m * a.N + row, vA);
+          store_y(a.y, a.y_dtype, (int64_t)m * a.N + row + 1, vB);
+        }
+      }
+      continue;
+    }
     float acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = 0.f;
@@ -751,9 +802,9 @@ __global__ void __launch_bounds__(QmvBounds<qmv_weight(MR, GL, XS)>::v) qmv_kern
   }
 }
 
-template <int T, int MR, bool XS, int GL, bool A4>
+template <int T, int MR, bool XS, int GL, bool A4, bool PR2 = false>
 static hipError_t launch_qmv_t(const QmvArgs& a, int grid, int threads, size_t lds, hipStream_t s) {
-  auto k = qmv_kernel<T, MR, XS, GL, A4>;
+  auto k = qmv_kernel<T, MR, XS, GL, A4, PR2>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
@@ -778,6 +829,7 @@ static int qmv_gl(int mr, bool xs) {
 template <int T, bool A4>
 static hipError_t launch_qmv_variant(const QmvArgs& a, int mr, bool xs, int grid, int threads, size_t lds,
                                      hipStream_t s) {
+  if (mr == 1 && !xs && a.pair) return launch_qmv_t<T, 1, false, 3, A4, true>(a, grid, threads, lds, s);
   if (mr == 1) return xs ? launch_qmv_t<T, 1, true, 1, A4>(a, grid, threads, lds, s) : launch_qmv_t<T, 1, false, 3, A4>(a, grid, threads, lds, s);
   if (mr == 2) return xs ? launch_qmv_t<T, 2, true, 1, A4>(a, grid, threads, lds, s) : launch_qmv_t<T, 2, false, 1, A4>(a, grid, threads, lds, s);
   if (mr == 4 && !xs) return launch_qmv_t<T, 4, false, 1, A4>(a, grid, threads, lds, s);
@@ -859,8 +911,8 @@ bool build_qmv_table(int qt, const uint16_t* grid16, const uint8_t* ksigns, std:
 static constexpr int kLdsBytes = 160 * 1024;
 
 // Launch-plan parameters: waves per workgroup, in-flight bytes per CU the ring depth aims
-// for, and workgroups per CU.
-QmvTuning g_qmv_tuning = {12, 96 * 1024, 1};
+// for, workgroups per CU, row pairing allowed.
+QmvTuning g_qmv_tuning = {12, 96 * 1024, 1, 1};
 
 // Activation rows per launch: up to 4 for fp16 activations, 2 for fp32/bf16.
 static int qmv_rows_per_launch(int xdt) { return xdt == DT_F16 ? 4 : 2; }
@@ -884,10 +936,6 @@ static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, 
   if (a.tbl_bytes > 0 && !tb.qmv_tbl) return hipErrorInvalidValue;
   const int lds_cap = kLdsBytes / wpc;
   a.x_bytes = M * K * (xdt == DT_F32 ? 4 : 2);
-  // item: GL slices of a row (+15 bytes of granule alignment, +4 of decoder over-read)
-  const int item_bytes = (a.nblk < 8 * gl ? a.nblk : 8 * gl) * bb;
-  a.cdma = (item_bytes + 19 + 1023) / 1024;
-  a.sbuf = a.cdma * 1024;
   // waves: as many as the variant allows (a multiple of W) unless the tuning asks for fewer
   int nw = g_qmv_tuning.waves < 1 ? 1 : g_qmv_tuning.waves;
   if (nw > max_waves) nw = max_waves;
@@ -898,7 +946,17 @@ static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, 
   int grid = num_cus * wpc;
   if (N < grid) grid = (int)N;
   a.rows_per_wg = (int)((N + grid - 1) / grid);
+  // rows in pairs where a row is 2.5 slices of one wave (one fp16 activation row, even N),
+  // once every row slot takes two or more pairs; whole pairs in every workgroup
+  a.pair = (g_qmv_tuning.pair && mr == 1 && !xs && a.nslices == gl && a.nblk == 8 * (gl - 1) + 4 &&
+            (N & 1) == 0 && a.rows_per_wg >= 4 * a.slots) ? 1 : 0;
+  if (a.pair && (a.rows_per_wg & 1)) ++a.rows_per_wg;
   grid = (int)((N + a.rows_per_wg - 1) / a.rows_per_wg);
+  // item: GL slices of a row, or a pair of rows (+15 bytes of granule alignment, +4 of decoder
+  // over-read)
+  const int item_bytes = a.pair ? 2 * a.row_bytes : (a.nblk < 8 * gl ? a.nblk : 8 * gl) * bb;
+  a.cdma = (item_bytes + 19 + 1023) / 1024;
+  a.sbuf = a.cdma * 1024;
   const int red_bytes = a.W > 1 ? ((a.rows_per_wg * mr * a.W * 4 + 15) & ~15) : 0;
   // activations go to LDS only if the ring keeps at least 3 items per wave
   a.x_lds = (a.tbl_bytes + a.x_bytes + red_bytes + nw * 3 * a.sbuf <= lds_cap) ? 1 : 0;
@@ -906,6 +964,12 @@ static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, 
   a.red_off = a.x_off + (a.x_lds ? a.x_bytes : 0);
   a.ring_off = a.red_off + red_bytes;
   int nb = (lds_cap - a.ring_off) / (nw * a.sbuf);
+  // large (paired) items: fewer waves rather than a ring of one buffer
+  while (nb < 2 && nw > a.W) {
+    nw -= a.W;
+    a.slots = nw / a.W;
+    nb = (lds_cap - a.ring_off) / (nw * a.sbuf);
+  }
   // in-flight target per CU: nw * (nb - 1) items
   const int want = 1 + (g_qmv_tuning.inflight_bytes * wpc / (item_bytes > 0 ? item_bytes : 1) + nw - 1) / nw;
   if (nb > want) nb = want;

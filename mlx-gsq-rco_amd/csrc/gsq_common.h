@@ -68,10 +68,12 @@ struct QmvTuning {
 };
 
 // Launch-plan overrides of the QMM kernel: activation tile height in 16-row blocks (0 = by
-// M) and the fewest K columns (256 wide) per workgroup (0 = default).
+// M), the fewest K columns (256 wide) per workgroup (0 = default) and waves per workgroup for
+// tiles of 128 or 256 rows (4, or 0 = 8).
 struct QmmTuning {
   int mf;
   int min_cols;
+  int waves;
 };
 
 // Per-device QMM workspace, allocated once: fp32 partial tiles of workgroups that share an

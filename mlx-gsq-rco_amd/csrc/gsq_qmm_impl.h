@@ -49,21 +49,27 @@ __device__ __forceinline__ void qmm_store_y(void* y, int dt, int64_t i, float v)
 }
 
 // ---- MFMA kernel ----------------------------------------------------------------------
-constexpr int kQWaves = 4;                  // waves per workgroup
-constexpr int kQWRows = 64;                 // weight rows per wave
-constexpr int kQBN = kQWaves * kQWRows;     // weight rows per tile
+constexpr int kQBN = 256;                   // weight rows per tile
 constexpr int kQLds = 160 * 1024;
 constexpr int kQSlotFloats = 256 * kQBN;    // one partial-sum slot (BM <= 256)
 
-template <int T>
+// WV waves per workgroup (4: one per SIMD, or 8: two per SIMD), each owning kQBN / WV weight
+// rows of the tile.
+template <int T, int WV>
 struct QmmGeo {
   static constexpr int kBB = BlockBytes<T>::v;
-  // granules per row slot (= DMA instructions per column): enough for a superblock at any
-  // 2-byte offset within its first granule, rounded up to an odd count so that the sixteen
-  // rows a wave reads at once fall into distinct LDS bank groups
-  static constexpr int kGran = ((kBB + 15) / 16 + 1) | 1;
+  static constexpr int kRows = kQBN / WV;  // weight rows per wave
+  static constexpr int kNB = kRows / 16;   // 16-row B blocks per wave
+  // granules per row slot: enough for a superblock at any 2-byte offset (up to 14) within its
+  // first granule, rounded up to an odd count so that the sixteen rows a wave reads at once
+  // fall into distinct LDS bank groups (except Q6_K with 8 waves, whose rings would otherwise
+  // leave no room for two activation stages of 256 rows)
+  static constexpr int kNeed = (kBB + 14 + 15) / 16;
+  static constexpr int kGran = (T == Q6_K && WV == 8) ? kNeed : (kNeed | 1);
   static constexpr int kSlot = kGran * 16;
-  static constexpr int kRing = 2 * kQWRows * kSlot;  // per wave: two columns
+  static constexpr int kGW = (kRows * kGran + 63) / 64;  // DMA instructions per column per wave
+  static constexpr int kCol = kGW * 1024;                // one column of the wave's ring
+  static constexpr int kRing = 2 * kCol;                 // per wave: two columns
 };
 
 // Byte size of a type's LDS table image (the QMV kernel's image: fp16 codebook followed by
@@ -79,20 +85,20 @@ constexpr int qmm_tbl_bytes() {
                                  : 0;
 }
 
-// LDS plan of (type, activation tile height MF x 16 rows): table image, activation ring of
-// kLx K32 stages (as deep as the LDS left over allows, up to 8), the four waves' weight rings
-// and a small broadcast slot.
-template <int T, int MF>
+// LDS plan of (type, activation tile height MF x 16 rows, waves): table image, activation ring
+// of kLx K32 stages (as deep as the LDS left over allows, up to 8), the waves' weight rings and
+// a small broadcast slot.
+template <int T, int MF, int WV>
 struct QmmPlan {
   static constexpr int kTbl = qmm_tbl_bytes<T>();
-  static constexpr int kW = kQWaves * QmmGeo<T>::kRing;
+  static constexpr int kW = WV * QmmGeo<T, WV>::kRing;
   static constexpr int kLx0 = (kQLds - kTbl - kW - 32) / (16 * MF * 64);
   static constexpr int kLx = kLx0 > 8 ? 8 : kLx0;
   static constexpr int kXOff = kTbl;
   static constexpr int kWOff = kXOff + kLx * 16 * MF * 64;
   static constexpr int kBcOff = kWOff + kW;
   static constexpr int kLds = kBcOff + 32;
-  static constexpr bool kValid = kLx >= 2;
+  static constexpr bool kValid = kLx >= 2 && MF >= WV;  // every wave issues activation DMA
 };
 
 // The DMA schedule of one wave (per K32 stage q of Q): the table copy, then column 0 and
@@ -212,13 +218,13 @@ __device__ __forceinline__ int qmm_first_col(int w, int units, int G) {
   return (int)((long long)w * units / G);
 }
 
-template <int MF>
-__device__ __forceinline__ void qmm_store_tile(void* y, int ydt, int M, int N, const float4_t (&acc)[MF][4], int m0,
+template <int MF, int NB>
+__device__ __forceinline__ void qmm_store_tile(void* y, int ydt, int M, int N, const float4_t (&acc)[MF][NB], int m0,
                                                int n0, int lane) {
 #pragma unroll
   for (int i = 0; i < MF; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NB; ++j) {
       const int n = n0 + 16 * j + (lane & 15);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -275,8 +281,8 @@ struct QmmXIter {
   }
 };
 
-template <int T, int MF, bool A4>
-__global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs args) {
+template <int T, int MF, bool A4, int WV>
+__global__ void __launch_bounds__(64 * WV, 1) qmm_mfma_kernel(QmmMfmaArgs args) {
   // the arguments as plain values (no reference to the argument block escapes, so it is never
   // copied to scratch memory, whose loads would wait on the DMA counter)
   const uint8_t* const packed = args.packed;
@@ -288,10 +294,11 @@ __global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs args) {
   const uint8_t* const tblg = args.tbl;
   float* const part = args.part;
   int* const cnt = args.cnt;
-  using Geo = QmmGeo<T>;
-  constexpr int BB = Geo::kBB, GW = Geo::kGran, S = Geo::kSlot;
-  constexpr int BM = 16 * MF, NX = MF / 4;  // NX: activation DMA instructions per wave per stage
-  using Plan = QmmPlan<T, MF>;
+  using Geo = QmmGeo<T, WV>;
+  constexpr int BB = Geo::kBB, GW = Geo::kGW, GR = Geo::kGran, S = Geo::kSlot;
+  constexpr int RW = Geo::kRows, NB = Geo::kNB, TH = 64 * WV;
+  constexpr int BM = 16 * MF, NX = MF / WV;  // NX: activation DMA instructions per wave per stage
+  using Plan = QmmPlan<T, MF, WV>;
   constexpr int LX = Plan::kLx;
   static_assert(Plan::kValid, "activation ring needs two stages");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -308,23 +315,24 @@ __global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs args) {
   const uint8_t* tbl = lds;
 
   // the type's table image first in this wave's DMA order: the first wait covers it
-  if (tbl_bytes) dma_copy(tblg, tbl_bytes, lds, wave, kQWaves, lane);
+  if (tbl_bytes) dma_copy(tblg, tbl_bytes, lds, wave, WV, lane);
 
   // activation stages are issued in order by an iterator
   QmmXIter<NX, BM, LX> xi;
   xi.init(xg, M, K, mt, nblk, ub, wave, lane);
-  // weight column cl (local index): the wave's 64 superblocks, granule e of the column at
-  // slot byte 16e (row e / GW, granule e % GW of that row); granules past a row's last one
-  // reload its last granule so every lane stays active and the count stays fixed
+  // weight column cl (local index): the wave's RW superblocks, granule e of the column at
+  // byte 16e (row e / GR, granule e % GR of that row); granules past a row's last one reload
+  // its last granule, and lanes past the last row (whole instructions) reload the last row's,
+  // so every lane stays active and the count stays fixed
   auto issue_w = [&](int cl) {
     const int u = ub + cl;
     const int tile = u / nblk, c = u - tile * nblk;
-    const int n0 = (tile / mt) * kQBN + wave * kQWRows;
-    uint8_t* buf = wring + (cl & 1) * (kQWRows * S);
+    const int n0 = (tile / mt) * kQBN + wave * RW;
+    uint8_t* buf = wring + (cl & 1) * Geo::kCol;
 #pragma unroll
     for (int i = 0; i < GW; ++i) {
       const int e = i * 64 + lane;
-      const int r = e / GW, qg = e - r * GW;
+      const int r = min(e / GR, RW - 1), qg = e - (e / GR) * GR;
       const int n = min(n0 + r, N - 1);
       const uintptr_t p = reinterpret_cast<uintptr_t>(packed) + (uintptr_t)((long long)n * row_bytes) +
                           (uintptr_t)c * BB;
@@ -344,7 +352,7 @@ __global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs args) {
   auto end_x = [&](int k) { return k < P ? GW + NX * (k + 1) : issued_before(k - lx + 1) + NX; };
   // A operands one stage ahead when the ring has a stage to spare: stage q reads stage q + 1's
   // activations while its MFMAs run on the operands read during stage q - 1
-  constexpr bool PF = LX >= 3;
+  constexpr bool PF = LX >= 3 && WV == 4;
   auto end_w = [&](int c) {
     if (c == 0) return GW;
     const int qp = 8 * (c - 1);
@@ -353,21 +361,21 @@ __global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs args) {
 
   // B operands of stage q: the four 16-row blocks of the wave's weight rows, group q % 8 of
   // column q / 8; dl = the low address bits of the lane's four superblocks in that column
-  auto decode = [&](int q, const uint32_t (&dl)[4], half8_t (&bf)[4]) {
-    const uint8_t* wb = wring + ((q >> 3) & 1) * (kQWRows * S);
+  auto decode = [&](int q, const uint32_t (&dl)[NB], half8_t (&bf)[NB]) {
+    const uint8_t* wb = wring + ((q >> 3) & 1) * Geo::kCol;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NB; ++j) {
       uint32_t o[4];
       QmmDec<T, A4>::run(wb + (16 * j + (lane & 15)) * S + dl[j], tbl, q & 7, lane >> 4, o);
       bf[j] = __builtin_bit_cast(half8_t, o);
     }
   };
-  auto col_delta = [&](int q, uint32_t (&dl)[4]) {
+  auto col_delta = [&](int q, uint32_t (&dl)[NB]) {
     const int u = ub + (q >> 3);
     const int tl = u / nblk, c = u - tl * nblk;
-    const int n0 = (tl / mt) * kQBN + wave * kQWRows;
+    const int n0 = (tl / mt) * kQBN + wave * RW;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NB; ++j) {
       const int n = min(n0 + 16 * j + (lane & 15), N - 1);
       dl[j] = (uint32_t)((reinterpret_cast<uintptr_t>(packed) + (uintptr_t)((long long)n * row_bytes) +
                           (uintptr_t)c * BB) & 15u);
@@ -391,11 +399,11 @@ __global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs args) {
   for (int q = 0; q < P; ++q) xi.issue(xring, wave, lane);
   qmm_wait<LX, NX, GW>(NX * (P - 1));  // table, column 0 and stage 0 (this wave's share)
   __syncthreads();
-  uint32_t dl[4];
+  uint32_t dl[NB];
   col_delta(0, dl);
-  half8_t bcur[4];
+  half8_t bcur[NB];
   decode(0, dl, bcur);
-  half8_t acur[MF], anext[MF], bnext[4];
+  half8_t acur[MF], anext[MF], bnext[NB];
   if constexpr (PF) load_a(0, acur);
   int rb = PF ? 1 : 0;  // ring slot of the next activations read
 
@@ -405,18 +413,18 @@ __global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs args) {
     const int u0 = ub + (q0 >> 3);
     const int tile = u0 / nblk;
     const int q1 = q0 + 8 * (min(ue, (tile + 1) * nblk) - u0);
-    const int m0 = (tile % mt) * BM, n0 = (tile / mt) * kQBN + wave * kQWRows;
-    float4_t acc[MF][4];
+    const int m0 = (tile % mt) * BM, n0 = (tile / mt) * kQBN + wave * RW;
+    float4_t acc[MF][NB];
 #pragma unroll
     for (int i = 0; i < MF; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = (float4_t){0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < NB; ++j) acc[i][j] = (float4_t){0.f, 0.f, 0.f, 0.f};
 
     // stage q: the operands (ua, ub_) were read and decoded during stage q - 1; this stage reads
     // and decodes those of stage q + 1 into (na, nb). Two stages per iteration with the roles
     // of the register sets swapped, so no operand is copied between stages.
-    auto stage = [&](int q, const half8_t (&ua)[MF], const half8_t (&ub_)[4], half8_t (&na)[MF],
-                     half8_t (&nb)[4]) __attribute__((always_inline)) {
+    auto stage = [&](int q, const half8_t (&ua)[MF], const half8_t (&ub_)[NB], half8_t (&na)[MF],
+                     half8_t (&nb)[NB]) __attribute__((always_inline)) {
       const int cl = q >> 3;
       {  // the activations read now and the column of stage q + 1 have landed (this wave's DMAs)
         int need = end_x(PF && q + 1 < Q ? q + 1 : q);
@@ -441,7 +449,7 @@ __global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs args) {
 #pragma unroll
       for (int i = 0; i < MF; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NB; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(PF ? ua[i] : na[i], ub_[j], acc[i][j], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);  // stages stay apart: two sets of operands at most
     };
@@ -455,7 +463,7 @@ __global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs args) {
     const int wf = qmm_owner(tile * nblk, units, G);
     const int wl = qmm_owner(tile * nblk + nblk - 1, units, G);
     if (wf == wl) {
-      qmm_store_tile<MF>(yg, ydt, M, N, acc, m0, n0, lane);
+      qmm_store_tile<MF, NB>(yg, ydt, M, N, acc, m0, n0, lane);
     } else {
       // slot 2w: the tile this workgroup starts in; slot 2w + 1: the tile it ends in
       const int slot = 2 * w + (q0 == 0 ? 0 : 1);
@@ -464,7 +472,7 @@ __global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs args) {
 #pragma unroll
       for (int i = 0; i < MF; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) qmm_st_coherent(ps, ((i * 4 + j) * 256 + tid) * 16, acc[i][j]);
+        for (int j = 0; j < NB; ++j) qmm_st_coherent(ps, ((i * NB + j) * TH + tid) * 16, acc[i][j]);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       if (tid == 0) bc[0] = __hip_atomic_fetch_add(&cnt[wf], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -474,7 +482,7 @@ __global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs args) {
         const int mb = m0 + 4 * (lane >> 4), nb = n0 + (lane & 15);
         constexpr int CH = 8;  // output blocks per batch of loads
 #pragma unroll 1
-        for (int ij0 = 0; ij0 < MF * 4; ij0 += CH) {
+        for (int ij0 = 0; ij0 < MF * NB; ij0 += CH) {
           float4_t sum[CH];
 #pragma unroll
           for (int t = 0; t < CH; ++t) sum[t] = (float4_t){0.f, 0.f, 0.f, 0.f};
@@ -483,17 +491,17 @@ __global__ void __launch_bounds__(256, 1) qmm_mfma_kernel(QmmMfmaArgs args) {
             const __amdgpu_buffer_rsrc_t pv = qmm_slot_rsrc(part, vs);
             float4_t ld[CH];
 #pragma unroll
-            for (int t = 0; t < CH; ++t) ld[t] = qmm_ld_coherent(pv, ((ij0 + t) * 256 + tid) * 16);
+            for (int t = 0; t < CH; ++t) ld[t] = qmm_ld_coherent(pv, ((ij0 + t) * TH + tid) * 16);
 #pragma unroll
             for (int t = 0; t < CH; ++t) sum[t] += ld[t];
           }
 #pragma unroll
           for (int t = 0; t < CH; ++t) {
             const int ij = ij0 + t;
-            const int n = nb + 16 * (ij & 3);
+            const int n = nb + 16 * (ij % NB);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              const int m = mb + 16 * (ij >> 2) + e;
+              const int m = mb + 16 * (ij / NB) + e;
               if (m < M && n < N) qmm_store_y(yg, ydt, (int64_t)m * N + n, sum[t][e]);
             }
           }
@@ -614,40 +622,48 @@ static bool qmm_grid_type(int qt) {
   return qt == IQ1_S || qt == IQ1_M || qt == IQ2_XXS || qt == IQ2_XS || qt == IQ2_S || qt == IQ3_XXS || qt == IQ3_S;
 }
 
-template <int T, int MF, bool A4>
+template <int T, int MF, bool A4, int WV>
 static hipError_t launch_mfma_t(const QmmMfmaArgs& a, hipStream_t s) {
-  if constexpr (!QmmPlan<T, MF>::kValid) {
+  if constexpr (!QmmPlan<T, MF, WV>::kValid) {
     return hipErrorInvalidValue;
   } else {
-    auto k = qmm_mfma_kernel<T, MF, A4>;
+    auto k = qmm_mfma_kernel<T, MF, A4, WV>;
     static bool attr_set = false;
     if (!attr_set) {
       hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, kQLds);
       if (e != hipSuccess) return e;
       attr_set = true;
     }
-    constexpr size_t lds = QmmPlan<T, MF>::kLds;
-    hipLaunchKernelGGL(k, dim3(a.G), dim3(256), lds, s, a);
+    constexpr size_t lds = QmmPlan<T, MF, WV>::kLds;
+    hipLaunchKernelGGL(k, dim3(a.G), dim3(64 * WV), lds, s, a);
     return hipGetLastError();
   }
 }
 
-template <int T, int MF>
-static hipError_t launch_mfma_mf(const QmmMfmaArgs& a, bool a4, hipStream_t s) {
+template <int T, int MF, int WV>
+static hipError_t launch_mfma_a4(const QmmMfmaArgs& a, bool a4, hipStream_t s) {
   if constexpr (BlockBytes<T>::v % 4 == 0) {
-    if (a4) return launch_mfma_t<T, MF, true>(a, s);
+    if (a4) return launch_mfma_t<T, MF, true, WV>(a, s);
   }
-  return launch_mfma_t<T, MF, false>(a, s);
+  return launch_mfma_t<T, MF, false, WV>(a, s);
+}
+// 8 waves where the tile allows it (and the tuning does not ask for 4), else 4
+template <int T, int MF>
+static hipError_t launch_mfma_mf(const QmmMfmaArgs& a, bool a4, bool w8, hipStream_t s) {
+  if constexpr (QmmPlan<T, MF, 8>::kValid) {
+    if (w8) return launch_mfma_a4<T, MF, 8>(a, a4, s);
+  }
+  return launch_mfma_a4<T, MF, 4>(a, a4, s);
 }
 
 // Plan and launch the MFMA kernel for type T: activation tile height (MF 16-row blocks) from M
-// (64 rows up to 64, 128 up to 192, else 256), then the stream-K grid:
+// (64 rows up to 64, 128 up to 128, else 256), then the stream-K grid:
 // one workgroup per CU, at most one per (tile, K column) unit.
 template <int T>
 static hipError_t launch_mfma(QmmMfmaArgs& a, int num_cus, const QmmWorkspace& ws, hipStream_t s) {
-  if (a.tbl_bytes != QmmPlan<T, 4>::kTbl) return hipErrorInvalidValue;
+  if (a.tbl_bytes != qmm_tbl_bytes<T>()) return hipErrorInvalidValue;
   int mf = g_qmm_tuning.mf;
-  if (mf == 0) mf = a.M <= 64 ? 4 : (a.M <= 192 ? 8 : 16);
+  if (mf == 0) mf = a.M <= 64 ? 4 : (a.M <= 128 ? 8 : 16);
   if (mf != 4 && mf != 8 && mf != 16) return hipErrorInvalidValue;
   const int bm = 16 * mf;
   a.mt = (a.M + bm - 1) / bm;
@@ -664,10 +680,11 @@ static hipError_t launch_mfma(QmmMfmaArgs& a, int num_cus, const QmmWorkspace& w
   a.part = ws.part;
   a.cnt = ws.cnt;
   const bool a4 = (reinterpret_cast<uintptr_t>(a.packed) & 3) == 0;
+  const bool w8 = g_qmm_tuning.waves != 4;
   switch (mf) {
-    case 4: return launch_mfma_mf<T, 4>(a, a4, s);
-    case 8: return launch_mfma_mf<T, 8>(a, a4, s);
-    default: return launch_mfma_mf<T, 16>(a, a4, s);
+    case 4: return launch_mfma_mf<T, 4>(a, a4, w8, s);
+    case 8: return launch_mfma_mf<T, 8>(a, a4, w8, s);
+    default: return launch_mfma_mf<T, 16>(a, a4, w8, s);
   }
 }
 

@@ -146,8 +146,8 @@ struct QmmDec<IQ4_XS, A4> {
   }
 };
 
-// IQ3_S (iq3_s_decode.py:16-40): w = +-d*(1+2*s)*grid[gi][c], 9-bit grid index; sign masks
-// per nibble (two pairs) after the codebook
+// IQ3_S (iq3_s_decode.py:16-40): w = +-d*(1+2*s)*grid[gi][c], 9-bit grid index; one byte
+// sign mask (eight signs, four words) per two entries, after the codebook
 template <bool A4>
 struct QmmDec<IQ3_S, A4> {
   static constexpr uint32_t kGridB = 512 * 4 * 2;
@@ -162,12 +162,11 @@ struct QmmDec<IQ3_S, A4> {
     const uint32_t signs = lds_u8(sb, 74 + 4 * g + kq);
     const uint32_t* e0 = tbl_words(tbl, i0 * 8);
     const uint32_t* e1 = tbl_words(tbl, i1 * 8);
-    const uint32_t* m0 = tbl_words(tbl, kGridB + (signs & 15u) * 8);
-    const uint32_t* m1 = tbl_words(tbl, kGridB + (signs >> 4) * 8);
-    o[0] = mix2(db, e0[0], 0.f) ^ m0[0];
-    o[1] = mix2(db, e0[1], 0.f) ^ m0[1];
-    o[2] = mix2(db, e1[0], 0.f) ^ m1[0];
-    o[3] = mix2(db, e1[1], 0.f) ^ m1[1];
+    const uint32_t* m = tbl_words(tbl, kGridB + signs * 16);  // byte mask: 8 signs
+    o[0] = mix2(db, e0[0], 0.f) ^ m[0];
+    o[1] = mix2(db, e0[1], 0.f) ^ m[1];
+    o[2] = mix2(db, e1[0], 0.f) ^ m[2];
+    o[3] = mix2(db, e1[1], 0.f) ^ m[3];
   }
 };
 

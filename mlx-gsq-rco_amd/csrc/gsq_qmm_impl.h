@@ -81,7 +81,7 @@ constexpr int qmm_tbl_bytes() {
        : T == IQ2_XS             ? 512 * 8 * 2 + 128 * 16
        : T == IQ2_S              ? 1024 * 8 * 2 + 256 * 16
        : T == IQ3_XXS            ? 256 * 4 * 2 + 128 * 16
-       : T == IQ3_S              ? 512 * 4 * 2 + 16 * 8
+       : T == IQ3_S              ? 512 * 4 * 2 + 256 * 16
                                  : 0;
 }
 
@@ -281,6 +281,19 @@ struct QmmXIter {
   }
 };
 
+// The type's table image in static LDS (LDS address 0).
+template <int B>
+struct QmmTblLds {
+  __device__ __forceinline__ static uint8_t* get() {
+    __shared__ __attribute__((aligned(16))) uint8_t t[B];
+    return t;
+  }
+};
+template <>
+struct QmmTblLds<0> {
+  __device__ __forceinline__ static uint8_t* get() { return nullptr; }
+};
+
 template <int T, int MF, bool A4, int WV>
 __global__ void __launch_bounds__(64 * WV, 1) qmm_mfma_kernel(QmmMfmaArgs args) {
   // the arguments as plain values (no reference to the argument block escapes, so it is never
@@ -310,12 +323,16 @@ __global__ void __launch_bounds__(64 * WV, 1) qmm_mfma_kernel(QmmMfmaArgs args) 
   const int ncols = ue - ub;  // >= 1: G <= units
   const int Q = 8 * ncols;    // K32 stages of this workgroup
   constexpr int lx = LX;
-  uint8_t* xring = lds + Plan::kXOff;
-  uint8_t* wring = lds + Plan::kWOff + wave * Geo::kRing;
-  const uint8_t* tbl = lds;
+  // the table image is static LDS at address 0 (its reads fold the base into their address
+  // arithmetic); the plan's other offsets count from the table's start, where dynamic LDS
+  // begins after the table
+  uint8_t* dyn = lds - Plan::kTbl;
+  uint8_t* xring = dyn + Plan::kXOff;
+  uint8_t* wring = dyn + Plan::kWOff + wave * Geo::kRing;
+  uint8_t* tbl = QmmTblLds<Plan::kTbl>::get();
 
   // the type's table image first in this wave's DMA order: the first wait covers it
-  if (tbl_bytes) dma_copy(tblg, tbl_bytes, lds, wave, WV, lane);
+  if (tbl_bytes) dma_copy(tblg, tbl_bytes, tbl, wave, WV, lane);
 
   // activation stages are issued in order by an iterator
   QmmXIter<NX, BM, LX> xi;
@@ -392,7 +409,7 @@ __global__ void __launch_bounds__(64 * WV, 1) qmm_mfma_kernel(QmmMfmaArgs args) 
       af[i] = __builtin_bit_cast(half8_t, aw);
     }
   };
-  int* bc = reinterpret_cast<int*>(lds + Plan::kBcOff);
+  int* bc = reinterpret_cast<int*>(dyn + Plan::kBcOff);
 
   // prologue: table, column 0 and the first activation stages in flight; stage 0's weights
   issue_w(0);
@@ -630,11 +647,12 @@ static hipError_t launch_mfma_t(const QmmMfmaArgs& a, hipStream_t s) {
     auto k = qmm_mfma_kernel<T, MF, A4, WV>;
     static bool attr_set = false;
     if (!attr_set) {
-      hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, kQLds);
+      hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         kQLds - QmmPlan<T, MF, WV>::kTbl);
       if (e != hipSuccess) return e;
       attr_set = true;
     }
-    constexpr size_t lds = QmmPlan<T, MF, WV>::kLds;
+    constexpr size_t lds = QmmPlan<T, MF, WV>::kLds - QmmPlan<T, MF, WV>::kTbl;  // dynamic part
     hipLaunchKernelGGL(k, dim3(a.G), dim3(64 * WV), lds, s, a);
     return hipGetLastError();
   }

@@ -269,11 +269,13 @@ template <> struct Qmv<IQ4_XS> {
     float acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = 0.f;
+    uint32_t v[16];  // all sixteen value-pair reads of the group in flight before the first use
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < 4; ++k)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dacc<MR, XS>(t[(q[k] >> (8 * i)) & 255u], x, 4 * k + i, acc);
-    }
+      for (int i = 0; i < 4; ++i) v[4 * k + i] = t[bfe(q[k], 8 * i, 8)];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) dacc<MR, XS>(v[j], x, j, acc);
     const float s = d * (float)scale;
 #pragma unroll
     for (int m = 0; m < MR; ++m) out[m] += s * acc[m];
@@ -284,7 +286,7 @@ template <> struct Qmv<IQ3_S> {
   static constexpr int kPair = PAIR_NAT;
   static constexpr int kSums = 0;
   static constexpr int kGridB = 512 * 4 * 2;
-  static constexpr int kTbl = kGridB + 16 * 8;  // grid + 16 nibble sign masks
+  static constexpr int kTbl = kGridB + 256 * 16;  // grid + 256 byte sign masks
   template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
@@ -296,17 +298,22 @@ template <> struct Qmv<IQ3_S> {
     const uint32_t qh = lds_u8(buf, off + 66 + g);
     const uint32_t sg = lds_w32<A4>(buf, off + 74 + 4 * g);
     const LdsV2 grid{tbl};
-    const LdsV2 sm{tbl + kGridB};
+    const LdsV4 bm{tbl + kGridB};
     float acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = 0.f;
+    uint4 Ms[4];
+    uint2 Gs[8];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) Ms[p] = bm[bfe(sg, 8 * p, 8)];  // sign byte of entries 2p, 2p + 1
+#pragma unroll
+    for (int e = 0; e < 8; ++e) Gs[e] = grid[bfe(q[e >> 2], 8 * (e & 3), 8) | (bfe(qh, e, 1) << 8)];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const uint32_t idx = ((q[e >> 2] >> (8 * (e & 3))) & 255u) | (((qh >> e) & 1u) << 8);
-      uint2 G = grid[idx];
-      const uint2 M = sm[(sg >> (4 * e)) & 15u];
-      dacc<MR, XS>(G.x ^ M.x, x, 2 * e, acc);
-      dacc<MR, XS>(G.y ^ M.y, x, 2 * e + 1, acc);
+      const uint4 M = Ms[e >> 1];
+      const bool h = e & 1;
+      dacc<MR, XS>(Gs[e].x ^ (h ? M.z : M.x), x, 2 * e, acc);
+      dacc<MR, XS>(Gs[e].y ^ (h ? M.w : M.y), x, 2 * e + 1, acc);
     }
 #pragma unroll
     for (int m = 0; m < MR; ++m) out[m] += db * acc[m];
@@ -331,15 +338,20 @@ template <> struct Qmv<IQ3_XXS> {
     float acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = 0.f;
+    uint4 M[4];
+    uint2 G0[4], G1[4];
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {  // all table reads of the group in flight before the first use
+      M[l] = km[bfe(u, 7 * l, 7)];
+      G0[l] = grid[bfe(q[l >> 1], 16 * (l & 1), 8)];
+      G1[l] = grid[bfe(q[l >> 1], 16 * (l & 1) + 8, 8)];
+    }
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
-      const uint4 M = km[(u >> (7 * l)) & 127u];
-      const uint2 G0 = grid[(q[l >> 1] >> (16 * (l & 1))) & 255u];
-      const uint2 G1 = grid[(q[l >> 1] >> (16 * (l & 1) + 8)) & 255u];
-      dacc<MR, XS>(G0.x ^ M.x, x, 4 * l, acc);
-      dacc<MR, XS>(G0.y ^ M.y, x, 4 * l + 1, acc);
-      dacc<MR, XS>(G1.x ^ M.z, x, 4 * l + 2, acc);
-      dacc<MR, XS>(G1.y ^ M.w, x, 4 * l + 3, acc);
+      dacc<MR, XS>(G0[l].x ^ M[l].x, x, 4 * l, acc);
+      dacc<MR, XS>(G0[l].y ^ M[l].y, x, 4 * l + 1, acc);
+      dacc<MR, XS>(G1[l].x ^ M[l].z, x, 4 * l + 2, acc);
+      dacc<MR, XS>(G1[l].y ^ M[l].w, x, 4 * l + 3, acc);
     }
 #pragma unroll
     for (int m = 0; m < MR; ++m) out[m] += d * acc[m];
@@ -364,14 +376,19 @@ template <> struct Qmv<IQ2_XXS> {
     float acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = 0.f;
+    // all eight table reads of the group in flight before the first use
+    uint4 M[4], G[4];
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
-      const uint4 M = km[(u >> (7 * l)) & 127u];
-      const uint4 G = grid[(q[0] >> (8 * l)) & 255u];
-      dacc<MR, XS>(G.x ^ M.x, x, 4 * l, acc);
-      dacc<MR, XS>(G.y ^ M.y, x, 4 * l + 1, acc);
-      dacc<MR, XS>(G.z ^ M.z, x, 4 * l + 2, acc);
-      dacc<MR, XS>(G.w ^ M.w, x, 4 * l + 3, acc);
+      M[l] = km[bfe(u, 7 * l, 7)];
+      G[l] = grid[bfe(q[0], 8 * l, 8)];
+    }
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      dacc<MR, XS>(G[l].x ^ M[l].x, x, 4 * l, acc);
+      dacc<MR, XS>(G[l].y ^ M[l].y, x, 4 * l + 1, acc);
+      dacc<MR, XS>(G[l].z ^ M[l].z, x, 4 * l + 2, acc);
+      dacc<MR, XS>(G[l].w ^ M[l].w, x, 4 * l + 3, acc);
     }
 #pragma unroll
     for (int m = 0; m < MR; ++m) out[m] += d * acc[m];
@@ -395,11 +412,15 @@ template <> struct Qmv<IQ2_XS> {
     float a0[MR], a1[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) { a0[m] = 0.f; a1[m] = 0.f; }
+    uint4 Ms[4], Gs[4];
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {  // all table reads of the group in flight before the first use
+      Ms[l] = km[bfe(q[l >> 1], 16 * (l & 1) + 9, 7)];
+      Gs[l] = grid[bfe(q[l >> 1], 16 * (l & 1), 9)];
+    }
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
-      const uint32_t v = (q[l >> 1] >> (16 * (l & 1))) & 0xFFFFu;
-      const uint4 M = km[(v >> 9) & 127u];
-      const uint4 G = grid[v & 511u];
+      const uint4 M = Ms[l], G = Gs[l];
       if (l < 2) {
         dacc<MR, XS>(G.x ^ M.x, x, 4 * l, a0); dacc<MR, XS>(G.y ^ M.y, x, 4 * l + 1, a0);
         dacc<MR, XS>(G.z ^ M.z, x, 4 * l + 2, a0); dacc<MR, XS>(G.w ^ M.w, x, 4 * l + 3, a0);
@@ -432,11 +453,15 @@ template <> struct Qmv<IQ2_S> {
     float a0[MR], a1[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) { a0[m] = 0.f; a1[m] = 0.f; }
+    uint4 Ms[4], Gs[4];
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {  // all table reads of the group in flight before the first use
+      Gs[l] = grid[bfe(qs, 8 * l, 8) | (bfe(qh, 2 * l, 2) << 8)];
+      Ms[l] = bm[bfe(sg, 8 * l, 8)];
+    }
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
-      const uint32_t idx = ((qs >> (8 * l)) & 255u) | (((qh >> (2 * l)) & 3u) << 8);
-      const uint4 G = grid[idx];
-      const uint4 M = bm[(sg >> (8 * l)) & 255u];
+      const uint4 M = Ms[l], G = Gs[l];
       if (l < 2) {
         dacc<MR, XS>(G.x ^ M.x, x, 4 * l, a0); dacc<MR, XS>(G.y ^ M.y, x, 4 * l + 1, a0);
         dacc<MR, XS>(G.z ^ M.z, x, 4 * l + 2, a0); dacc<MR, XS>(G.w ^ M.w, x, 4 * l + 3, a0);
@@ -467,9 +492,12 @@ template <> struct Qmv<IQ1_S> {
     float acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = 0.f;
+    uint4 Gs[4];
+#pragma unroll
+    for (int l = 0; l < 4; ++l) Gs[l] = grid[bfe(qs, 8 * l, 8) | (bfe(h, 3 * l, 3) << 8)];
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
-      const uint4 G = grid[((qs >> (8 * l)) & 255u) | (((h >> (3 * l)) & 7u) << 8)];
+      const uint4 G = Gs[l];
       dacc<MR, XS>(G.x, x, 4 * l, acc); dacc<MR, XS>(G.y, x, 4 * l + 1, acc);
       dacc<MR, XS>(G.z, x, 4 * l + 2, acc); dacc<MR, XS>(G.w, x, 4 * l + 3, acc);
     }
@@ -505,10 +533,13 @@ template <> struct Qmv<IQ1_M> {
     for (int l = 0; l < 4; ++l)
 #pragma unroll
       for (int m = 0; m < MR; ++m) a[l][m] = 0.f;
+    uint4 Gs[4];
+#pragma unroll
+    for (int l = 0; l < 4; ++l) Gs[l] = grid[bfe(qs, 8 * l, 8) | (bfe(qh, 4 * l, 3) << 8)];
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
-      const uint32_t hn = (qh >> (4 * l)) & 15u;
-      const uint4 G = grid[((qs >> (8 * l)) & 255u) | ((hn & 7u) << 8)];
+      const uint32_t hn = bfe(qh, 4 * l, 4);
+      const uint4 G = Gs[l];
       dacc<MR, XS>(G.x, x, 4 * l, a[l]); dacc<MR, XS>(G.y, x, 4 * l + 1, a[l]);
       dacc<MR, XS>(G.z, x, 4 * l + 2, a[l]); dacc<MR, XS>(G.w, x, 4 * l + 3, a[l]);
       const float delta = (hn & 8u) ? -0.125f : 0.125f;
@@ -660,6 +691,20 @@ __device__ __forceinline__ void qmv_load_x1(XReg<MR, XS, Qmv<T>::kSums>& xr, boo
   }
 }
 
+// The type's table image in static LDS (at LDS address 0, a constant the table reads fold into
+// their address arithmetic); the rest of the layout is dynamic LDS behind it.
+template <int B>
+struct QmvTblLds {
+  __device__ __forceinline__ static uint8_t* get() {
+    __shared__ __attribute__((aligned(16))) uint8_t t[B];
+    return t;
+  }
+};
+template <>
+struct QmvTblLds<0> {
+  __device__ __forceinline__ static uint8_t* get() { return nullptr; }
+};
+
 // PR2 (one fp16 activation row, K = 5120: 20 superblocks = 2.5 slices per row): an item is
 // two neighbouring rows A and B, decoded as five full slices per lane instead of 2 x 3 with
 // half of every third slice idle: slices 0 and 1 of A, slices 0 and 1 of B, and a shared
@@ -674,10 +719,12 @@ __global__ void __launch_bounds__(QmvBounds<qmv_weight(MR, GL, XS)>::v) qmv_kern
   // item count, DMA wait counts, loop bounds) then stays in scalar registers and branches
   const int tid = threadIdx.x, lane = tid & 63, nw = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  uint8_t* tbl = smem;
-  uint8_t* xst = smem + a.x_off;
-  float* red = reinterpret_cast<float*>(smem + a.red_off);   // [rows_per_wg][MR][W] (W > 1)
-  uint8_t* ring = smem + a.ring_off + wave * a.nb * a.sbuf;  // this wave's ring
+  // layout offsets count from the table's start; dynamic LDS starts where the table ends
+  uint8_t* tbl = QmvTblLds<P::kTbl>::get();
+  uint8_t* dyn = smem - a.tbl_bytes;
+  uint8_t* xst = dyn + a.x_off;
+  float* red = reinterpret_cast<float*>(dyn + a.red_off);   // [rows_per_wg][MR][W] (W > 1)
+  uint8_t* ring = dyn + a.ring_off + wave * a.nb * a.sbuf;  // this wave's ring
 
   const int64_t r0 = (int64_t)blockIdx.x * a.rows_per_wg;
   const int64_t r1 = min(a.N, r0 + (int64_t)a.rows_per_wg);
@@ -807,7 +854,8 @@ static hipError_t launch_qmv_t(const QmvArgs& a, int grid, int threads, size_t l
   auto k = qmv_kernel<T, MR, XS, GL, A4, PR2>;
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       160 * 1024 - Qmv<T>::kTbl);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
@@ -894,10 +942,7 @@ bool build_qmv_table(int qt, const uint16_t* grid16, const uint8_t* ksigns, std:
       }
       break;
     }
-    case IQ3_S:  // 16 nibble masks, 2 dwords each
-      for (int i = 0; i < 32; ++i) m[i] = sign_mask_pair_host((uint32_t)(i >> 1), i & 1);
-      break;
-    case IQ2_S:  // 256 byte masks, 4 dwords each
+    case IQ3_S: case IQ2_S:  // 256 byte masks, 4 dwords each
       for (int i = 0; i < 256 * 4; ++i) m[i] = sign_mask_pair_host((uint32_t)(i >> 2), i & 3);
       break;
     case IQ2_XXS: case IQ2_XS: case IQ3_XXS:  // 128 ksigns masks, 4 dwords each
@@ -978,8 +1023,9 @@ static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, 
   if (nb < 2) return hipErrorInvalidValue;
   a.nb = nb;
   const int threads = nw * 64;
-  const size_t lds = (size_t)a.ring_off + (size_t)nw * nb * a.sbuf;
-  if (lds > (size_t)lds_cap) return hipErrorInvalidValue;
+  const size_t lds_all = (size_t)a.ring_off + (size_t)nw * nb * a.sbuf;
+  if (lds_all > (size_t)lds_cap) return hipErrorInvalidValue;
+  const size_t lds = lds_all - (size_t)a.tbl_bytes;  // dynamic part: the table is static LDS
   switch (qt) {
     case Q2_K: return launch_qmv_type<Q2_K>(a, mr, xs, grid, threads, lds, s);
     case Q4_K: return launch_qmv_type<Q4_K>(a, mr, xs, grid, threads, lds, s);

@@ -745,14 +745,19 @@ __global__ void __launch_bounds__(QmvBounds<qmv_weight(MR, GL, XS)>::v) qmv_kern
   const uintptr_t base = reinterpret_cast<uintptr_t>(a.packed) + (uintptr_t)(row0 * a.row_bytes + (int64_t)sl0 * 8 * BB);
   const uintptr_t stride = (uintptr_t)a.row_bytes * (uintptr_t)(RI * a.slots);
 
-  // ---- prologue: table + activations (once per workgroup), then this wave's first items ----
+  // ---- prologue: the table and the activations (once per workgroup), then this wave's first
+  // item; the ring fills up gradually (below). A wave that queued its whole ring at once would
+  // stall in DMA issue (the CU's memory queue is full at kernel start) before its first item's
+  // decode, and would put the first items of the waves behind it back.
   if constexpr (P::kTbl > 0) dma_copy(a.tb.qmv_tbl, P::kTbl, tbl, wave, nw, lane);
   if (a.x_lds) dma_copy(a.x, a.x_bytes, xst, wave, nw, lane);
-  const int pre = min(a.nb - 1, nitems);
-  for (int i = 0; i < pre; ++i)
-    dma_item(base + (uintptr_t)i * stride, item_bytes, a.cdma, ring + i * a.sbuf, lane);
-  wait_vmcnt(pre * a.cdma);  // this wave's share of the table and activations has landed
-  __syncthreads();           // ... and every other wave's share
+  int issued = 0;  // items issued so far (wave-uniform)
+  if (nitems > 0) {
+    dma_item(base, item_bytes, a.cdma, ring, lane);
+    issued = 1;
+  }
+  wait_vmcnt(issued * a.cdma);  // this wave's share of the table and activations has landed
+  __syncthreads();              // ... and every other wave's share
 
   XReg<MR, XS, P::kSums> xr[GL];
 #pragma unroll
@@ -763,15 +768,16 @@ __global__ void __launch_bounds__(QmvBounds<qmv_weight(MR, GL, XS)>::v) qmv_kern
     else qmv_load_x1<T, MR, XS>(xr[q], act, act ? u : 0, a.x, a.x_dtype, a.K, a.M);
   }
 
-  // ---- main loop: one item per row, nb-1 items in flight ----
+  // ---- main loop: one item per row, up to nb-1 items in flight ----
   int buf = 0;
   for (int t = 0; t < nitems; ++t) {
-    wait_vmcnt(min(a.nb - 2, nitems - 1 - t) * a.cdma);  // item t has landed
-    if (t + a.nb - 1 < nitems) {
-      int nbuf = buf + a.nb - 1;
-      if (nbuf >= a.nb) nbuf -= a.nb;
-      dma_item(base + (uintptr_t)(t + a.nb - 1) * stride, item_bytes, a.cdma, ring + nbuf * a.sbuf, lane);
-    }
+    wait_vmcnt((issued - 1 - t) * a.cdma);  // item t has landed (vmcnt is in order)
+    // top the ring up to item t + nb - 1, at most two items per step (one in steady state);
+    // item i goes to buffer i % nb, whose previous item (i - nb < t) has been consumed
+    const int lim = min(nitems, t + a.nb);
+#pragma unroll 1
+    for (int k = 0; k < 2 && issued < lim; ++k, ++issued)
+      dma_item(base + (uintptr_t)issued * stride, item_bytes, a.cdma, ring + (issued % a.nb) * a.sbuf, lane);
     const int64_t row = row0 + (int64_t)t * RI * a.slots;
     const uint32_t delta = (uint32_t)((base + (uintptr_t)t * stride) & 15u);
     const uint8_t* b = ring + buf * a.sbuf;

@@ -31,6 +31,8 @@ extern "C" {
 #define GSQ_F32 0
 #define GSQ_F16 1
 #define GSQ_BF16 2
+#define GSQ_IDS_I32 0       /* embedding id dtype codes */
+#define GSQ_IDS_I64 1
 
 /* Library ABI version. */
 int gsq_version(void);
@@ -64,6 +66,15 @@ int gsq_qmv(int qtype_id, const void* packed, const void* x, int x_dtype, void* 
  * (mlx_gsq/runtime/kernels/qmm.py:559-594). */
 int gsq_qmm(int qtype_id, const void* packed, const void* x, int x_dtype, void* y, int y_dtype,
             int64_t M, int64_t N, int64_t K, void* stream);
+
+/* Packed embedding gather: out[t, :] = dequantized row ids[t] of a (vocab, dims) packed table,
+ * rounded to out_dtype (GSQ_F32 / GSQ_F16 / GSQ_BF16, round-to-nearest-even from the exact
+ * float32 value); ids are int32 (GSQ_IDS_I32) or int64 (GSQ_IDS_I64), n_ids of them; dims a
+ * multiple of 256; out 16-byte aligned, n_ids * dims values. Ids outside [0, vocab) give rows
+ * of zeros. Replaces iq2_s_embedding (mlx_gsq/runtime/kernels/embedding.py:30-36), which is
+ * IQ2_S only; this entry point takes any of the 11 types. */
+int gsq_embedding(int qtype_id, const void* packed, const void* ids, int ids_dtype, int64_t n_ids,
+                  int64_t vocab, int64_t dims, void* out, int out_dtype, void* stream);
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* gsq_last_error(void);

@@ -19,6 +19,8 @@ hipError_t launch_qmv(int qt, const uint8_t* packed, const void* x, int xdt, voi
                       int K, const DevTables& tb, int num_cus, hipStream_t s);
 hipError_t launch_qmm(int qt, const uint8_t* packed, const void* x, int xdt, void* y, int ydt, int64_t M, int64_t N,
                       int K, const DevTables& tb, int num_cus, const QmmWorkspace& ws, hipStream_t s);
+hipError_t launch_embedding(int qt, const uint8_t* packed, const void* ids, int ids64, int64_t n_ids, int64_t vocab,
+                            int64_t dims, void* out, int odt, const DevTables& t, hipStream_t s);
 int qmv_table_bytes(int qt);
 bool build_qmv_table(int qt, const uint16_t* grid16, const uint8_t* ksigns, std::vector<uint8_t>& out);
 }  // namespace gsq
@@ -282,6 +284,27 @@ int gsq_qmm(int qt, const void* packed, const void* x, int xdt, void* y, int ydt
   hipError_t e = launch_qmm(qt, static_cast<const uint8_t*>(packed), x, xdt, y, ydt, M, N, (int)K, tb, cus, ws,
                             static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(GSQ_E_HIP, "qmm launch: %s", hipGetErrorString(e));
+  return GSQ_OK;
+}
+
+int gsq_embedding(int qt, const void* packed, const void* ids, int ids_dtype, int64_t n_ids, int64_t vocab,
+                  int64_t dims, void* out, int out_dtype, void* stream) {
+  if (block_bytes_of(qt) == 0) return fail(GSQ_E_UNSUPPORTED, "unsupported quant type id %d", qt);
+  if (ids_dtype != GSQ_IDS_I32 && ids_dtype != GSQ_IDS_I64) return fail(GSQ_E_TYPE, "ids must be int32 or int64");
+  if (out_dtype != GSQ_F32 && out_dtype != GSQ_F16 && out_dtype != GSQ_BF16)
+    return fail(GSQ_E_TYPE, "unsupported output dtype code %d", out_dtype);
+  if (dims <= 0 || dims % 256) return fail(GSQ_E_VALUE, "embedding dimensions must be divisible by 256");
+  if (n_ids < 0 || vocab < 0) return fail(GSQ_E_VALUE, "negative id count or vocabulary size");
+  if (n_ids == 0) return GSQ_OK;
+  if (!packed || !ids || !out) return fail(GSQ_E_VALUE, "NULL pointer");
+  if (reinterpret_cast<uintptr_t>(out) & 15) return fail(GSQ_E_VALUE, "out must be 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(ids) & (ids_dtype == GSQ_IDS_I64 ? 7 : 3)) return fail(GSQ_E_VALUE, "misaligned ids");
+  DevTables tb;
+  int cus;
+  if (int rc = resolve(qt, &tb, &cus)) return rc;
+  hipError_t e = launch_embedding(qt, static_cast<const uint8_t*>(packed), ids, ids_dtype == GSQ_IDS_I64, n_ids, vocab,
+                                  dims, out, out_dtype, tb, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(GSQ_E_HIP, "embedding launch: %s", hipGetErrorString(e));
   return GSQ_OK;
 }
 

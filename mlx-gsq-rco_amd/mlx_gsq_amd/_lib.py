@@ -17,6 +17,7 @@ LIB_PATH = os.environ.get("GSQ_LIB") or os.path.join(os.path.dirname(os.path.abs
 
 GSQ_OK, GSQ_E_VALUE, GSQ_E_UNSUPPORTED, GSQ_E_TABLES, GSQ_E_HIP, GSQ_E_TYPE = range(6)
 DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+ID_CODES = {torch.int32: 0, torch.int64: 1}
 
 # Every symbol include/gsq.h declares, with its ctypes signature.
 _I64, _I32, _VP = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p
@@ -28,6 +29,7 @@ EXPORTS = {
     "gsq_dequant": (_I32, [_I32, _VP, _I64, _VP, _VP]),
     "gsq_qmv": (_I32, [_I32, _VP, _VP, _I32, _VP, _I32, _I64, _I64, _I64, _VP]),
     "gsq_qmm": (_I32, [_I32, _VP, _VP, _I32, _VP, _I32, _I64, _I64, _I64, _VP]),
+    "gsq_embedding": (_I32, [_I32, _VP, _VP, _I32, _I64, _I64, _I64, _VP, _I32, _VP]),
     "gsq_last_error": (ctypes.c_char_p, []),
 }
 

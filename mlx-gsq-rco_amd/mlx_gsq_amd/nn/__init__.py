@@ -1,4 +1,5 @@
 """Packed-weight modules."""
+from .embedding import GSQEmbedding
 from .linear import GSQLinear
 
-__all__ = ["GSQLinear"]
+__all__ = ["GSQEmbedding", "GSQLinear"]

@@ -80,6 +80,27 @@ def test_python_validation_mirrors_reference():
         decode_weight(w)
 
 
+def test_embedding_validation_mirrors_reference():
+    """embedding.py:30-33 and nn/embedding.py:6 checks, before any device work."""
+    from mlx_gsq_amd import _lib
+    from mlx_gsq_amd.nn import GSQEmbedding
+    from mlx_gsq_amd.runtime.kernels import iq2_s_embedding
+    from mlx_gsq_amd.runtime.store import PackedWeight
+    ids = torch.zeros(1, 3, dtype=torch.int32)
+    p = torch.zeros(10 * 2 * 82, dtype=torch.uint8)
+    with pytest.raises(ValueError, match="divisible by 256"):
+        iq2_s_embedding(ids, p, vocab_size=10, dimensions=300)
+    with pytest.raises(ValueError, match="size mismatch"):
+        iq2_s_embedding(ids, p[:-1], vocab_size=10, dimensions=512)
+    w = PackedWeight("e", p, (512, 10), (10, 512), "IQ2_XS", 17, 5120, p.numel())
+    with pytest.raises(NotImplementedError, match="IQ2_XS"):
+        GSQEmbedding(w)
+    rc = _lib.lib().gsq_embedding(22, 1, 1, 0, 3, 10, 300, 16, 1, None)
+    assert rc == _lib.GSQ_E_VALUE and b"divisible by 256" in _lib.lib().gsq_last_error()
+    rc = _lib.lib().gsq_embedding(22, 1, 1, 2, 3, 10, 512, 16, 1, None)
+    assert rc == _lib.GSQ_E_TYPE
+
+
 def test_codebook_validation():
     from mlx_gsq_amd import tables
     t = tables.synthetic_tables(3)

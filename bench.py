@@ -294,6 +294,48 @@ def run_crossover(device, reps=20):
     return {"per_projection": out, "layer_total": totals}
 
 
+def run_embedding(device, vocab=248320, dims=5120, tokens=(1, 4096), reps=20):
+    """Packed IQ2_S embedding gather (the reference's token-embedding lookup, 27B shape: a
+    248320 x 5120 IQ2_S table, 407 MB) for a decode step (1 token) and a prefill batch; bf16
+    rows. Bytes = packed rows read + output written; HIP events on the launch stream."""
+    import torch
+    from mlx_gsq_amd import _lib, tables
+    from mlx_gsq_amd.formats import TYPE_IDS
+    tables.set_tables(tables.synthetic_tables(0))
+    _lib.ensure_tables("IQ2_S", device)
+    lib = _lib.lib()
+    packed = make_device_packed("IQ2_S", vocab, dims, seed=77, device=device)
+    stream = torch.cuda.current_stream(device)
+    res = {}
+    for t in tokens:
+        ids = torch.randint(0, vocab, (t,), dtype=torch.int64, device=device,
+                            generator=torch.Generator(device=device).manual_seed(t))
+        out = torch.empty((t, dims), dtype=torch.bfloat16, device=device)
+
+        def launch():
+            rc = lib.gsq_embedding(TYPE_IDS["IQ2_S"], packed.data_ptr(), ids.data_ptr(), 1, t, vocab, dims,
+                                   out.data_ptr(), 2, stream.cuda_stream)
+            if rc:
+                raise RuntimeError(lib.gsq_last_error().decode())
+
+        for _ in range(3):
+            launch()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            launch()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        nbytes = t * (dims // 256) * 82 + t * dims * 2
+        res[f"tokens={t}"] = {"us": round(us, 2), "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                              "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    log(f"embedding: {res}")
+    return {"table": f"IQ2_S {vocab}x{dims}", "out": "bf16", **res}
+
+
 def run_stack(device, layers=64, reps=10):
     """one decode token of the 448 projection GEMVs (64 layers x the 7 projections of
     the mixed layer, distinct random weights per layer, 8.34 GB resident) at M=1, captured in one
@@ -468,6 +510,7 @@ def main():
     qmm = {} if args.no_qmm else run_qmm(device)
     crossover = {} if args.no_layer else run_crossover(device)
     stack = {} if args.no_layer else run_stack(device)
+    emb = {} if args.no_layer else run_embedding(device)
     cpu = None if args.no_cpu else cpu_baseline()
     from mlx_gsq_amd.formats import QTYPES
     step_bytes = qc.step_bytes()
@@ -511,6 +554,7 @@ def main():
         "qmm": qmm,
         "layer_crossover": crossover,
         "decode_stack": stack,
+        "embedding": emb,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

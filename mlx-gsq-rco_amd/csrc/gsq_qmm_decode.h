@@ -15,8 +15,10 @@
 // single rounding can differ from its float32-then-fp16 double rounding by one fp16 ulp when
 // the float32 value falls on an fp16 tie.
 //
-// `sb` points at the superblock in LDS (2-byte aligned; A4: 4-byte aligned), `tbl` at the
-// type's table image: fp16 codebook (entries x coords) followed by its sign masks.
+// The superblock sits at byte `sd` (2-byte aligned; A4: 4-byte aligned) of its 16-byte aligned
+// LDS row slot `sb`: word reads take the aligned slot address and funnel-shift by sd's low bits
+// (LDS reads at 2-byte aligned addresses are served, but stall). `tbl` points at the type's
+// table image: fp16 codebook (entries x coords) followed by its sign masks.
 #pragma once
 #include "gsq_common.h"
 
@@ -59,14 +61,14 @@ struct QmmDec;
 // Q2_K (k_decode.py:18-30): w = d*(sm&15)*q - dmin*(sm>>4)
 template <bool A4>
 struct QmmDec<Q2_K, A4> {
-  __device__ __forceinline__ static void run(const uint8_t* sb, const uint8_t*, int g, int kq, uint32_t (&o)[4]) {
+  __device__ __forceinline__ static void run(const uint8_t* sb, uint32_t sd, const uint8_t*, int g, int kq, uint32_t (&o)[4]) {
     uint32_t q[2];
-    lds_words<2, A4>(sb, 16 + (g >> 2) * 32 + 8 * kq, q);
+    lds_words<2, A4>(sb, sd + 16 + (g >> 2) * 32 + 8 * kq, q);
     const int sh = 2 * (g & 3);
     q[0] = (q[0] >> sh) & 0x03030303u;
     q[1] = (q[1] >> sh) & 0x03030303u;
-    const uint32_t dd = lds_w32<A4>(sb, 80);
-    const uint32_t sm = lds_u8(sb, 2 * g + (kq >> 1));
+    const uint32_t dd = lds_w32<A4>(sb, sd + 80);
+    const uint32_t sm = lds_u8(sb, sd + 2 * g + (kq >> 1));
     const float a = h2f(dd & 0xFFFFu) * (float)(sm & 15u);
     const float b = h2f(dd >> 16) * (float)(sm >> 4);
     codes8(q, a * kCode, -b, o);
@@ -76,15 +78,15 @@ struct QmmDec<Q2_K, A4> {
 // Q4_K (k_decode.py:31-50): w = d*sc*q - dmin*mn with 6-bit scales/mins
 template <bool A4>
 struct QmmDec<Q4_K, A4> {
-  __device__ __forceinline__ static void run(const uint8_t* sb, const uint8_t*, int g, int kq, uint32_t (&o)[4]) {
+  __device__ __forceinline__ static void run(const uint8_t* sb, uint32_t sd, const uint8_t*, int g, int kq, uint32_t (&o)[4]) {
     uint32_t q[2];
-    lds_words<2, A4>(sb, 16 + (g >> 1) * 32 + 8 * kq, q);
+    lds_words<2, A4>(sb, sd + 16 + (g >> 1) * 32 + 8 * kq, q);
     const int sh = 4 * (g & 1);
     q[0] = (q[0] >> sh) & 0x0F0F0F0Fu;
     q[1] = (q[1] >> sh) & 0x0F0F0F0Fu;
     uint32_t s[3];
-    lds_words<3, A4>(sb, 4, s);
-    const uint32_t dd = lds_w32<A4>(sb, 0);
+    lds_words<3, A4>(sb, sd + 4, s);
+    const uint32_t dd = lds_w32<A4>(sb, sd + 0);
     uint32_t sc, mn;
     const int gg = g & 3;
     if (g < 4) {
@@ -104,17 +106,17 @@ struct QmmDec<Q4_K, A4> {
 // Q6_K (k_decode.py:51-65): w = d*scale*(q - 32), q = low nibble | 2 high bits << 4
 template <bool A4>
 struct QmmDec<Q6_K, A4> {
-  __device__ __forceinline__ static void run(const uint8_t* sb, const uint8_t*, int g, int kq, uint32_t (&o)[4]) {
+  __device__ __forceinline__ static void run(const uint8_t* sb, uint32_t sd, const uint8_t*, int g, int kq, uint32_t (&o)[4]) {
     const int h = g >> 2, pl = g & 3;
     uint32_t ql[2], qh[2];
-    lds_words<2, A4>(sb, h * 64 + (pl & 1) * 32 + 8 * kq, ql);
-    lds_words<2, A4>(sb, 128 + h * 32 + 8 * kq, qh);
+    lds_words<2, A4>(sb, sd + h * 64 + (pl & 1) * 32 + 8 * kq, ql);
+    lds_words<2, A4>(sb, sd + 128 + h * 32 + 8 * kq, qh);
     const int shl = 4 * (pl >> 1), shh = 2 * pl;
     uint32_t q[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) q[i] = ((ql[i] >> shl) & 0x0F0F0F0Fu) | (((qh[i] >> shh) & 0x03030303u) << 4);
-    const int sc = (int)(int8_t)lds_u8(sb, 192 + 2 * g + (kq >> 1));
-    const float a = h2f(lds_u16(sb, 208)) * (float)sc;
+    const int sc = (int)(int8_t)lds_u8(sb, sd + 192 + 2 * g + (kq >> 1));
+    const float a = h2f(lds_u16(sb, sd + 208)) * (float)sc;
     codes8(q, a * kCode, -32.f * a, o);
   }
 };
@@ -122,12 +124,12 @@ struct QmmDec<Q6_K, A4> {
 // IQ4_XS (k_decode.py:66-80): w = d*scale*kvalues[q]; kvalues + 128 looked up as bytes
 template <bool A4>
 struct QmmDec<IQ4_XS, A4> {
-  __device__ __forceinline__ static void run(const uint8_t* sb, const uint8_t*, int g, int kq, uint32_t (&o)[4]) {
+  __device__ __forceinline__ static void run(const uint8_t* sb, uint32_t sd, const uint8_t*, int g, int kq, uint32_t (&o)[4]) {
     uint32_t q[2];
-    lds_words<2, A4>(sb, 8 + 16 * g + 8 * (kq & 1), q);
+    lds_words<2, A4>(sb, sd + 8 + 16 * g + 8 * (kq & 1), q);
     const int sh = 4 * (kq >> 1);
-    const uint32_t dw = lds_w32<A4>(sb, 0);
-    const uint32_t low = (lds_u8(sb, 4 + g / 2) >> (4 * (g & 1))) & 15u;
+    const uint32_t dw = lds_w32<A4>(sb, sd + 0);
+    const uint32_t low = (lds_u8(sb, sd + 4 + g / 2) >> (4 * (g & 1))) & 15u;
     const uint32_t high = ((dw >> 16) >> (2 * g)) & 3u;
     const float a = h2f(dw & 0xFFFFu) * (float)((int)(low | (high << 4)) - 32);
     // kvalues + 128 = {1,24,45,63,79,93,106,118,129,141,153,166,181,197,217,241}
@@ -146,27 +148,30 @@ struct QmmDec<IQ4_XS, A4> {
   }
 };
 
-// IQ3_S (iq3_s_decode.py:16-40): w = +-d*(1+2*s)*grid[gi][c], 9-bit grid index; one byte
-// sign mask (eight signs, four words) per two entries, after the codebook
+// IQ3_S (iq3_s_decode.py:16-40): w = +-d*(1+2*s)*grid[gi][c], 9-bit grid index; sign masks
+// per nibble (two words) at the end of the table image
 template <bool A4>
 struct QmmDec<IQ3_S, A4> {
   static constexpr uint32_t kGridB = 512 * 4 * 2;
-  __device__ __forceinline__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
-    const float d = h2f(lds_u16(sb, 0));
-    const uint32_t sbyte = lds_u8(sb, 106 + (g >> 1));
+  static constexpr uint32_t kMaskB = kGridB + 256 * 16;  // after the QMV kernel's byte masks
+  __device__ __forceinline__ static void run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+    const float d = h2f(lds_u16(sb, sd + 0));
+    const uint32_t sbyte = lds_u8(sb, sd + 106 + (g >> 1));
     const float db = d * (float)(1u + 2u * ((sbyte >> (4 * (g & 1))) & 15u));
-    const uint32_t qh = lds_u8(sb, 66 + g);
-    const uint32_t qq = lds_u16(sb, 2 + 8 * g + 2 * kq);
+    const uint32_t qh = lds_u8(sb, sd + 66 + g);
+    const uint32_t qq = lds_u16(sb, sd + 2 + 8 * g + 2 * kq);
     const uint32_t i0 = (qq & 0xFFu) | ((qh << (8 - 2 * kq)) & 256u);
     const uint32_t i1 = (qq >> 8) | ((qh << (7 - 2 * kq)) & 256u);
-    const uint32_t signs = lds_u8(sb, 74 + 4 * g + kq);
+    const uint32_t signs = lds_u8(sb, sd + 74 + 4 * g + kq);
     const uint32_t* e0 = tbl_words(tbl, i0 * 8);
     const uint32_t* e1 = tbl_words(tbl, i1 * 8);
-    const uint32_t* m = tbl_words(tbl, kGridB + signs * 16);  // byte mask: 8 signs
-    o[0] = mix2(db, e0[0], 0.f) ^ m[0];
-    o[1] = mix2(db, e0[1], 0.f) ^ m[1];
-    o[2] = mix2(db, e1[0], 0.f) ^ m[2];
-    o[3] = mix2(db, e1[1], 0.f) ^ m[3];
+    // nibble masks (16 entries: few distinct LDS addresses per read, unlike the 256 byte masks)
+    const uint32_t* m0 = tbl_words(tbl, kMaskB + (signs & 15u) * 8);
+    const uint32_t* m1 = tbl_words(tbl, kMaskB + (signs >> 4) * 8);
+    o[0] = mix2(db, e0[0], 0.f) ^ m0[0];
+    o[1] = mix2(db, e0[1], 0.f) ^ m0[1];
+    o[2] = mix2(db, e1[0], 0.f) ^ m1[0];
+    o[3] = mix2(db, e1[1], 0.f) ^ m1[1];
   }
 };
 
@@ -182,11 +187,11 @@ __device__ __forceinline__ void grid8(const uint8_t* tbl, uint32_t qi, float d, 
 template <bool A4>
 struct QmmDec<IQ3_XXS, A4> {
   static constexpr uint32_t kGridB = 256 * 4 * 2;
-  __device__ __forceinline__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
-    const uint32_t u = lds_w32<A4>(sb, 66 + 4 * g);
-    const float d = h2f(lds_u16(sb, 0)) * (0.5f + (float)(u >> 28)) * 0.5f;
+  __device__ __forceinline__ static void run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+    const uint32_t u = lds_w32<A4>(sb, sd + 66 + 4 * g);
+    const float d = h2f(lds_u16(sb, sd + 0)) * (0.5f + (float)(u >> 28)) * 0.5f;
     const uint32_t* m = tbl_words(tbl, kGridB + ((u >> (7 * kq)) & 127u) * 16);
-    const uint32_t qq = lds_u16(sb, 2 + 8 * g + 2 * kq);
+    const uint32_t qq = lds_u16(sb, sd + 2 + 8 * g + 2 * kq);
     const uint32_t* e0 = tbl_words(tbl, (qq & 0xFFu) * 8);
     const uint32_t* e1 = tbl_words(tbl, (qq >> 8) * 8);
     o[0] = mix2(d, e0[0], 0.f) ^ m[0];
@@ -200,10 +205,10 @@ struct QmmDec<IQ3_XXS, A4> {
 template <bool A4>
 struct QmmDec<IQ2_XXS, A4> {
   static constexpr uint32_t kGridB = 256 * 8 * 2;
-  __device__ __forceinline__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
-    const uint32_t u = lds_w32<A4>(sb, 2 + 8 * g + 4);
-    const float d = h2f(lds_u16(sb, 0)) * (0.5f + (float)(u >> 28)) * 0.25f;
-    grid8(tbl, lds_u8(sb, 2 + 8 * g + kq), d, 0.f, tbl_words(tbl, kGridB + ((u >> (7 * kq)) & 127u) * 16), o);
+  __device__ __forceinline__ static void run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+    const uint32_t u = lds_w32<A4>(sb, sd + 2 + 8 * g + 4);
+    const float d = h2f(lds_u16(sb, sd + 0)) * (0.5f + (float)(u >> 28)) * 0.25f;
+    grid8(tbl, lds_u8(sb, sd + 2 + 8 * g + kq), d, 0.f, tbl_words(tbl, kGridB + ((u >> (7 * kq)) & 127u) * 16), o);
   }
 };
 
@@ -211,10 +216,10 @@ struct QmmDec<IQ2_XXS, A4> {
 template <bool A4>
 struct QmmDec<IQ2_XS, A4> {
   static constexpr uint32_t kGridB = 512 * 8 * 2;
-  __device__ __forceinline__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
-    const uint32_t q = lds_u16(sb, 2 + 2 * (4 * g + kq));
-    const uint32_t sc = (lds_u8(sb, 66 + g) >> (4 * (kq >> 1))) & 15u;
-    const float d = h2f(lds_u16(sb, 0)) * (0.5f + (float)sc) * 0.25f;
+  __device__ __forceinline__ static void run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+    const uint32_t q = lds_u16(sb, sd + 2 + 2 * (4 * g + kq));
+    const uint32_t sc = (lds_u8(sb, sd + 66 + g) >> (4 * (kq >> 1))) & 15u;
+    const float d = h2f(lds_u16(sb, sd + 0)) * (0.5f + (float)sc) * 0.25f;
     grid8(tbl, q & 511u, d, 0.f, tbl_words(tbl, kGridB + (q >> 9) * 16), o);
   }
 };
@@ -223,24 +228,24 @@ struct QmmDec<IQ2_XS, A4> {
 template <bool A4>
 struct QmmDec<IQ2_S, A4> {
   static constexpr uint32_t kGridB = 1024 * 8 * 2;
-  __device__ __forceinline__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+  __device__ __forceinline__ static void run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
     const int oo = 4 * g + kq;
-    const uint32_t hi = (lds_u8(sb, 66 + g) >> (2 * kq)) & 3u;
-    const uint32_t qi = lds_u8(sb, 2 + oo) | (hi << 8);
-    const uint32_t sc = (lds_u8(sb, 74 + g) >> (4 * (kq >> 1))) & 15u;
-    const float d = h2f(lds_u16(sb, 0)) * (0.5f + (float)sc) * 0.25f;
-    grid8(tbl, qi, d, 0.f, tbl_words(tbl, kGridB + lds_u8(sb, 34 + oo) * 16), o);
+    const uint32_t hi = (lds_u8(sb, sd + 66 + g) >> (2 * kq)) & 3u;
+    const uint32_t qi = lds_u8(sb, sd + 2 + oo) | (hi << 8);
+    const uint32_t sc = (lds_u8(sb, sd + 74 + g) >> (4 * (kq >> 1))) & 15u;
+    const float d = h2f(lds_u16(sb, sd + 0)) * (0.5f + (float)sc) * 0.25f;
+    grid8(tbl, qi, d, 0.f, tbl_words(tbl, kGridB + lds_u8(sb, sd + 34 + oo) * 16), o);
   }
 };
 
 // IQ1_S (iq_lookup_decode.py:27-30): w = d*(2*s+1)*(grid[qi][c] + delta) = fma(d, grid, d*delta)
 template <bool A4>
 struct QmmDec<IQ1_S, A4> {
-  __device__ __forceinline__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
-    const uint32_t h = lds_u16(sb, 34 + 2 * g);
-    const float d = h2f(lds_u16(sb, 0)) * (float)(2u * ((h >> 12) & 7u) + 1u);
+  __device__ __forceinline__ static void run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+    const uint32_t h = lds_u16(sb, sd + 34 + 2 * g);
+    const float d = h2f(lds_u16(sb, sd + 0)) * (float)(2u * ((h >> 12) & 7u) + 1u);
     const float dd = (h & 32768u) ? -0.125f * d : 0.125f * d;
-    const uint32_t qi = lds_u8(sb, 2 + 4 * g + kq) | (((h >> (3 * kq)) & 7u) << 8);
+    const uint32_t qi = lds_u8(sb, sd + 2 + 4 * g + kq) | (((h >> (3 * kq)) & 7u) << 8);
     grid8(tbl, qi, d, dd, nullptr, o);
   }
 };
@@ -249,14 +254,14 @@ struct QmmDec<IQ1_S, A4> {
 // scale words' top nibbles
 template <bool A4>
 struct QmmDec<IQ1_M, A4> {
-  __device__ __forceinline__ static void run(const uint8_t* sb, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+  __device__ __forceinline__ static void run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
     uint32_t w[2];
-    lds_words<2, A4>(sb, 48, w);
+    lds_words<2, A4>(sb, sd + 48, w);
     const uint32_t w0 = w[0] & 0xFFFFu, w1 = w[0] >> 16, w2 = w[1] & 0xFFFFu, w3 = w[1] >> 16;
     const uint32_t dbits = ((w0 & 61440u) >> 12) | ((w1 & 61440u) >> 8) | ((w2 & 61440u) >> 4) | (w3 & 61440u);
     const int oo = 4 * g + kq;
-    const uint32_t hn = (lds_u8(sb, 32 + oo / 2) >> (4 * (oo & 1))) & 15u;
-    const uint32_t qi = lds_u8(sb, oo) | ((hn & 7u) << 8);
+    const uint32_t hn = (lds_u8(sb, sd + 32 + oo / 2) >> (4 * (oo & 1))) & 15u;
+    const uint32_t qi = lds_u8(sb, sd + oo) | ((hn & 7u) << 8);
     const int sci = 2 * g + (kq >> 1);
     const uint32_t ww = (sci >> 2) == 0 ? w0 : ((sci >> 2) == 1 ? w1 : ((sci >> 2) == 2 ? w2 : w3));
     const uint32_t sc = (ww >> (3 * (sci & 3))) & 7u;

@@ -81,7 +81,7 @@ constexpr int qmm_tbl_bytes() {
        : T == IQ2_XS             ? 512 * 8 * 2 + 128 * 16
        : T == IQ2_S              ? 1024 * 8 * 2 + 256 * 16
        : T == IQ3_XXS            ? 256 * 4 * 2 + 128 * 16
-       : T == IQ3_S              ? 512 * 4 * 2 + 256 * 16
+       : T == IQ3_S              ? 512 * 4 * 2 + 256 * 16 + 16 * 8
                                  : 0;
 }
 
@@ -383,7 +383,7 @@ __global__ void __launch_bounds__(64 * WV, 1) qmm_mfma_kernel(QmmMfmaArgs args) 
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       uint32_t o[4];
-      QmmDec<T, A4>::run(wb + (16 * j + (lane & 15)) * S + dl[j], tbl, q & 7, lane >> 4, o);
+      QmmDec<T, A4>::run(wb + (16 * j + (lane & 15)) * S, dl[j], tbl, q & 7, lane >> 4, o);
       bf[j] = __builtin_bit_cast(half8_t, o);
     }
   };

@@ -286,7 +286,8 @@ template <> struct Qmv<IQ3_S> {
   static constexpr int kPair = PAIR_NAT;
   static constexpr int kSums = 0;
   static constexpr int kGridB = 512 * 4 * 2;
-  static constexpr int kTbl = kGridB + 256 * 16;  // grid + 256 byte sign masks
+  // grid + 256 byte sign masks + 16 nibble sign masks (the QMM kernel's)
+  static constexpr int kTbl = kGridB + 256 * 16 + 16 * 8;
   template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
@@ -948,7 +949,11 @@ bool build_qmv_table(int qt, const uint16_t* grid16, const uint8_t* ksigns, std:
       }
       break;
     }
-    case IQ3_S: case IQ2_S:  // 256 byte masks, 4 dwords each
+    case IQ3_S:  // 256 byte masks, 4 dwords each, then 16 nibble masks, 2 dwords each
+      for (int i = 0; i < 256 * 4; ++i) m[i] = sign_mask_pair_host((uint32_t)(i >> 2), i & 3);
+      for (int i = 0; i < 16 * 2; ++i) m[256 * 4 + i] = sign_mask_pair_host((uint32_t)(i >> 1), i & 1);
+      break;
+    case IQ2_S:  // 256 byte masks, 4 dwords each
       for (int i = 0; i < 256 * 4; ++i) m[i] = sign_mask_pair_host((uint32_t)(i >> 2), i & 3);
       break;
     case IQ2_XXS: case IQ2_XS: case IQ3_XXS:  // 128 ksigns masks, 4 dwords each

@@ -258,7 +258,11 @@ def _time_launches(fn, stream, reps):
 
 def run_crossover(device, reps=20):
     """per projection of the mixed layer and M in {1,2,4,8,16}, QMV vs QMM time (HIP
-    events, weights resident); the crossover is the smallest M at which QMM is faster."""
+    events, weights resident); the crossover is the smallest M at which QMM is faster. gsq_qmm
+    runs the small-batch kernel for M <= 16 fp16 rows. `routed_us` follows quantized_matvec's
+    routing (QMM from 8 rows, or from 3 rows on large matrices); `best_us` takes the faster."""
+    from mlx_gsq_amd.runtime.kernels.qmm import QMM_MIN_ROWS
+    from mlx_gsq_amd.runtime.kernels.qmv import _small_batch_faster
     import torch
     from mlx_gsq_amd import _lib
     from mlx_gsq_amd.formats import TYPE_IDS
@@ -279,7 +283,9 @@ def run_crossover(device, reps=20):
             if tv is None:
                 from mlx_gsq_amd import _lib as L
                 note = L.lib().gsq_last_error().decode()
-            row[f"M={m}"] = {"qmv_us": None if tv is None else round(tv, 2), "qmm_us": round(tm, 2)}
+            routed = "qmm" if (m >= QMM_MIN_ROWS or _small_batch_faster(m, torch.float16, n, k)) else "qmv"
+            row[f"M={m}"] = {"qmv_us": None if tv is None else round(tv, 2), "qmm_us": round(tm, 2),
+                             "routed": routed}
             if tv is None:
                 row[f"M={m}"]["qmv_refused"] = note
         cross = next((m for m in CROSS_ROWS if row[f"M={m}"]["qmv_us"] is None
@@ -288,8 +294,11 @@ def run_crossover(device, reps=20):
         del packed
     def best(r):  # the routed time: QMV where it runs and is faster, else QMM
         return r["qmm_us"] if r["qmv_us"] is None else min(r["qmv_us"], r["qmm_us"])
+    def routed(r):
+        return r["qmm_us"] if r["routed"] == "qmm" or r["qmv_us"] is None else r["qmv_us"]
     totals = {f"M={m}": {"qmm_us": round(sum(v["rows"][f"M={m}"]["qmm_us"] for v in out.values()), 2),
-                         "best_us": round(sum(best(v["rows"][f"M={m}"]) for v in out.values()), 2)}
+                         "best_us": round(sum(best(v["rows"][f"M={m}"]) for v in out.values()), 2),
+                         "routed_us": round(sum(routed(v["rows"][f"M={m}"]) for v in out.values()), 2)}
               for m in CROSS_ROWS}
     return {"per_projection": out, "layer_total": totals}
 

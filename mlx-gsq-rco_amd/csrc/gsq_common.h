@@ -67,13 +67,19 @@ struct QmvTuning {
   int pair;
 };
 
-// Launch-plan overrides of the QMM kernel: activation tile height in 16-row blocks (0 = by
+// Launch-plan overrides of the QMM kernels: activation tile height in 16-row blocks (0 = by
 // M), the fewest K columns (256 wide) per workgroup (0 = default) and waves per workgroup for
-// tiles of 128 or 256 rows (4, or 0 = 8).
+// tiles of 128 or 256 rows (4, or 0 = 8); the small-batch kernel's largest M (0 = 16, -1 =
+// never used), waves (4, or 0 = 8), 16-row blocks per wave (2, or 0 = 1) and fewest columns
+// per workgroup (0 = 1).
 struct QmmTuning {
   int mf;
   int min_cols;
   int waves;
+  int small_max_m;
+  int small_waves;
+  int small_nb;
+  int small_min_cols;
 };
 
 // Per-device QMM workspace, allocated once: fp32 partial tiles of workgroups that share an

@@ -4,7 +4,7 @@
 
 namespace gsq {
 
-QmmTuning g_qmm_tuning = {0, 0, 0};
+QmmTuning g_qmm_tuning = {0, 0, 0, 0, 0, 0, 0};
 
 hipError_t launch_qmm_q2_k(const uint8_t* packed, const void* x, int xdt, void* y, int ydt, int64_t M,
     int64_t N, int K, const DevTables& tb, int num_cus, const QmmWorkspace& ws, hipStream_t s);

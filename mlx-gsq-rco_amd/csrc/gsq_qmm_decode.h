@@ -175,12 +175,21 @@ struct QmmDec<IQ3_S, A4> {
   }
 };
 
-// one 8-wide codebook entry times d, with four sign-mask pairs
+// one 8-wide codebook entry times d, with four sign-mask pairs (HM) or none; the entry and
+// mask words are read before any is used
+template <bool HM>
 __device__ __forceinline__ void grid8(const uint8_t* tbl, uint32_t qi, float d, float c, const uint32_t* m,
                                       uint32_t (&o)[4]) {
   const uint32_t* e = tbl_words(tbl, qi * 16);
+  uint32_t ev[4], mv[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = mix2(d, e[i], c) ^ (m ? m[i] : 0u);
+  for (int i = 0; i < 4; ++i) ev[i] = e[i];
+  if constexpr (HM) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mv[i] = m[i];
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = mix2(d, ev[i], c) ^ mv[i];
 }
 
 // IQ3_XXS (iq_lookup_decode.py:7-12): w = +-d*(0.5+s)*0.5*grid[qi][c], ksigns masks
@@ -208,7 +217,7 @@ struct QmmDec<IQ2_XXS, A4> {
   __device__ __forceinline__ static void run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
     const uint32_t u = lds_w32<A4>(sb, sd + 2 + 8 * g + 4);
     const float d = h2f(lds_u16(sb, sd + 0)) * (0.5f + (float)(u >> 28)) * 0.25f;
-    grid8(tbl, lds_u8(sb, sd + 2 + 8 * g + kq), d, 0.f, tbl_words(tbl, kGridB + ((u >> (7 * kq)) & 127u) * 16), o);
+    grid8<true>(tbl, lds_u8(sb, sd + 2 + 8 * g + kq), d, 0.f, tbl_words(tbl, kGridB + ((u >> (7 * kq)) & 127u) * 16), o);
   }
 };
 
@@ -220,7 +229,7 @@ struct QmmDec<IQ2_XS, A4> {
     const uint32_t q = lds_u16(sb, sd + 2 + 2 * (4 * g + kq));
     const uint32_t sc = (lds_u8(sb, sd + 66 + g) >> (4 * (kq >> 1))) & 15u;
     const float d = h2f(lds_u16(sb, sd + 0)) * (0.5f + (float)sc) * 0.25f;
-    grid8(tbl, q & 511u, d, 0.f, tbl_words(tbl, kGridB + (q >> 9) * 16), o);
+    grid8<true>(tbl, q & 511u, d, 0.f, tbl_words(tbl, kGridB + (q >> 9) * 16), o);
   }
 };
 
@@ -234,7 +243,7 @@ struct QmmDec<IQ2_S, A4> {
     const uint32_t qi = lds_u8(sb, sd + 2 + oo) | (hi << 8);
     const uint32_t sc = (lds_u8(sb, sd + 74 + g) >> (4 * (kq >> 1))) & 15u;
     const float d = h2f(lds_u16(sb, sd + 0)) * (0.5f + (float)sc) * 0.25f;
-    grid8(tbl, qi, d, 0.f, tbl_words(tbl, kGridB + lds_u8(sb, sd + 34 + oo) * 16), o);
+    grid8<true>(tbl, qi, d, 0.f, tbl_words(tbl, kGridB + lds_u8(sb, sd + 34 + oo) * 16), o);
   }
 };
 
@@ -246,7 +255,7 @@ struct QmmDec<IQ1_S, A4> {
     const float d = h2f(lds_u16(sb, sd + 0)) * (float)(2u * ((h >> 12) & 7u) + 1u);
     const float dd = (h & 32768u) ? -0.125f * d : 0.125f * d;
     const uint32_t qi = lds_u8(sb, sd + 2 + 4 * g + kq) | (((h >> (3 * kq)) & 7u) << 8);
-    grid8(tbl, qi, d, dd, nullptr, o);
+    grid8<false>(tbl, qi, d, dd, nullptr, o);
   }
 };
 
@@ -266,7 +275,7 @@ struct QmmDec<IQ1_M, A4> {
     const uint32_t ww = (sci >> 2) == 0 ? w0 : ((sci >> 2) == 1 ? w1 : ((sci >> 2) == 2 ? w2 : w3));
     const uint32_t sc = (ww >> (3 * (sci & 3))) & 7u;
     const float d = h2f(dbits) * (float)(2u * sc + 1u);
-    grid8(tbl, qi, d, (hn & 8u) ? -0.125f * d : 0.125f * d, nullptr, o);
+    grid8<false>(tbl, qi, d, (hn & 8u) ? -0.125f * d : 0.125f * d, nullptr, o);
   }
 };
 

@@ -631,6 +631,12 @@ __global__ void __launch_bounds__(256) qmm_generic_kernel(QmmArgs a) {
     }
 }
 
+}  // namespace gsq
+
+#include "gsq_qmm_small.h"
+
+namespace gsq {
+
 // ---- host side --------------------------------------------------------------------------
 extern QmmTuning g_qmm_tuning;
 
@@ -706,6 +712,38 @@ static hipError_t launch_mfma(QmmMfmaArgs& a, int num_cus, const QmmWorkspace& w
   }
 }
 
+template <int T, int WV, int NB>
+static hipError_t launch_qms_a4(const QmsArgs& a, bool a4, hipStream_t s) {
+  if constexpr (BlockBytes<T>::v % 4 == 0) {
+    if (a4) return launch_qms_t<T, true, WV, NB>(a, s);
+  }
+  return launch_qms_t<T, false, WV, NB>(a, s);
+}
+
+// Plan and launch the small-batch kernel for type T (M <= 16): row groups of WV * 16 * NB
+// rows (8 waves of 16 rows unless the tuning asks otherwise), units divided over at most one
+// workgroup per CU, at least min_cols columns each.
+template <int T>
+static hipError_t launch_qms(QmsArgs& a, int num_cus, const QmmWorkspace& ws, hipStream_t s) {
+  if (a.tbl_bytes != qmm_tbl_bytes<T>()) return hipErrorInvalidValue;
+  const int wv = g_qmm_tuning.small_waves == 4 ? 4 : 8;
+  const int nb = g_qmm_tuning.small_nb == 2 ? 2 : 1;
+  const int rg = wv * 16 * nb;
+  const long long units = (((long long)a.N + rg - 1) / rg) * a.nblk;
+  if (units >= (1ll << 31)) return hipErrorInvalidValue;
+  a.units = (int)units;
+  const int min_cols = g_qmm_tuning.small_min_cols > 0 ? g_qmm_tuning.small_min_cols : 1;
+  const int gmax = (a.units + min_cols - 1) / min_cols;
+  a.G = num_cus < gmax ? num_cus : gmax;
+  if (a.G > ws.max_groups) a.G = ws.max_groups;
+  a.xcd_remap = (a.G % 8 == 0) ? 1 : 0;
+  a.part = ws.part;
+  a.cnt = ws.cnt;
+  const bool a4 = (reinterpret_cast<uintptr_t>(a.packed) & 3) == 0;
+  if (wv == 8) return nb == 2 ? launch_qms_a4<T, 8, 2>(a, a4, s) : launch_qms_a4<T, 8, 1>(a, a4, s);
+  return nb == 2 ? launch_qms_a4<T, 4, 2>(a, a4, s) : launch_qms_a4<T, 4, 1>(a, a4, s);
+}
+
 template <int T>
 static hipError_t launch_generic_t(const QmmArgs& a, hipStream_t s) {
   dim3 grid((unsigned)((a.N + kGBN - 1) / kGBN), (unsigned)((a.M + kGBM - 1) / kGBM));
@@ -717,6 +755,25 @@ template <int T>
 static hipError_t launch_qmm_type(const uint8_t* packed, const void* x, int xdt, void* y, int ydt, int64_t M,
                                   int64_t N, int K, const DevTables& tb, int num_cus, const QmmWorkspace& ws,
                                   hipStream_t s) {
+  const int small_max = g_qmm_tuning.small_max_m == 0 ? 16 : g_qmm_tuning.small_max_m;
+  if (xdt == QDT_F16 && ws.part && M >= 1 && M <= small_max && M <= 16 && N < (1ll << 31)) {
+    QmsArgs a{};
+    a.packed = packed;
+    a.x = static_cast<const _Float16*>(x);
+    a.y = y;
+    a.M = (int)M;
+    a.N = (int)N;
+    a.K = K;
+    a.y_dtype = ydt;
+    a.nblk = K / 256;
+    a.row_bytes = (long long)a.nblk * BlockBytes<T>::v;
+    if (qmm_grid_type(T)) {
+      if (!tb.qmv_tbl) return hipErrorInvalidValue;
+      a.tbl = tb.qmv_tbl;
+      a.tbl_bytes = qmv_table_bytes(T);
+    }
+    return launch_qms<T>(a, num_cus, ws, s);
+  }
   if (xdt == QDT_F16 && ws.part && M < (1ll << 31) && N < (1ll << 31)) {
     QmmMfmaArgs a{};
     a.packed = packed;

@@ -37,6 +37,19 @@ def _check_tensors(x, packed):
         raise ValueError("x and packed must be on the same GPU device")
 
 
+# gfx950 routing beyond the reference's row threshold: from 3 fp16 rows on, a large matrix is
+# faster through gsq_qmm's small-batch kernel (weights decoded once for all rows) than through
+# the vector kernel (whose dot-product work grows with the rows); small matrices stay on the
+# vector kernel, whose fixed cost is lower.
+SMALL_BATCH_MIN_ROWS = 3
+SMALL_BATCH_MIN_WEIGHTS = 1 << 24
+
+
+def _small_batch_faster(rows, dtype, out_features, in_features):
+    return (dtype == torch.float16 and SMALL_BATCH_MIN_ROWS <= rows
+            and out_features * in_features >= SMALL_BATCH_MIN_WEIGHTS)
+
+
 def quantized_matvec(x, packed, *, qtype: str, out_features: int, in_features: int, out_dtype=None):
     """y = x @ W.T for packed ``W`` of shape ``(out_features, in_features)``.
 
@@ -50,7 +63,7 @@ def quantized_matvec(x, packed, *, qtype: str, out_features: int, in_features: i
     # the fused QMV keeps a row's activations in registers: K <= 65536 for fp16 activations,
     # K <= 32768 for fp32/bf16 (split into two fp16 parts); wider rows go to the tiled QMM
     max_k = 65536 if x.dtype == torch.float16 else 32768
-    if rows >= QMM_MIN_ROWS or in_features > max_k:
+    if rows >= QMM_MIN_ROWS or in_features > max_k or _small_batch_faster(rows, x.dtype, out_features, in_features):
         return quantized_matmul(flat, packed, qtype=qtype, out_features=out_features,
                                 in_features=in_features, out_dtype=out_dtype).reshape(*original, out_features)
     if qtype not in QTYPES:

@@ -177,6 +177,56 @@ def test_qmm_multi_tile_shapes(qtype, shape):
     np.testing.assert_allclose(y, want, rtol=2e-3, atol=2e-3 * scale)
 
 
+# Small batches (M <= 16) take the small-batch kernel: row groups of 128 weight rows split
+# over the K columns of as many workgroups as there are CUs, partial sums of a group summed by
+# the last workgroup to finish it. Shapes cover groups split over many workgroups, a ragged
+# last group, one column per workgroup and 27B row widths.
+SMALL_SHAPES = [
+    (1, 1024, 5120),
+    (2, 200, 2048),
+    (5, 1000, 4096),
+    (11, 520, 17408),
+    (16, 5120, 1024),
+]
+
+
+@pytest.mark.parametrize("qtype", QTYPES)
+@pytest.mark.parametrize("shape", SMALL_SHAPES)
+def test_qmm_small_batch_shapes(qtype, shape):
+    from mlx_gsq_amd.runtime.kernels.qmm import quantized_matmul
+    M, N, K = shape
+    print(f"qmm small {qtype} M={M} N={N} K={K}", flush=True)
+    packed = synth.make_packed(qtype, N, K, seed=29)
+    x = synth.make_x(M, K, seed=13, dtype=np.float16)
+    y = quantized_matmul(dev(x), dev(packed), qtype=qtype, out_features=N, in_features=K,
+                         out_dtype=torch.float32).cpu().numpy()
+    want = O.matmul_reference(x, packed, qtype, N, K, TABLES.get(qtype))
+    assert rel_l2(y, want) <= 1e-3, rel_l2(y, want)
+    scale = np.abs(want).max()
+    np.testing.assert_allclose(y, want, rtol=2e-3, atol=2e-3 * scale)
+
+
+@pytest.mark.parametrize("qtype", QTYPES)
+def test_qmm_small_batch_unaligned_deterministic_fp16_out(qtype):
+    """Small batch on a 2-byte aligned packed view: two launches bit-identical, fp16 output
+    within 1e-2 of the oracle."""
+    from mlx_gsq_amd.runtime.kernels.qmm import quantized_matmul
+    M, N, K = 6, 700, 3072
+    print(f"qmm small unaligned {qtype}", flush=True)
+    packed = synth.make_packed(qtype, N, K, seed=41)
+    big = torch.zeros(packed.size + 64, dtype=torch.uint8, device="cuda")
+    big[10:10 + packed.size] = dev(packed)
+    view = big[10:10 + packed.size]
+    xd = dev(synth.make_x(M, K, seed=3, dtype=np.float16))
+    y1 = quantized_matmul(xd, view, qtype=qtype, out_features=N, in_features=K, out_dtype=torch.float32)
+    y2 = quantized_matmul(xd, view, qtype=qtype, out_features=N, in_features=K, out_dtype=torch.float32)
+    assert torch.equal(y1, y2)
+    want = O.matmul_reference(xd.cpu().numpy(), packed, qtype, N, K, TABLES.get(qtype))
+    assert rel_l2(y1.cpu().numpy(), want) <= 1e-3
+    y16 = quantized_matmul(xd, view, qtype=qtype, out_features=N, in_features=K).float().cpu().numpy()
+    assert rel_l2(y16, want) <= 1e-2
+
+
 @pytest.mark.parametrize("qtype", QTYPES)
 def test_qmm_unaligned_packed_view_deterministic(qtype):
     """A 2-byte aligned packed view (no 4-byte word reads, superblocks at every offset within

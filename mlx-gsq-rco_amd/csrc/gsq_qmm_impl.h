@@ -756,7 +756,8 @@ static hipError_t launch_qmm_type(const uint8_t* packed, const void* x, int xdt,
                                   int64_t N, int K, const DevTables& tb, int num_cus, const QmmWorkspace& ws,
                                   hipStream_t s) {
   const int small_max = g_qmm_tuning.small_max_m == 0 ? 16 : g_qmm_tuning.small_max_m;
-  if (xdt == QDT_F16 && ws.part && M >= 1 && M <= small_max && M <= 16 && N < (1ll << 31)) {
+  const bool x16 = (reinterpret_cast<uintptr_t>(x) & 15) == 0;  // the MFMA kernels read 16-byte pieces
+  if (xdt == QDT_F16 && x16 && ws.part && M >= 1 && M <= small_max && M <= 16 && N < (1ll << 31)) {
     QmsArgs a{};
     a.packed = packed;
     a.x = static_cast<const _Float16*>(x);
@@ -774,7 +775,7 @@ static hipError_t launch_qmm_type(const uint8_t* packed, const void* x, int xdt,
     }
     return launch_qms<T>(a, num_cus, ws, s);
   }
-  if (xdt == QDT_F16 && ws.part && M < (1ll << 31) && N < (1ll << 31)) {
+  if (xdt == QDT_F16 && x16 && ws.part && M < (1ll << 31) && N < (1ll << 31)) {
     QmmMfmaArgs a{};
     a.packed = packed;
     a.x = static_cast<const _Float16*>(x);

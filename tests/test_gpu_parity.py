@@ -227,6 +227,24 @@ def test_qmm_small_batch_unaligned_deterministic_fp16_out(qtype):
     assert rel_l2(y16, want) <= 1e-2
 
 
+@pytest.mark.parametrize("rows", [4, 40])
+def test_qmm_activations_not_16_byte_aligned(rows):
+    """fp16 activations at an 8-byte offset take the generic kernel (the MFMA kernels read
+    16-byte pieces of x); same results within tolerance."""
+    from mlx_gsq_amd.runtime.kernels.qmm import quantized_matmul
+    N, K = 300, 1024
+    packed = synth.make_packed("IQ3_S", N, K, seed=2)
+    x = synth.make_x(rows, K, seed=4, dtype=np.float16)
+    big = torch.zeros(x.size + 8, dtype=torch.float16, device="cuda")
+    big[4:4 + x.size] = dev(x).reshape(-1)
+    xv = big[4:4 + x.size].reshape(rows, K)
+    assert xv.data_ptr() % 16 == 8
+    y = quantized_matmul(xv, dev(packed), qtype="IQ3_S", out_features=N, in_features=K,
+                         out_dtype=torch.float32).cpu().numpy()
+    want = O.matmul_reference(x, packed, "IQ3_S", N, K, TABLES["IQ3_S"])
+    assert rel_l2(y, want) <= 1e-3
+
+
 @pytest.mark.parametrize("qtype", QTYPES)
 def test_qmm_unaligned_packed_view_deterministic(qtype):
     """A 2-byte aligned packed view (no 4-byte word reads, superblocks at every offset within

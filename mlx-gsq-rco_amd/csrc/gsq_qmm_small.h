@@ -205,9 +205,25 @@ qms_kernel(QmsArgs args) {
         float4_t sum[NB];
 #pragma unroll
         for (int j = 0; j < NB; ++j) sum[j] = (float4_t){0.f, 0.f, 0.f, 0.f};
-        for (int v = wf; v <= wl; ++v) {
-          const int vs = 2 * v + (grp == qmm_first_col(v, units, G) / nblk ? 0 : 1);
-          const __amdgpu_buffer_rsrc_t pv = qmm_slot_rsrc(part, vs);
+        // workgroups after wf start inside this group (their slot 2v); wf may have started in
+        // an earlier one. Four workgroups' loads in flight at a time, summed in order.
+        const int s0 = 2 * wf + (qmm_first_col(wf, units, G) / nblk == grp ? 0 : 1);
+        int v = wf;
+        for (; v + 3 <= wl; v += 4) {
+          float4_t ld[4][NB];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const __amdgpu_buffer_rsrc_t pv = qmm_slot_rsrc(part, v + t == wf ? s0 : 2 * (v + t));
+#pragma unroll
+            for (int j = 0; j < NB; ++j) ld[t][j] = qmm_ld_coherent(pv, (j * TH + tid) * 16);
+          }
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int j = 0; j < NB; ++j) sum[j] += ld[t][j];
+        }
+        for (; v <= wl; ++v) {
+          const __amdgpu_buffer_rsrc_t pv = qmm_slot_rsrc(part, v == wf ? s0 : 2 * v);
 #pragma unroll
           for (int j = 0; j < NB; ++j) sum[j] += qmm_ld_coherent(pv, (j * TH + tid) * 16);
         }

@@ -37,17 +37,20 @@ def _check_tensors(x, packed):
         raise ValueError("x and packed must be on the same GPU device")
 
 
-# gfx950 routing beyond the reference's row threshold: from 3 fp16 rows on, a large matrix is
-# faster through gsq_qmm's small-batch kernel (weights decoded once for all rows) than through
-# the vector kernel (whose dot-product work grows with the rows); small matrices stay on the
-# vector kernel, whose fixed cost is lower.
-SMALL_BATCH_MIN_ROWS = 3
-SMALL_BATCH_MIN_WEIGHTS = 1 << 24
+# gfx950 routing beyond the reference's row threshold: from 4 fp16 rows on (3 for matrices of
+# at least 2^24 weights) gsq_qmm's small-batch kernel, which decodes the weights once for all
+# rows, is faster than the vector kernel, whose dot-product work grows with the rows.
+SMALL_BATCH_MIN_ROWS = 4
+SMALL_BATCH_LARGE_MIN_ROWS = 3
+SMALL_BATCH_LARGE_WEIGHTS = 1 << 24
 
 
 def _small_batch_faster(rows, dtype, out_features, in_features):
-    return (dtype == torch.float16 and SMALL_BATCH_MIN_ROWS <= rows
-            and out_features * in_features >= SMALL_BATCH_MIN_WEIGHTS)
+    if dtype != torch.float16:
+        return False
+    if out_features * in_features >= SMALL_BATCH_LARGE_WEIGHTS:
+        return rows >= SMALL_BATCH_LARGE_MIN_ROWS
+    return rows >= SMALL_BATCH_MIN_ROWS
 
 
 def quantized_matvec(x, packed, *, qtype: str, out_features: int, in_features: int, out_dtype=None):

@@ -20,6 +20,7 @@ Printed JSON line (one, on stdout):
                 TFLOP/s and fraction of the 2.5 PFLOP/s dense fp16 MFMA peak per case
   layer_crossover  configs[3]: QMV vs QMM time per projection of the mixed layer, M in 1..16
   decode_stack  configs[4]: 448 GEMVs (64 layers, 8.34 GB) in one HIP graph: GB/s, tokens/s
+  decode_stack_fused  the same products with q|k and gate|up fused (320 launches)
   cpu_baseline  the numpy oracle (dequant + float32 matmul, one thread) on a bounded sample
 
 Algorithmic bytes per QMV launch = N*(K/256)*block_bytes + M*K*2 (x fp16) + M*N*4 (y fp32).
@@ -345,22 +346,30 @@ def run_embedding(device, vocab=248320, dims=5120, tokens=(1, 4096), reps=20):
     return {"table": f"IQ2_S {vocab}x{dims}", "out": "bf16", **res}
 
 
-def run_stack(device, layers=64, reps=10):
+# The mixed layer with the projections that share a type and an input fused (q|k, gate|up):
+# the same weights and bytes in 5 launches per layer instead of 7 (GSQFusedLinear).
+LAYER_FUSED = (("qk", "IQ2_XS", 6144, 5120), ("v", "IQ4_XS", 1024, 5120), ("o", "IQ3_S", 5120, 5120),
+               ("gateup", "IQ2_S", 34816, 5120), ("down", "Q4_K", 5120, 17408))
+
+
+def run_stack(device, layers=64, reps=10, fused=False):
     """one decode token of the 448 projection GEMVs (64 layers x the 7 projections of
     the mixed layer, distinct random weights per layer, 8.34 GB resident) at M=1, captured in one
-    HIP graph and replayed; aggregate GB/s and implied linear-layer tokens/s."""
+    HIP graph and replayed; aggregate GB/s and implied linear-layer tokens/s. fused: the same
+    products with q|k and gate|up as one launch each (320 launches)."""
     import torch
     from mlx_gsq_amd import _lib
     from mlx_gsq_amd.formats import TYPE_IDS
     lib = _lib.lib()
     stream = torch.cuda.current_stream(device)
     mats, total = [], 0
+    spec = LAYER_FUSED if fused else LAYER
     xs = {k: torch.randn(1, k, device=device).half() for k in (5120, 17408)}
-    ys = {n: torch.empty(1, n, device=device, dtype=torch.float32) for n in (1024, 5120, 17408)}
-    for (_, q, _, _) in LAYER:
+    ys = {n: torch.empty(1, n, device=device, dtype=torch.float32) for (_, _, n, _) in spec}
+    for (_, q, _, _) in spec:
         _lib.ensure_tables(q, device)
     for layer in range(layers):
-        for (name, q, n, k) in LAYER:
+        for (name, q, n, k) in spec:
             p = make_device_packed(q, n, k, seed=5000 + len(mats), device=device)
             mats.append((TYPE_IDS[q], p, n, k))
             total += qmv_bytes(q, n, k)
@@ -390,10 +399,12 @@ def run_stack(device, layers=64, reps=10):
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / reps
     gbs = total / (ms * 1e-3) / 1e9
-    res = {"gemvs": len(mats), "bytes": int(total), "ms_per_token": round(ms, 4), "GB/s": round(gbs, 1),
+    res = {"gemvs": len(mats) if not fused else 7 * layers, "launches": len(mats), "bytes": int(total),
+           "ms_per_token": round(ms, 4), "GB/s": round(gbs, 1),
            "frac": round(gbs / HBM_PEAK_GBS, 4), "linear_tokens_per_s": round(1e3 / ms, 1),
            "mix": "per layer: q 5120x5120 IQ2_XS, k/v 1024x5120 IQ2_XS/IQ4_XS, o 5120x5120 IQ3_S, "
-                  "gate/up 17408x5120 IQ2_S, down 5120x17408 Q4_K"}
+                  "gate/up 17408x5120 IQ2_S, down 5120x17408 Q4_K"
+                  + ("; q|k and gate|up fused into one launch each" if fused else "")}
     del mats
     torch.cuda.empty_cache()
     return res
@@ -519,6 +530,7 @@ def main():
     qmm = {} if args.no_qmm else run_qmm(device)
     crossover = {} if args.no_layer else run_crossover(device)
     stack = {} if args.no_layer else run_stack(device)
+    stack_fused = {} if args.no_layer else run_stack(device, fused=True)
     emb = {} if args.no_layer else run_embedding(device)
     cpu = None if args.no_cpu else cpu_baseline()
     from mlx_gsq_amd.formats import QTYPES
@@ -563,6 +575,7 @@ def main():
         "qmm": qmm,
         "layer_crossover": crossover,
         "decode_stack": stack,
+        "decode_stack_fused": stack_fused,
         "embedding": emb,
         "cpu_baseline": cpu,
     }

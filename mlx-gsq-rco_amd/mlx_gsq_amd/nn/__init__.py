@@ -1,5 +1,5 @@
 """Packed-weight modules."""
 from .embedding import GSQEmbedding
-from .linear import GSQLinear
+from .linear import GSQFusedLinear, GSQLinear
 
-__all__ = ["GSQEmbedding", "GSQLinear"]
+__all__ = ["GSQEmbedding", "GSQFusedLinear", "GSQLinear"]

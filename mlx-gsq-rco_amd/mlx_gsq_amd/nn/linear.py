@@ -35,3 +35,52 @@ class GSQLinear(torch.nn.Module):
 
     def extra_repr(self) -> str:
         return f"in_features={self.in_features}, out_features={self.out_features}, qtype={self.qtype}"
+
+
+class GSQFusedLinear(torch.nn.Module):
+    """Several packed linears of one quantization type and input width applied to the same
+    input in one launch (q/k, gate/up of a decoder layer).
+
+    Packed rows are whole superblocks, row-major, so concatenating the matrices along the
+    output dimension is a byte concatenation; it is done once here, on the weights' device.
+    ``forward`` returns one output per weight (views of one result), computed exactly as
+    ``GSQLinear`` computes the concatenated matrix (one row → QMV, more → QMM). No counterpart
+    in the reference, whose model applies each projection on its own.
+    """
+
+    def __init__(self, weights, biases=None):
+        super().__init__()
+        weights = list(weights)
+        if not weights:
+            raise ValueError("no weights to fuse")
+        qtypes = {w.quantization_type for w in weights}
+        widths = {w.logical_shape[1] for w in weights}
+        if len(qtypes) != 1:
+            raise ValueError(f"fused weights must share one quantization type, got {sorted(qtypes)}")
+        if len(widths) != 1:
+            raise ValueError(f"fused weights must share one input width, got {sorted(widths)}")
+        if biases is not None and len(biases) != len(weights):
+            raise ValueError("one bias (or None) per weight")
+        self.qtype = weights[0].quantization_type
+        self.in_features = weights[0].logical_shape[1]
+        self.splits = [w.logical_shape[0] for w in weights]
+        self.out_features = sum(self.splits)
+        self.packed_weight = torch.cat([torch.as_tensor(w.data).reshape(-1) for w in weights])
+        self.biases = biases
+
+    def forward(self, x):
+        rows = x.numel() // self.in_features
+        if rows == 1:
+            y = quantized_matvec(x, self.packed_weight, qtype=self.qtype,
+                                 out_features=self.out_features, in_features=self.in_features)
+        else:
+            y = quantized_matmul(x, self.packed_weight, qtype=self.qtype,
+                                 out_features=self.out_features, in_features=self.in_features)
+        outs = y.split(self.splits, dim=-1)
+        if self.biases is None:
+            return outs
+        return tuple(o if b is None else o + b for o, b in zip(outs, self.biases))
+
+    def extra_repr(self) -> str:
+        return f"in_features={self.in_features}, splits={self.splits}, qtype={self.qtype}"
+

@@ -143,3 +143,27 @@ def test_codebook_file_source(tmp_path, monkeypatch):
     finally:
         tables.clear_tables()
         tables._registered.update(saved)
+
+
+def test_fused_linear_concatenates_rows_and_validates():
+    import torch
+    from mlx_gsq_amd import synth
+    from mlx_gsq_amd.nn import GSQFusedLinear
+    from mlx_gsq_amd.runtime.store import PackedWeight
+
+    def pw(q, n, k, seed, qid, bb):
+        data = torch.from_numpy(synth.make_packed(q, n, k, seed=seed))
+        return PackedWeight(name=f"w{seed}", data=data, gguf_shape=(k, n), logical_shape=(n, k),
+                            quantization_type=q, quantization_type_id=qid, num_elements=n * k,
+                            num_bytes=n * (k // 256) * bb)
+    a, b = pw("IQ2_XS", 32, 512, 1, 17, 74), pw("IQ2_XS", 16, 512, 2, 17, 74)
+    fused = GSQFusedLinear([a, b])
+    assert fused.out_features == 48 and fused.splits == [32, 16] and fused.qtype == "IQ2_XS"
+    assert torch.equal(fused.packed_weight, torch.cat([a.data, b.data]))
+    with pytest.raises(ValueError):
+        GSQFusedLinear([a, pw("IQ4_XS", 16, 512, 3, 23, 136)])
+    with pytest.raises(ValueError):
+        GSQFusedLinear([a, pw("IQ2_XS", 16, 1024, 4, 17, 74)])
+    with pytest.raises(ValueError):
+        GSQFusedLinear([])
+

@@ -29,6 +29,15 @@ def _codebooks():
     yield
 
 
+@pytest.fixture
+def vector_kernel_only(monkeypatch):
+    """Keep quantized_matvec on the vector kernel for every row count below the reference's QMM
+    threshold (it otherwise sends fp16 batches of 3+ rows to the small-batch QMM kernel), so
+    the vector kernel's multi-row variants stay covered at their own tolerance."""
+    from mlx_gsq_amd.runtime.kernels import qmv
+    monkeypatch.setattr(qmv, "_small_batch_faster", lambda *a: False)
+
+
 def rel_l2(a, b):
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)
@@ -64,7 +73,7 @@ def test_dequant_raw_random_bytes(qtype):
 
 @pytest.mark.parametrize("qtype", QTYPES)
 @pytest.mark.parametrize("rows", [1, 2, 3, 4, 5])
-def test_qmv_matches_oracle(qtype, rows):
+def test_qmv_matches_oracle(qtype, rows, vector_kernel_only):
     from mlx_gsq_amd.runtime.kernels.qmv import quantized_matvec
     N, K = 4100, 512  # several rows per workgroup and several staging steps
     print(f"qmv {qtype} M={rows} N={N} K={K}", flush=True)
@@ -106,7 +115,7 @@ def test_qmv_27b_row_widths(qtype, shape):
 
 @pytest.mark.parametrize("qtype", ["Q4_K", "IQ2_S", "IQ3_XXS"])
 @pytest.mark.parametrize("rows", [4, 7])
-def test_qmv_wide_rows_multi_row(qtype, rows):
+def test_qmv_wide_rows_multi_row(qtype, rows, vector_kernel_only):
     """4..7 activation rows of the 17408-wide down projection: more waves per row than the
     4-row variant holds, so the rows go out in 2-row launches."""
     from mlx_gsq_amd.runtime.kernels.qmv import quantized_matvec
@@ -278,6 +287,22 @@ def test_qmm_fp16_output_and_fp32_input(qtype):
     assert rel_l2(y32, want) <= 1e-3
 
 
+@pytest.mark.parametrize("rows,n", [(4, 300), (3, 4096), (2, 4096)])
+def test_matvec_routes_small_fp16_batches(rows, n):
+    """fp16 batches of 4+ rows (3+ on matrices of 2^24+ weights) take the small-batch QMM
+    kernel (fp16-rounded weights, QMM tolerance); 2 rows stay on the vector kernel."""
+    from mlx_gsq_amd.runtime.kernels import qmv
+    K = 4096
+    routed = qmv._small_batch_faster(rows, torch.float16, n, K)
+    assert routed == (rows >= 3 and n * K >= 1 << 24 or rows >= 4)
+    packed = synth.make_packed("Q4_K", n, K, seed=8)
+    x = synth.make_x(rows, K, seed=8, dtype=np.float16)
+    y = qmv.quantized_matvec(dev(x), dev(packed), qtype="Q4_K", out_features=n, in_features=K,
+                             out_dtype=torch.float32).cpu().numpy()
+    want = O.matmul_reference(x, packed, "Q4_K", n, K)
+    assert rel_l2(y, want) <= (1e-3 if routed else 1e-4)
+
+
 def test_matvec_routes_many_rows_to_qmm():
     from mlx_gsq_amd.runtime.kernels.qmv import quantized_matvec
     N, K = 64, 512
@@ -311,6 +336,30 @@ def test_gsq_linear_and_store_roundtrip(tmp_path):
     x4 = synth.make_x(4, K, seed=6, dtype=np.float32)
     y4 = lin(dev(x4)).cpu().numpy()
     assert rel_l2(y4, O.matmul_reference(x4, packed, "IQ2_XS", N, K, TABLES["IQ2_XS"])) <= 1e-3
+
+
+@pytest.mark.parametrize("rows", [1, 5, 12])
+def test_fused_linear_matches_separate_projections(rows):
+    """q|k and gate|up style fusion: one launch over the concatenated packed rows gives each
+    projection's output (oracle tolerance)."""
+    from mlx_gsq_amd.nn import GSQFusedLinear
+    from mlx_gsq_amd.runtime.store import PackedWeight
+    K = 1024
+    shapes = [(512, 17), (128, 18)]
+    ws, packs = [], []
+    for i, (n, seed) in enumerate(shapes):
+        p = synth.make_packed("IQ2_XS", n, K, seed=seed)
+        packs.append(p)
+        ws.append(PackedWeight(name=f"w{i}", data=dev(p), gguf_shape=(K, n), logical_shape=(n, K),
+                               quantization_type="IQ2_XS", quantization_type_id=17, num_elements=n * K,
+                               num_bytes=p.size))
+    fused = GSQFusedLinear(ws)
+    x = synth.make_x(rows, K, seed=6, dtype=np.float32)
+    outs = fused(dev(x))
+    assert [tuple(o.shape) for o in outs] == [(rows, n) for n, _ in shapes]
+    for o, p, (n, _) in zip(outs, packs, shapes):
+        want = O.matmul_reference(x, p, "IQ2_XS", n, K, TABLES["IQ2_XS"])
+        assert rel_l2(o.cpu().numpy(), want) <= 1e-3
 
 
 def test_deterministic_repeat():

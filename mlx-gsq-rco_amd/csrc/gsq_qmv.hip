@@ -24,6 +24,8 @@
 //   applied once per group.
 // * Prologue: the type's LDS table and the activations are fetched once per workgroup (DMA),
 //   behind the first weight slices of every wave.
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -47,7 +49,6 @@ struct QmvArgs {
   int sbuf;         // bytes per ring buffer (cdma KB)
   int cdma;         // DMA instructions per item
   int tbl_bytes, x_off, x_bytes, x_lds, red_off, ring_off;  // LDS layout
-  int pair;         // rows go in pairs (see qmv_kernel)
   DevTables tb;
 };
 
@@ -647,10 +648,9 @@ __device__ __forceinline__ float wave_sum_to_lane63(float v) {
 // Register weight of a variant = activation rows x slices per wave, doubled for
 // split-precision (fp32/bf16) activations, which keep two fp16 parts per value. Workgroups
 // shrink as the weight grows so that no variant spills: weight <= 2: 16 waves, 3: 12 waves,
-// 4 and more: 8 waves.
+// 4 and more: 8 waves (16 waves of weight 3 measured no faster than 12).
 constexpr int qmv_weight(int mr, int gl, bool xs) { return mr * gl * (xs ? 2 : 1); }
 constexpr int qmv_max_threads(int w) { return w >= 4 ? 512 : (w == 3 ? 768 : 1024); }
-template <int W> struct QmvBounds { static constexpr int v = qmv_max_threads(W); };
 constexpr int kMaxRing = 16;
 
 template <int T, int MR, bool XS>
@@ -706,13 +706,8 @@ struct QmvTblLds<0> {
   __device__ __forceinline__ static uint8_t* get() { return nullptr; }
 };
 
-// PR2 (one fp16 activation row, K = 5120: 20 superblocks = 2.5 slices per row): an item is
-// two neighbouring rows A and B, decoded as five full slices per lane instead of 2 x 3 with
-// half of every third slice idle: slices 0 and 1 of A, slices 0 and 1 of B, and a shared
-// tail slice whose lanes 0-31 take A's last 4 superblocks and lanes 32-63 B's. Every row uses
-// the same activations, so the tail slice's activations are those of groups 128 + lane % 32.
-template <int T, int MR, bool XS, int GL, bool A4, bool PR2 = false>
-__global__ void __launch_bounds__(QmvBounds<qmv_weight(MR, GL, XS)>::v) qmv_kernel(QmvArgs a) {
+template <int T, int MR, bool XS, int GL, bool A4>
+__global__ void __launch_bounds__(qmv_max_threads(qmv_weight(MR, GL, XS))) qmv_kernel(QmvArgs a) {
   using P = Qmv<T>;
   constexpr int BB = BlockBytes<T>::v;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -733,18 +728,17 @@ __global__ void __launch_bounds__(QmvBounds<qmv_weight(MR, GL, XS)>::v) qmv_kern
   // r0 + s, r0 + s + slots, ...: at any time the waves of a workgroup read neighbouring rows,
   // one contiguous span of the packed matrix.
   const int slot = wave / a.W, ws = wave - slot * a.W;
-  constexpr int RI = PR2 ? 2 : 1;  // rows per item
-  const int nrow_items = (int)((r1 - r0) / RI);
+  const int nrow_items = (int)(r1 - r0);
   const bool live = slot < a.slots && slot < nrow_items;
   const int sl0 = ws * GL;
   const int nq = live ? max(0, min(GL, a.nslices - sl0)) : 0;
   const int nbk = min(8 * GL, a.nblk - sl0 * 8);             // superblocks per item (per row)
-  const int item_bytes = PR2 ? 2 * a.row_bytes : nbk * BB;
+  const int item_bytes = nbk * BB;
   const int nitems = nq > 0 ? (nrow_items - slot + a.slots - 1) / a.slots : 0;
-  // item t = K range of row(s) r0 + RI * (slot + t * slots)
-  const int64_t row0 = r0 + RI * slot;
+  // item t = K range of row r0 + slot + t * slots
+  const int64_t row0 = r0 + slot;
   const uintptr_t base = reinterpret_cast<uintptr_t>(a.packed) + (uintptr_t)(row0 * a.row_bytes + (int64_t)sl0 * 8 * BB);
-  const uintptr_t stride = (uintptr_t)a.row_bytes * (uintptr_t)(RI * a.slots);
+  const uintptr_t stride = (uintptr_t)a.row_bytes * (uintptr_t)a.slots;
 
   // ---- prologue: the table and the activations (once per workgroup), then this wave's first
   // item; the ring fills up gradually (below). A wave that queued its whole ring at once would
@@ -763,7 +757,7 @@ __global__ void __launch_bounds__(QmvBounds<qmv_weight(MR, GL, XS)>::v) qmv_kern
   XReg<MR, XS, P::kSums> xr[GL];
 #pragma unroll
   for (int q = 0; q < GL; ++q) {
-    const int u = PR2 ? (q < 2 ? q * 64 + lane : 128 + (lane & 31)) : (sl0 + q) * 64 + lane;
+    const int u = (sl0 + q) * 64 + lane;
     const bool act = q < nq && u < (a.K >> 5);
     if (a.x_lds) qmv_load_x1<T, MR, XS>(xr[q], act, act ? u : 0, xst, a.x_dtype, a.K, a.M);
     else qmv_load_x1<T, MR, XS>(xr[q], act, act ? u : 0, a.x, a.x_dtype, a.K, a.M);
@@ -779,40 +773,9 @@ __global__ void __launch_bounds__(QmvBounds<qmv_weight(MR, GL, XS)>::v) qmv_kern
 #pragma unroll 1
     for (int k = 0; k < 2 && issued < lim; ++k, ++issued)
       dma_item(base + (uintptr_t)issued * stride, item_bytes, a.cdma, ring + (issued % a.nb) * a.sbuf, lane);
-    const int64_t row = row0 + (int64_t)t * RI * a.slots;
+    const int64_t row = row0 + (int64_t)t * a.slots;
     const uint32_t delta = (uint32_t)((base + (uintptr_t)t * stride) & 15u);
     const uint8_t* b = ring + buf * a.sbuf;
-    if constexpr (PR2) {
-      float accA[MR], accB[MR], pt[MR];
-#pragma unroll
-      for (int m = 0; m < MR; ++m) { accA[m] = 0.f; accB[m] = 0.f; pt[m] = 0.f; }
-      const uint32_t rb = (uint32_t)a.row_bytes;
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const uint32_t off = delta + (uint32_t)((q * 8 + (lane >> 3)) * BB);
-        P::template dot<MR, XS, A4>(b, off, lane & 7, tbl, xr[q], accA);
-        P::template dot<MR, XS, A4>(b, off + rb, lane & 7, tbl, xr[q], accB);
-      }
-      const bool rowA = lane < 32;
-      P::template dot<MR, XS, A4>(b, delta + (rowA ? 0u : rb) + (uint32_t)((16 + ((lane & 31) >> 3)) * BB), lane & 7, tbl,
-                                  xr[2], pt);
-#pragma unroll
-      for (int m = 0; m < MR; ++m) {
-        accA[m] += rowA ? pt[m] : 0.f;
-        accB[m] += rowA ? 0.f : pt[m];
-      }
-      if (++buf == a.nb) buf = 0;
-#pragma unroll
-      for (int m = 0; m < MR; ++m) {
-        const float vA = wave_sum_to_lane63(accA[m]);
-        const float vB = wave_sum_to_lane63(accB[m]);
-        if (lane == 63 && m < a.M) {
-          store_y(a.y, a.y_dtype, (int64_t)m * a.N + row, vA);
-          store_y(a.y, a.y_dtype, (int64_t)m * a.N + row + 1, vB);
-        }
-      }
-      continue;
-    }
     float acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = 0.f;
@@ -856,9 +819,9 @@ __global__ void __launch_bounds__(QmvBounds<qmv_weight(MR, GL, XS)>::v) qmv_kern
   }
 }
 
-template <int T, int MR, bool XS, int GL, bool A4, bool PR2 = false>
+template <int T, int MR, bool XS, int GL, bool A4>
 static hipError_t launch_qmv_t(const QmvArgs& a, int grid, int threads, size_t lds, hipStream_t s) {
-  auto k = qmv_kernel<T, MR, XS, GL, A4, PR2>;
+  auto k = qmv_kernel<T, MR, XS, GL, A4>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -882,9 +845,9 @@ static int qmv_gl(int mr, bool xs) {
 }
 
 template <int T, bool A4>
-static hipError_t launch_qmv_variant(const QmvArgs& a, int mr, bool xs, int grid, int threads, size_t lds,
+static hipError_t launch_qmv_variant(const QmvArgs& a, int mr, bool xs, int gl, int grid, int threads, size_t lds,
                                      hipStream_t s) {
-  if (mr == 1 && !xs && a.pair) return launch_qmv_t<T, 1, false, 3, A4, true>(a, grid, threads, lds, s);
+  if (mr == 1 && !xs && gl == 1) return launch_qmv_t<T, 1, false, 1, A4>(a, grid, threads, lds, s);
   if (mr == 1) return xs ? launch_qmv_t<T, 1, true, 1, A4>(a, grid, threads, lds, s) : launch_qmv_t<T, 1, false, 3, A4>(a, grid, threads, lds, s);
   if (mr == 2) return xs ? launch_qmv_t<T, 2, true, 1, A4>(a, grid, threads, lds, s) : launch_qmv_t<T, 2, false, 1, A4>(a, grid, threads, lds, s);
   if (mr == 4 && !xs) return launch_qmv_t<T, 4, false, 1, A4>(a, grid, threads, lds, s);
@@ -894,13 +857,13 @@ static hipError_t launch_qmv_variant(const QmvArgs& a, int mr, bool xs, int grid
 // Types whose superblock size is a multiple of 4 read their fields with plain dword loads when
 // the packed matrix is 4-byte aligned (every superblock then is); the rest funnel-shift.
 template <int T>
-static hipError_t launch_qmv_type(const QmvArgs& a, int mr, bool xs, int grid, int threads, size_t lds,
+static hipError_t launch_qmv_type(const QmvArgs& a, int mr, bool xs, int gl, int grid, int threads, size_t lds,
                                   hipStream_t s) {
   if constexpr (BlockBytes<T>::v % 4 == 0) {
     if ((reinterpret_cast<uintptr_t>(a.packed) & 3) == 0)
-      return launch_qmv_variant<T, true>(a, mr, xs, grid, threads, lds, s);
+      return launch_qmv_variant<T, true>(a, mr, xs, gl, grid, threads, lds, s);
   }
-  return launch_qmv_variant<T, false>(a, mr, xs, grid, threads, lds, s);
+  return launch_qmv_variant<T, false>(a, mr, xs, gl, grid, threads, lds, s);
 }
 
 int qmv_table_bytes(int qt) {
@@ -967,8 +930,18 @@ bool build_qmv_table(int qt, const uint16_t* grid16, const uint8_t* ksigns, std:
 static constexpr int kLdsBytes = 160 * 1024;
 
 // Launch-plan parameters: waves per workgroup, in-flight bytes per CU the ring depth aims
-// for, workgroups per CU, row pairing allowed.
-QmvTuning g_qmv_tuning = {12, 96 * 1024, 1, 1};
+// for, workgroups per CU.
+// GSQ_QMV_TUNING="waves,inflight_kib,wg_per_cu,gl1_rows,gl1_waves" overrides the defaults (read once, at library
+// load), for measuring launch plans without a rebuild.
+static QmvTuning qmv_tuning_from_env() {
+  QmvTuning t = {12, 96 * 1024, 1, 5120, 12};
+  if (const char* s = std::getenv("GSQ_QMV_TUNING")) {
+    int v[5];
+    if (std::sscanf(s, "%d,%d,%d,%d,%d", &v[0], &v[1], &v[2], &v[3], &v[4]) == 5) t = {v[0], v[1] * 1024, v[2], v[3], v[4]};
+  }
+  return t;
+}
+QmvTuning g_qmv_tuning = qmv_tuning_from_env();
 
 // Activation rows per launch: up to 4 for fp16 activations, 2 for fp32/bf16.
 static int qmv_rows_per_launch(int xdt) { return xdt == DT_F16 ? 4 : 2; }
@@ -984,7 +957,10 @@ static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, 
   a.row_bytes = a.nblk * bb;
   a.nslices = (a.nblk + 7) / 8;
   const bool xs = xdt != DT_F16;
-  const int gl = qmv_gl(mr, xs);
+  int gl = qmv_gl(mr, xs);
+  // one fp16 row of at most 3 slices and few rows: one slice per wave (3 waves per row)
+  const bool gl1 = mr == 1 && !xs && a.nslices <= 3 && N <= g_qmv_tuning.gl1_rows;
+  if (gl1) gl = 1;
   a.W = (a.nslices + gl - 1) / gl;
   const int wpc = g_qmv_tuning.wg_per_cu < 1 ? 1 : g_qmv_tuning.wg_per_cu;
   const int max_waves = qmv_max_threads(qmv_weight(mr, gl, xs)) / 64;
@@ -993,7 +969,8 @@ static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, 
   const int lds_cap = kLdsBytes / wpc;
   a.x_bytes = M * K * (xdt == DT_F32 ? 4 : 2);
   // waves: as many as the variant allows (a multiple of W) unless the tuning asks for fewer
-  int nw = g_qmv_tuning.waves < 1 ? 1 : g_qmv_tuning.waves;
+  int nw = gl1 ? g_qmv_tuning.gl1_waves : g_qmv_tuning.waves;
+  if (nw < 1) nw = 1;
   if (nw > max_waves) nw = max_waves;
   if (a.W > max_waves) return hipErrorInvalidValue;
   if (nw < a.W) nw = a.W;
@@ -1002,15 +979,9 @@ static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, 
   int grid = num_cus * wpc;
   if (N < grid) grid = (int)N;
   a.rows_per_wg = (int)((N + grid - 1) / grid);
-  // rows in pairs where a row is 2.5 slices of one wave (one fp16 activation row, even N),
-  // once every row slot takes two or more pairs; whole pairs in every workgroup
-  a.pair = (g_qmv_tuning.pair && mr == 1 && !xs && a.nslices == gl && a.nblk == 8 * (gl - 1) + 4 &&
-            (N & 1) == 0 && a.rows_per_wg >= 4 * a.slots) ? 1 : 0;
-  if (a.pair && (a.rows_per_wg & 1)) ++a.rows_per_wg;
   grid = (int)((N + a.rows_per_wg - 1) / a.rows_per_wg);
-  // item: GL slices of a row, or a pair of rows (+15 bytes of granule alignment, +4 of decoder
-  // over-read)
-  const int item_bytes = a.pair ? 2 * a.row_bytes : (a.nblk < 8 * gl ? a.nblk : 8 * gl) * bb;
+  // item: GL slices of a row (+15 bytes of granule alignment, +4 of decoder over-read)
+  const int item_bytes = (a.nblk < 8 * gl ? a.nblk : 8 * gl) * bb;
   a.cdma = (item_bytes + 19 + 1023) / 1024;
   a.sbuf = a.cdma * 1024;
   const int red_bytes = a.W > 1 ? ((a.rows_per_wg * mr * a.W * 4 + 15) & ~15) : 0;
@@ -1020,7 +991,7 @@ static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, 
   a.red_off = a.x_off + (a.x_lds ? a.x_bytes : 0);
   a.ring_off = a.red_off + red_bytes;
   int nb = (lds_cap - a.ring_off) / (nw * a.sbuf);
-  // large (paired) items: fewer waves rather than a ring of one buffer
+  // large items: fewer waves rather than a ring of one buffer
   while (nb < 2 && nw > a.W) {
     nw -= a.W;
     a.slots = nw / a.W;
@@ -1038,17 +1009,17 @@ static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, 
   if (lds_all > (size_t)lds_cap) return hipErrorInvalidValue;
   const size_t lds = lds_all - (size_t)a.tbl_bytes;  // dynamic part: the table is static LDS
   switch (qt) {
-    case Q2_K: return launch_qmv_type<Q2_K>(a, mr, xs, grid, threads, lds, s);
-    case Q4_K: return launch_qmv_type<Q4_K>(a, mr, xs, grid, threads, lds, s);
-    case Q6_K: return launch_qmv_type<Q6_K>(a, mr, xs, grid, threads, lds, s);
-    case IQ4_XS: return launch_qmv_type<IQ4_XS>(a, mr, xs, grid, threads, lds, s);
-    case IQ3_S: return launch_qmv_type<IQ3_S>(a, mr, xs, grid, threads, lds, s);
-    case IQ3_XXS: return launch_qmv_type<IQ3_XXS>(a, mr, xs, grid, threads, lds, s);
-    case IQ2_XXS: return launch_qmv_type<IQ2_XXS>(a, mr, xs, grid, threads, lds, s);
-    case IQ2_XS: return launch_qmv_type<IQ2_XS>(a, mr, xs, grid, threads, lds, s);
-    case IQ2_S: return launch_qmv_type<IQ2_S>(a, mr, xs, grid, threads, lds, s);
-    case IQ1_S: return launch_qmv_type<IQ1_S>(a, mr, xs, grid, threads, lds, s);
-    case IQ1_M: return launch_qmv_type<IQ1_M>(a, mr, xs, grid, threads, lds, s);
+    case Q2_K: return launch_qmv_type<Q2_K>(a, mr, xs, gl, grid, threads, lds, s);
+    case Q4_K: return launch_qmv_type<Q4_K>(a, mr, xs, gl, grid, threads, lds, s);
+    case Q6_K: return launch_qmv_type<Q6_K>(a, mr, xs, gl, grid, threads, lds, s);
+    case IQ4_XS: return launch_qmv_type<IQ4_XS>(a, mr, xs, gl, grid, threads, lds, s);
+    case IQ3_S: return launch_qmv_type<IQ3_S>(a, mr, xs, gl, grid, threads, lds, s);
+    case IQ3_XXS: return launch_qmv_type<IQ3_XXS>(a, mr, xs, gl, grid, threads, lds, s);
+    case IQ2_XXS: return launch_qmv_type<IQ2_XXS>(a, mr, xs, gl, grid, threads, lds, s);
+    case IQ2_XS: return launch_qmv_type<IQ2_XS>(a, mr, xs, gl, grid, threads, lds, s);
+    case IQ2_S: return launch_qmv_type<IQ2_S>(a, mr, xs, gl, grid, threads, lds, s);
+    case IQ1_S: return launch_qmv_type<IQ1_S>(a, mr, xs, gl, grid, threads, lds, s);
+    case IQ1_M: return launch_qmv_type<IQ1_M>(a, mr, xs, gl, grid, threads, lds, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -101,8 +101,9 @@ def test_qmv_split_precision_inputs(qtype, xdtype):
 
 
 @pytest.mark.parametrize("qtype", QTYPES)
-@pytest.mark.parametrize("shape", [(1024, 5120), (512, 17408)])
+@pytest.mark.parametrize("shape", [(1024, 5120), (5200, 5120), (512, 17408)])
 def test_qmv_27b_row_widths(qtype, shape):
+    """K = 5120 rows go one slice per wave up to 5120 rows and three slices per wave above."""
     from mlx_gsq_amd.runtime.kernels.qmv import quantized_matvec
     N, K = shape
     packed = synth.make_packed(qtype, N, K, seed=7)

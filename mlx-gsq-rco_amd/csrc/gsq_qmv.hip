@@ -653,11 +653,68 @@ constexpr int qmv_weight(int mr, int gl, bool xs) { return mr * gl * (xs ? 2 : 1
 constexpr int qmv_max_threads(int w) { return w >= 4 ? 512 : (w == 3 ? 768 : 1024); }
 constexpr int kMaxRing = 16;
 
+// fp16 x[e0] (low half) and x[e1] (high half) out of the 16 words holding x[0..31], by one
+// byte permute (v_perm_b32 selector bytes 0-3 pick the second source, 4-7 the first).
+__device__ __forceinline__ uint32_t half_pair(const uint32_t (&w)[16], int e0, int e1) {
+  const uint32_t b0 = 2u * (uint32_t)(e0 & 1), b2 = 4u + 2u * (uint32_t)(e1 & 1);
+  const uint32_t sel = b0 | ((b0 + 1u) << 8) | (b2 << 16) | ((b2 + 1u) << 24);
+  return __builtin_amdgcn_perm(w[e1 >> 1], w[e0 >> 1], sel);
+}
+
 template <int T, int MR, bool XS>
 __device__ __forceinline__ void qmv_load_x1(XReg<MR, XS, Qmv<T>::kSums>& xr, bool act, int u, const void* x, int dt,
                                             int K, int M) {
   constexpr int NS = Qmv<T>::kSums;
   using P = Qmv<T>;
+  if constexpr (!XS) {
+    // fp16 activations (the only input of the !XS variants): the pairs are byte permutes of
+    // the loaded words and the partial sums v_dot2 against (1, 1), with no conversions
+    (void)dt;
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      uint32_t w[16];
+      if (act && m < M) {
+        const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(x) + (int64_t)m * K + 32 * u);
+        uint4 v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = p[k];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          w[4 * k] = v[k].x; w[4 * k + 1] = v[k].y; w[4 * k + 2] = v[k].z; w[4 * k + 3] = v[k].w;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) w[i] = 0u;
+      }
+      if constexpr (NS > 0) {
+        constexpr uint32_t kOnes = 0x3C003C00u;  // fp16 (1, 1)
+        float s8[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float sm = 0.f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) sm = dot2(w[4 * i + j], kOnes, sm);
+          s8[i] = sm;
+        }
+        if constexpr (NS == 4) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) xr.s8[m][i] = s8[i];
+        } else if constexpr (NS == 2) {
+          xr.s8[m][0] = s8[0] + s8[1];
+          xr.s8[m][1] = s8[2] + s8[3];
+        } else {
+          xr.s8[m][0] = (s8[0] + s8[1]) + (s8[2] + s8[3]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        int e0, e1;
+        pair_idx<P::kPair>(i, e0, e1);
+        xr.h[m][i] = half_pair(w, e0, e1);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
     float xv[32];

@@ -60,13 +60,15 @@ struct DevTables {
 
 // Launch-plan parameters of the QMV kernel: waves per workgroup, target in-flight weight
 // bytes per CU, workgroups per CU, the most rows for which a single fp16 activation row of
-// at most 3 slices goes one slice per wave, and the waves per workgroup of that plan.
+// at most 3 slices goes one slice per wave, the waves per workgroup of that plan, and the
+// most ring items a wave issues per main-loop step.
 struct QmvTuning {
   int waves;
   int inflight_bytes;
   int wg_per_cu;
   int gl1_rows;
   int gl1_waves;
+  int fill;
 };
 
 // Launch-plan overrides of the QMM kernels: activation tile height in 16-row blocks (0 = by

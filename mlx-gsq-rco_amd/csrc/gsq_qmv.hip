@@ -10,7 +10,7 @@
 //   GL*8 superblocks) and keeps their activations in registers as fp16 pairs, permuted to
 //   match the type's decode pairing, with the partial sums the offset terms need. Rows with
 //   more slices are split across W waves (a row slot); each wave reduces its 64 lanes with
-//   DPP, and W > 1 partials are combined once at the end.
+//   DPP into LDS, and the workgroup writes its rows (summing W > 1 partials) once at the end.
 // * Every wave streams its K range of consecutive rows (one "item" per row) through a
 //   private LDS ring with direct-to-LDS DMA loads (global_load_lds_dwordx4), nb-1 items in
 //   flight, and waits only on its own vmcnt: the main loop has no workgroup barriers, so
@@ -48,6 +48,7 @@ struct QmvArgs {
   int nb;           // ring depth per wave (items)
   int sbuf;         // bytes per ring buffer (cdma KB)
   int cdma;         // DMA instructions per item
+  int fill;         // most ring items issued per main-loop step
   int tbl_bytes, x_off, x_bytes, x_lds, red_off, ring_off;  // LDS layout
   DevTables tb;
 };
@@ -776,7 +777,7 @@ __global__ void __launch_bounds__(qmv_max_threads(qmv_weight(MR, GL, XS))) qmv_k
   uint8_t* tbl = QmvTblLds<P::kTbl>::get();
   uint8_t* dyn = smem - a.tbl_bytes;
   uint8_t* xst = dyn + a.x_off;
-  float* red = reinterpret_cast<float*>(dyn + a.red_off);   // [rows_per_wg][MR][W] (W > 1)
+  float* red = reinterpret_cast<float*>(dyn + a.red_off);   // [rows_per_wg][MR][W]
   uint8_t* ring = dyn + a.ring_off + wave * a.nb * a.sbuf;  // this wave's ring
 
   const int64_t r0 = (int64_t)blockIdx.x * a.rows_per_wg;
@@ -828,7 +829,7 @@ __global__ void __launch_bounds__(qmv_max_threads(qmv_weight(MR, GL, XS))) qmv_k
     // item i goes to buffer i % nb, whose previous item (i - nb < t) has been consumed
     const int lim = min(nitems, t + a.nb);
 #pragma unroll 1
-    for (int k = 0; k < 2 && issued < lim; ++k, ++issued)
+    for (int k = 0; k < a.fill && issued < lim; ++k, ++issued)
       dma_item(base + (uintptr_t)issued * stride, item_bytes, a.cdma, ring + (issued % a.nb) * a.sbuf, lane);
     const int64_t row = row0 + (int64_t)t * a.slots;
     const uint32_t delta = (uint32_t)((base + (uintptr_t)t * stride) & 15u);
@@ -855,16 +856,12 @@ __global__ void __launch_bounds__(qmv_max_threads(qmv_weight(MR, GL, XS))) qmv_k
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
       const float v = wave_sum_to_lane63(acc[m]);
-      if (lane == 63) {
-        if (a.W == 1) {
-          if (m < a.M) store_y(a.y, a.y_dtype, (int64_t)m * a.N + row, v);
-        } else {
-          red[(rl * MR + m) * a.W + ws] = v;
-        }
-      }
+      // row sums stay in LDS until the end: a global store here would count against vmcnt
+      // behind the ring's DMA and make the next item's wait also wait for the store
+      if (lane == 63) red[(rl * MR + m) * a.W + ws] = v;
     }
   }
-  if (a.W > 1) {
+  {
     __syncthreads();
     const int nout = (int)(r1 - r0) * MR;
     for (int o = tid; o < nout; o += blockDim.x) {
@@ -988,13 +985,14 @@ static constexpr int kLdsBytes = 160 * 1024;
 
 // Launch-plan parameters: waves per workgroup, in-flight bytes per CU the ring depth aims
 // for, workgroups per CU.
-// GSQ_QMV_TUNING="waves,inflight_kib,wg_per_cu,gl1_rows,gl1_waves" overrides the defaults (read once, at library
+// GSQ_QMV_TUNING="waves,inflight_kib,wg_per_cu,gl1_rows,gl1_waves,fill" overrides the defaults (read once, at library
 // load), for measuring launch plans without a rebuild.
 static QmvTuning qmv_tuning_from_env() {
-  QmvTuning t = {12, 96 * 1024, 1, 5120, 12};
+  QmvTuning t = {12, 96 * 1024, 1, 5120, 15, 1};
   if (const char* s = std::getenv("GSQ_QMV_TUNING")) {
-    int v[5];
-    if (std::sscanf(s, "%d,%d,%d,%d,%d", &v[0], &v[1], &v[2], &v[3], &v[4]) == 5) t = {v[0], v[1] * 1024, v[2], v[3], v[4]};
+    int v[6];
+    if (std::sscanf(s, "%d,%d,%d,%d,%d,%d", &v[0], &v[1], &v[2], &v[3], &v[4], &v[5]) == 6)
+      t = {v[0], v[1] * 1024, v[2], v[3], v[4], v[5]};
   }
   return t;
 }
@@ -1041,7 +1039,7 @@ static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, 
   const int item_bytes = (a.nblk < 8 * gl ? a.nblk : 8 * gl) * bb;
   a.cdma = (item_bytes + 19 + 1023) / 1024;
   a.sbuf = a.cdma * 1024;
-  const int red_bytes = a.W > 1 ? ((a.rows_per_wg * mr * a.W * 4 + 15) & ~15) : 0;
+  const int red_bytes = (a.rows_per_wg * mr * a.W * 4 + 15) & ~15;
   // activations go to LDS only if the ring keeps at least 3 items per wave
   a.x_lds = (a.tbl_bytes + a.x_bytes + red_bytes + nw * 3 * a.sbuf <= lds_cap) ? 1 : 0;
   a.x_off = a.tbl_bytes;
@@ -1061,6 +1059,7 @@ static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, 
   while (nb > 2 && (nb - 2) * a.cdma > 31) --nb;  // exact vmcnt waits go up to 31
   if (nb < 2) return hipErrorInvalidValue;
   a.nb = nb;
+  a.fill = g_qmv_tuning.fill < 1 ? 1 : g_qmv_tuning.fill;
   const int threads = nw * 64;
   const size_t lds_all = (size_t)a.ring_off + (size_t)nw * nb * a.sbuf;
   if (lds_all > (size_t)lds_cap) return hipErrorInvalidValue;

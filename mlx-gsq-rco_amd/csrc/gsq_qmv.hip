@@ -985,14 +985,14 @@ static constexpr int kLdsBytes = 160 * 1024;
 
 // Launch-plan parameters: waves per workgroup, in-flight bytes per CU the ring depth aims
 // for, workgroups per CU.
-// GSQ_QMV_TUNING="waves,inflight_kib,wg_per_cu,gl1_rows,gl1_waves,fill" overrides the defaults (read once, at library
+// GSQ_QMV_TUNING="waves,inflight_kib,wg_per_cu,gl1_rows,gl1_waves,fill,x_lds" overrides the defaults (read once, at library
 // load), for measuring launch plans without a rebuild.
 static QmvTuning qmv_tuning_from_env() {
-  QmvTuning t = {12, 96 * 1024, 1, 5120, 15, 1};
+  QmvTuning t = {12, 96 * 1024, 1, 5120, 15, 1, 1};
   if (const char* s = std::getenv("GSQ_QMV_TUNING")) {
-    int v[6];
-    if (std::sscanf(s, "%d,%d,%d,%d,%d,%d", &v[0], &v[1], &v[2], &v[3], &v[4], &v[5]) == 6)
-      t = {v[0], v[1] * 1024, v[2], v[3], v[4], v[5]};
+    int v[7];
+    if (std::sscanf(s, "%d,%d,%d,%d,%d,%d,%d", &v[0], &v[1], &v[2], &v[3], &v[4], &v[5], &v[6]) == 7)
+      t = {v[0], v[1] * 1024, v[2], v[3], v[4], v[5], v[6]};
   }
   return t;
 }
@@ -1041,7 +1041,7 @@ static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, 
   a.sbuf = a.cdma * 1024;
   const int red_bytes = (a.rows_per_wg * mr * a.W * 4 + 15) & ~15;
   // activations go to LDS only if the ring keeps at least 3 items per wave
-  a.x_lds = (a.tbl_bytes + a.x_bytes + red_bytes + nw * 3 * a.sbuf <= lds_cap) ? 1 : 0;
+  a.x_lds = (g_qmv_tuning.x_lds && a.tbl_bytes + a.x_bytes + red_bytes + nw * 3 * a.sbuf <= lds_cap) ? 1 : 0;
   a.x_off = a.tbl_bytes;
   a.red_off = a.x_off + (a.x_lds ? a.x_bytes : 0);
   a.ring_off = a.red_off + red_bytes;

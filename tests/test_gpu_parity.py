@@ -146,8 +146,9 @@ def test_qmv_unaligned_packed_view_and_odd_rows():
 
 
 @pytest.mark.parametrize("qtype", QTYPES)
-@pytest.mark.parametrize("rows", [8, 16, 33, 182])
+@pytest.mark.parametrize("rows", [8, 16, 33, 100, 128, 182, 257])
 def test_qmm_matches_oracle(qtype, rows):
+    """Activation tiles of 64 (M <= 64), 128 (M <= 128) and 256 rows, ragged and exact."""
     from mlx_gsq_amd.runtime.kernels.qmm import quantized_matmul
     N, K = 200, 512
     print(f"qmm {qtype} M={rows}", flush=True)

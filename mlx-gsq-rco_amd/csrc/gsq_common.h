@@ -61,8 +61,9 @@ struct DevTables {
 // Launch-plan parameters of the QMV kernel: waves per workgroup, target in-flight weight
 // bytes per CU, workgroups per CU, the most rows for which a single fp16 activation row of
 // at most 3 slices goes one slice per wave, the waves per workgroup of that plan, and the
-// most ring items a wave issues per main-loop step, and whether the activations may be
-// staged in LDS (else every wave reads its slices from global memory).
+// most ring items a wave issues per main-loop step, whether the activations may be staged in
+// LDS (else every wave reads its slices from global memory), and whether 2.5-slice rows may be
+// decoded two items at a time.
 struct QmvTuning {
   int waves;
   int inflight_bytes;
@@ -71,6 +72,7 @@ struct QmvTuning {
   int gl1_waves;
   int fill;
   int x_lds;
+  int pair;
 };
 
 // Launch-plan overrides of the QMM kernels: activation tile height in 16-row blocks (0 = by

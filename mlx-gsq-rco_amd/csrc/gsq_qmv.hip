@@ -48,7 +48,8 @@ struct QmvArgs {
   int nb;           // ring depth per wave (items)
   int sbuf;         // bytes per ring buffer (cdma KB)
   int cdma;         // DMA instructions per item
-  int fill;         // most ring items issued per main-loop step
+  int fill;         // most ring items issued per main-loop step (per item pair: 2 x fill)
+  int pair;         // items decoded in pairs (the PR variant of qmv_kernel)
   int tbl_bytes, x_off, x_bytes, x_lds, red_off, ring_off;  // LDS layout
   DevTables tb;
 };
@@ -764,7 +765,13 @@ struct QmvTblLds<0> {
   __device__ __forceinline__ static uint8_t* get() { return nullptr; }
 };
 
-template <int T, int MR, bool XS, int GL, bool A4>
+// PR (one fp16 activation row, K = 5120: 20 superblocks = 2.5 slices per row, one wave per
+// row): the wave's items are decoded two at a time as five full slices instead of 2 x 3 with
+// half of every third slice idle: slices 0 and 1 of items t and t + 1, then one slice whose
+// lanes 0-31 take item t's last 4 superblocks and lanes 32-63 item t + 1's. Both rows use the
+// same activations, so that slice's activations are those of groups 128 + lane % 32. Items
+// stay one row each in the ring (separate buffers).
+template <int T, int MR, bool XS, int GL, bool A4, bool PR = false>
 __global__ void __launch_bounds__(qmv_max_threads(qmv_weight(MR, GL, XS))) qmv_kernel(QmvArgs a) {
   using P = Qmv<T>;
   constexpr int BB = BlockBytes<T>::v;
@@ -815,12 +822,56 @@ __global__ void __launch_bounds__(qmv_max_threads(qmv_weight(MR, GL, XS))) qmv_k
   XReg<MR, XS, P::kSums> xr[GL];
 #pragma unroll
   for (int q = 0; q < GL; ++q) {
-    const int u = (sl0 + q) * 64 + lane;
+    const int u = (PR && q == 2) ? 128 + (lane & 31) : (sl0 + q) * 64 + lane;
     const bool act = q < nq && u < (a.K >> 5);
     if (a.x_lds) qmv_load_x1<T, MR, XS>(xr[q], act, act ? u : 0, xst, a.x_dtype, a.K, a.M);
     else qmv_load_x1<T, MR, XS>(xr[q], act, act ? u : 0, a.x, a.x_dtype, a.K, a.M);
   }
 
+  if constexpr (PR) {
+    // ---- main loop, items in pairs: up to nb - 2 items in flight while a pair is decoded ----
+    for (int t = 0; t < nitems; t += 2) {
+      const int np = min(2, nitems - t);
+      // top the ring up to item t + nb - 1 (the buffers of items < t are consumed), at most
+      // 2 fill items per pair, then wait until items t and t + 1 have landed
+      const int lim = min(nitems, t + a.nb);
+#pragma unroll 1
+      for (int k = 0; k < 2 * a.fill && issued < lim; ++k, ++issued)
+        dma_item(base + (uintptr_t)issued * stride, item_bytes, a.cdma, ring + (issued % a.nb) * a.sbuf, lane);
+      wait_vmcnt((issued - t - np) * a.cdma);
+      const uint8_t* bA = ring + (t % a.nb) * a.sbuf;
+      const uint8_t* bB = np == 2 ? ring + ((t + 1) % a.nb) * a.sbuf : bA;
+      const uint32_t dA = (uint32_t)((base + (uintptr_t)t * stride) & 15u);
+      const uint32_t dB = np == 2 ? (uint32_t)((base + (uintptr_t)(t + 1) * stride) & 15u) : dA;
+      float accA[MR], accB[MR], pt[MR];
+#pragma unroll
+      for (int m = 0; m < MR; ++m) { accA[m] = 0.f; accB[m] = 0.f; pt[m] = 0.f; }
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const uint32_t o = (uint32_t)((q * 8 + (lane >> 3)) * BB);
+        P::template dot<MR, XS, A4>(bA, dA + o, lane & 7, tbl, xr[q], accA);
+        if (np == 2) P::template dot<MR, XS, A4>(bB, dB + o, lane & 7, tbl, xr[q], accB);
+      }
+      const bool rowA = lane < 32;
+      P::template dot<MR, XS, A4>(rowA ? bA : bB, (rowA ? dA : dB) + (uint32_t)((16 + ((lane & 31) >> 3)) * BB),
+                                  lane & 7, tbl, xr[2], pt);
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        accA[m] += rowA ? pt[m] : 0.f;
+        accB[m] += rowA ? 0.f : pt[m];
+      }
+      const int rl = (int)(row0 + (int64_t)t * a.slots - r0);
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        const float vA = wave_sum_to_lane63(accA[m]);
+        const float vB = wave_sum_to_lane63(accB[m]);
+        if (lane == 63) {
+          red[rl * MR + m] = vA;
+          if (np == 2) red[(rl + a.slots) * MR + m] = vB;
+        }
+      }
+    }
+  } else {
   // ---- main loop: one item per row, up to nb-1 items in flight ----
   int buf = 0;
   for (int t = 0; t < nitems; ++t) {
@@ -861,6 +912,7 @@ __global__ void __launch_bounds__(qmv_max_threads(qmv_weight(MR, GL, XS))) qmv_k
       if (lane == 63) red[(rl * MR + m) * a.W + ws] = v;
     }
   }
+  }
   {
     __syncthreads();
     const int nout = (int)(r1 - r0) * MR;
@@ -873,9 +925,9 @@ __global__ void __launch_bounds__(qmv_max_threads(qmv_weight(MR, GL, XS))) qmv_k
   }
 }
 
-template <int T, int MR, bool XS, int GL, bool A4>
+template <int T, int MR, bool XS, int GL, bool A4, bool PR = false>
 static hipError_t launch_qmv_t(const QmvArgs& a, int grid, int threads, size_t lds, hipStream_t s) {
-  auto k = qmv_kernel<T, MR, XS, GL, A4>;
+  auto k = qmv_kernel<T, MR, XS, GL, A4, PR>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -902,6 +954,7 @@ template <int T, bool A4>
 static hipError_t launch_qmv_variant(const QmvArgs& a, int mr, bool xs, int gl, int grid, int threads, size_t lds,
                                      hipStream_t s) {
   if (mr == 1 && !xs && gl == 1) return launch_qmv_t<T, 1, false, 1, A4>(a, grid, threads, lds, s);
+  if (mr == 1 && !xs && a.pair) return launch_qmv_t<T, 1, false, 3, A4, true>(a, grid, threads, lds, s);
   if (mr == 1) return xs ? launch_qmv_t<T, 1, true, 1, A4>(a, grid, threads, lds, s) : launch_qmv_t<T, 1, false, 3, A4>(a, grid, threads, lds, s);
   if (mr == 2) return xs ? launch_qmv_t<T, 2, true, 1, A4>(a, grid, threads, lds, s) : launch_qmv_t<T, 2, false, 1, A4>(a, grid, threads, lds, s);
   if (mr == 4 && !xs) return launch_qmv_t<T, 4, false, 1, A4>(a, grid, threads, lds, s);
@@ -985,14 +1038,15 @@ static constexpr int kLdsBytes = 160 * 1024;
 
 // Launch-plan parameters: waves per workgroup, in-flight bytes per CU the ring depth aims
 // for, workgroups per CU.
-// GSQ_QMV_TUNING="waves,inflight_kib,wg_per_cu,gl1_rows,gl1_waves,fill,x_lds" overrides the defaults (read once, at library
+// GSQ_QMV_TUNING="waves,inflight_kib,wg_per_cu,gl1_rows,gl1_waves,fill,x_lds,pair" overrides the defaults (read once, at library
 // load), for measuring launch plans without a rebuild.
 static QmvTuning qmv_tuning_from_env() {
-  QmvTuning t = {12, 96 * 1024, 1, 5120, 15, 1, 1};
+  QmvTuning t = {12, 96 * 1024, 1, 5120, 15, 1, 1, 1};
   if (const char* s = std::getenv("GSQ_QMV_TUNING")) {
-    int v[7];
-    if (std::sscanf(s, "%d,%d,%d,%d,%d,%d,%d", &v[0], &v[1], &v[2], &v[3], &v[4], &v[5], &v[6]) == 7)
-      t = {v[0], v[1] * 1024, v[2], v[3], v[4], v[5], v[6]};
+    // a prefix of the fields may be given; the rest keep their defaults
+    int v[8] = {t.waves, t.inflight_bytes / 1024, t.wg_per_cu, t.gl1_rows, t.gl1_waves, t.fill, t.x_lds, t.pair};
+    std::sscanf(s, "%d,%d,%d,%d,%d,%d,%d,%d", &v[0], &v[1], &v[2], &v[3], &v[4], &v[5], &v[6], &v[7]);
+    t = {v[0], v[1] * 1024, v[2], v[3], v[4], v[5], v[6], v[7]};
   }
   return t;
 }
@@ -1060,6 +1114,12 @@ static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, 
   if (nb < 2) return hipErrorInvalidValue;
   a.nb = nb;
   a.fill = g_qmv_tuning.fill < 1 ? 1 : g_qmv_tuning.fill;
+  // items decoded in pairs (qmv_kernel PR): one fp16 row of 20 superblocks per wave and at least
+  // three ring buffers (a pair being decoded and one in flight); for the types where it measured
+  // faster on 17408x5120 (IQ1_S/IQ1_M/IQ2_S/Q2_K 4-7%, IQ3_S/IQ4_XS 1-2%; Q4_K and IQ2_XS were
+  // 3-5% slower, the rest even)
+  const bool pair_type = qt == IQ1_S || qt == IQ1_M || qt == IQ2_S || qt == Q2_K || qt == IQ3_S || qt == IQ4_XS;
+  a.pair = (g_qmv_tuning.pair && pair_type && mr == 1 && !xs && gl == 3 && a.W == 1 && a.nblk == 20 && nb >= 3) ? 1 : 0;
   const int threads = nw * 64;
   const size_t lds_all = (size_t)a.ring_off + (size_t)nw * nb * a.sbuf;
   if (lds_all > (size_t)lds_cap) return hipErrorInvalidValue;

@@ -1,7 +1,7 @@
 """QMV parity under launch plans other than the default (run on an MI355X).
 
 The QMV launch plan (waves per workgroup, ring depth target, workgroups per CU, the
-one-slice-per-wave limit, ring fill rate, activation staging) is read from GSQ_QMV_TUNING
+one-slice-per-wave limit, ring fill rate, activation staging, paired items) is read from GSQ_QMV_TUNING
 once when libgsq.so loads, so each plan runs in a child process of its own. Each child checks
 a few types and both 27B row widths against the oracle at the QMV tolerance (rel-L2 1e-4) and
 elementwise within 1e-4 relative / 1e-5 of the largest output (the 5120- and 17408-wide rows
@@ -30,7 +30,7 @@ books = tables.synthetic_tables(0)
 tables.set_tables(books)
 dev = torch.device("cuda:0")
 for qtype, N, K, rows in (("Q6_K", 1100, 5120, 1), ("IQ2_S", 5200, 5120, 1), ("IQ1_M", 300, 17408, 1),
-                          ("Q4_K", 700, 5120, 2), ("IQ3_XXS", 900, 512, 1)):
+                          ("Q4_K", 700, 5120, 2), ("IQ3_XXS", 900, 512, 1), ("Q2_K", 5202, 5120, 1)):
     print(f"plan {os.environ['GSQ_QMV_TUNING']} {qtype} M={rows} N={N} K={K}", flush=True)
     packed = synth.make_packed(qtype, N, K, seed=31)
     x = synth.make_x(rows, K, seed=32, dtype=np.float16)
@@ -43,11 +43,12 @@ for qtype, N, K, rows in (("Q6_K", 1100, 5120, 1), ("IQ2_S", 5200, 5120, 1), ("I
 print("plan ok", flush=True)
 """
 
-# waves, in-flight KiB, workgroups per CU, one-slice-per-wave row limit, its waves, fill, x in LDS
+# waves, in-flight KiB, workgroups per CU, one-slice-per-wave row limit, its waves, fill, x in LDS,
+# paired items
 PLANS = [
-    "8,64,2,0,12,2,0",       # two workgroups per CU, three slices per wave everywhere, x from global
-    "12,128,1,17408,12,3,1",  # one slice per wave for every K=5120 matrix, deeper fill
-    "16,96,1,5120,9,1,1",    # more waves than the 3-slice variant allows (clamped), 3 row slots
+    "8,64,2,0,12,2,0,1",       # two workgroups per CU, three slices per wave everywhere, x from global
+    "12,128,1,17408,12,3,1,1",  # one slice per wave for every K=5120 matrix, deeper fill
+    "16,96,1,5120,9,1,1,0",    # more waves than the 3-slice variant allows (clamped), 3 row slots, no pairs
 ]
 
 

@@ -409,3 +409,47 @@ def test_qmv_hip_graph_replays_match_eager():
         torch.cuda.synchronize()
         for c, e in zip(cases, eager):
             assert torch.equal(c[3], e), f"replay {rep} differs"
+
+
+def test_qmm_hip_graph_replays_match_eager():
+    """Tiled (stream-K split tiles) and small-batch QMM launches captured in a HIP graph give the
+    eager results bit for bit on every replay: the split-tile counters reset themselves, so
+    nothing is cleared between calls (the first eager call allocates the workspace)."""
+    from mlx_gsq_amd import _lib
+    from mlx_gsq_amd.formats import TYPE_IDS
+    lib = _lib.lib()
+    cases = []
+    for i, (qtype, M, N, K) in enumerate((("IQ3_S", 200, 1536, 5120), ("Q4_K", 5, 1000, 4096),
+                                         ("IQ1_S", 64, 1000, 1024), ("Q6_K", 300, 520, 2048))):
+        packed = dev(synth.make_packed(qtype, N, K, seed=80 + i))
+        x = dev(synth.make_x(M, K, seed=90 + i, dtype=np.float16))
+        _lib.ensure_tables(qtype, packed.device)
+        cases.append((TYPE_IDS[qtype], packed, x, torch.empty(M, N, device="cuda"), M, N, K))
+
+    def launch_all(stream):
+        for tid, packed, x, y, M, N, K in cases:
+            assert lib.gsq_qmm(tid, packed.data_ptr(), x.data_ptr(), 1, y.data_ptr(), 0, M, N, K, stream) == 0
+
+    launch_all(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    eager = [c[3].clone() for c in cases]
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(graph, stream=cap):
+            launch_all(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.current_stream().wait_stream(cap)
+    for rep in range(4):
+        for c in cases:
+            c[3].fill_(float("nan"))          # eager work between replays
+        launch_all(torch.cuda.current_stream().cuda_stream)  # eager QMM calls share the workspace
+        torch.cuda.synchronize()
+        for c, e in zip(cases, eager):
+            assert torch.equal(c[3], e), f"eager call before replay {rep} differs"
+            c[3].fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for c, e in zip(cases, eager):
+            assert torch.equal(c[3], e), f"replay {rep} differs"

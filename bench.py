@@ -10,8 +10,8 @@ per product) step time is reported beside it.
 Printed JSON line (one, on stdout):
   value         whole-step throughput: algorithmic bytes of the 44 launches / graph step time
   roofline      the dominant QMV launch (largest share of kernel time): its algorithmic bytes
-                / its median duration from HIP events around that launch on the launch
-                stream, against the 8 TB/s HBM peak; `traffic` comes from the committed
+                / its time per launch (median of 5 loops of 128 back-to-back launches, HIP
+                events on the launch stream), against the 8 TB/s HBM peak; `traffic` comes from the committed
                 rocprofv3 counter summary (profiles/qmv_traffic.json) when it covers the
                 same kernel and shape, else null
   per_type      per-type GB/s and fraction of peak over its 4 shapes (kernel time)
@@ -47,6 +47,7 @@ FP16_PEAK_TFLOPS = 2500.0
 SHAPES = ((5120, 5120), (1024, 5120), (17408, 5120), (5120, 17408))
 METRIC = "QMV GB/s & % HBM peak (M=1); QMM TFLOPS & % MFMA peak (M=512); per type"
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qmv_traffic.json")
+ROOF_REPS, ROOF_REPEATS = 128, 5  # roofline kernel timing: 5 loops of 128 back-to-back launches
 
 
 def log(*a):
@@ -431,10 +432,10 @@ def qmm_profile_case(spec, reps, device):
     print(json.dumps({"qmm_profile_case": spec, "reps": reps, "flop_per_launch": 2 * m * n * k}), flush=True)
 
 
-def case_loop(q, n, k, reps, device, warmup=8):
-    """`reps` back-to-back launches of one (type, shape) product over 8 rotating weight copies on
-    the current stream, after `warmup` untimed ones; returns the mean time per launch (us) from
-    a HIP event pair on that stream."""
+def case_loop(q, n, k, reps, device, warmup=8, repeats=1):
+    """`repeats` timed loops of `reps` back-to-back launches of one (type, shape) product over 8
+    rotating weight copies on the current stream, after `warmup` untimed ones; returns the median
+    over the loops of the mean time per launch (us), each from a HIP event pair on that stream."""
     import torch
     from mlx_gsq_amd import _lib, tables
     from mlx_gsq_amd.formats import TYPE_IDS
@@ -455,22 +456,26 @@ def case_loop(q, n, k, reps, device, warmup=8):
     for i in range(warmup):
         launch(i)
     torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for i in range(reps):
-        launch(i)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1e3 / reps
+    per = []
+    for _ in range(repeats):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(reps):
+            launch(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        per.append(e0.elapsed_time(e1) * 1e3 / reps)
+    return statistics.median(per)
 
 
 def profile_case(spec, reps, device):
     """Only one (type, shape) product: the loop the roofline figure is timed with."""
     q, shape = spec.split(":")
     n, k = (int(v) for v in shape.split("x"))
-    us = case_loop(q, n, k, reps, device)
-    print(json.dumps({"profile_case": spec, "reps": reps, "warmup": 8, "bytes_per_launch": qmv_bytes(q, n, k),
+    us = case_loop(q, n, k, reps, device, repeats=ROOF_REPEATS)
+    print(json.dumps({"profile_case": spec, "reps": reps, "repeats": ROOF_REPEATS, "warmup": 8,
+                      "bytes_per_launch": qmv_bytes(q, n, k),
                       "us_per_launch": round(us, 3)}), flush=True)
 
 
@@ -546,13 +551,14 @@ def main():
         us = sum(per_launch[i] for i in idx)
         gbs = b / (us * 1e-6) / 1e9
         per_type[q] = {"GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
-    # the roofline kernel: the longest launch of the sweep, timed on its own as 64 back-to-back
-    # launches (the loop of --profile-case, which the committed kernel trace runs)
+    # the roofline kernel: the longest launch of the sweep, timed on its own as 5 loops of 128
+    # back-to-back launches, median loop (the loop of --profile-case, which the committed kernel
+    # trace runs)
     dom = max(range(len(qc.cases)), key=lambda i: per_launch[i])
     dq, _, dn, dk = qc.cases[dom][:4]
     dom_case = f"{dq} {dn}x{dk}"
     dom_bytes = qmv_bytes(dq, dn, dk)
-    dom_us = case_loop(dq, dn, dk, 64, device)
+    dom_us = case_loop(dq, dn, dk, ROOF_REPS, device, repeats=ROOF_REPEATS)
     achieved = dom_bytes / (dom_us * 1e-6) / 1e9
     kernel_time = sum(per_launch) * 1e-6
     line = {
@@ -565,8 +571,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(dom_case),
                      "kernel": f"qmv_kernel<{dq}> M=1", "case": dom_case, "bytes_per_launch": int(dom_bytes),
-                     "us_per_launch": round(dom_us, 3), "timing": "HIP events around 64 back-to-back launches "
-                     "(8 rotating weight copies) on the launch stream"},
+                     "us_per_launch": round(dom_us, 3), "timing": f"median of {ROOF_REPEATS} loops of HIP events "
+                     f"around {ROOF_REPS} back-to-back launches (8 rotating weight copies) on the launch stream"},
         "eager_ms_per_step": round(eager_ms, 4),
         "kernel_time_GBs": round(step_bytes / kernel_time / 1e9, 1),
         "mean_type_frac": round(sum(v["frac"] for v in per_type.values()) / len(per_type), 4),

@@ -485,11 +485,14 @@ __global__ void __launch_bounds__(64 * WV, 1) qmm_mfma_kernel(QmmMfmaArgs args) 
       // slot 2w: the tile this workgroup starts in; slot 2w + 1: the tile it ends in
       const int slot = 2 * w + (q0 == 0 ? 0 : 1);
       const __amdgpu_buffer_rsrc_t ps = qmm_slot_rsrc(part, slot);
-      // every store has completed (device-coherent) before the arrival count is incremented
+      // every store has completed (device-coherent) before the arrival count is incremented;
+      // 16-row blocks wholly past M (padding rows of the last activation tile) are not stored
 #pragma unroll
       for (int i = 0; i < MF; ++i)
+        if (m0 + 16 * i < M) {
 #pragma unroll
-        for (int j = 0; j < NB; ++j) qmm_st_coherent(ps, ((i * NB + j) * TH + tid) * 16, acc[i][j]);
+          for (int j = 0; j < NB; ++j) qmm_st_coherent(ps, ((i * NB + j) * TH + tid) * 16, acc[i][j]);
+        }
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       if (tid == 0) bc[0] = __hip_atomic_fetch_add(&cnt[wf], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -500,6 +503,8 @@ __global__ void __launch_bounds__(64 * WV, 1) qmm_mfma_kernel(QmmMfmaArgs args) 
         constexpr int CH = 8;  // output blocks per batch of loads
 #pragma unroll 1
         for (int ij0 = 0; ij0 < MF * NB; ij0 += CH) {
+          // batches that start past M hold only padding rows, whose partials were not stored
+          if (m0 + 16 * (ij0 / NB) >= M) break;
           float4_t sum[CH];
 #pragma unroll
           for (int t = 0; t < CH; ++t) sum[t] = (float4_t){0.f, 0.f, 0.f, 0.f};

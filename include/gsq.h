@@ -49,6 +49,14 @@ int gsq_block_bytes(int qtype_id);
 int gsq_set_tables(int qtype_id, const float* grid, int64_t entries, int64_t coords,
                    const uint8_t* ksigns, int64_t n_ksigns);
 
+/* Prepare the current device and `stream` (a hipStream_t; NULL = default stream) for calls
+ * that must neither allocate nor copy synchronously, such as calls under HIP graph capture:
+ * builds the fixed tables of the non-grid types and the QMM workspace of `stream`. Without
+ * it the first call on a device or stream does that work itself, which fails with
+ * GSQ_E_VALUE while the stream is capturing. Codebooks still come from gsq_set_tables. No
+ * counterpart in the reference (MLX compiles and caches its kernels lazily, qmv.py:66). */
+int gsq_prepare(void* stream);
+
 /* 1 if the current device holds the tables `qtype_id` needs, else 0. */
 int gsq_tables_ready(int qtype_id);
 
@@ -63,7 +71,10 @@ int gsq_qmv(int qtype_id, const void* packed, const void* x, int x_dtype, void* 
             int64_t M, int64_t N, int64_t K, void* stream);
 
 /* Same product with the tiled MFMA kernel (prefill, large M). Replaces quantized_matmul
- * (mlx_gsq/runtime/kernels/qmm.py:559-594). */
+ * (mlx_gsq/runtime/kernels/qmm.py:559-594). Workgroups that share an output tile exchange
+ * fp32 partials through a workspace the library keeps per (device, stream) and allocates on
+ * the first call on that stream (or in gsq_prepare): calls on one stream run in order and
+ * share it, calls on different streams may overlap and never share one. */
 int gsq_qmm(int qtype_id, const void* packed, const void* x, int x_dtype, void* y, int y_dtype,
             int64_t M, int64_t N, int64_t K, void* stream);
 

@@ -64,8 +64,18 @@ struct DevState {
   std::map<int, uint8_t*> qmv_tbls;   // per type with a QMV LDS table
   uint8_t* ksigns = nullptr;
   int num_cus = 0;
-  QmmWorkspace qmm_ws = {nullptr, nullptr, 0};
+  // QMM workspaces, one per stream: launches on one stream run in order, so they may share
+  // a workspace; launches on different streams may overlap and never share one
+  std::map<hipStream_t, QmmWorkspace> qmm_ws;
 };
+
+// True if `s` is capturing into a HIP graph: nothing may be allocated or copied
+// synchronously then.
+bool capturing(hipStream_t s) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &st) != hipSuccess) return false;
+  return st != hipStreamCaptureStatusNone;
+}
 
 // Upload (or refresh) the QMV LDS table image of `qt` on the current device; caller holds g_mu.
 int upload_qmv_table(DevState& st, int qt, const uint16_t* grid16_host, const uint8_t* ksigns_host) {
@@ -91,8 +101,9 @@ int current_device(int* dev) {
   return GSQ_OK;
 }
 
-// Resolve the device tables for `qt` on the current device (caller holds no lock).
-int resolve(int qt, DevTables* tb, int* num_cus) {
+// Resolve the device tables for `qt` on the current device (caller holds no lock). A fixed
+// table not built yet is built here unless `s` is capturing (gsq_prepare builds them first).
+int resolve(int qt, DevTables* tb, int* num_cus, hipStream_t s = nullptr) {
   int dev;
   if (int rc = current_device(&dev)) return rc;
   std::lock_guard<std::mutex> lk(g_mu);
@@ -114,6 +125,9 @@ int resolve(int qt, DevTables* tb, int* num_cus) {
       return fail(GSQ_E_TABLES, "ksigns table is not set on device %d", dev);
   } else if (qmv_table_bytes(qt) > 0 && !st.qmv_tbls.count(qt)) {
     // fixed tables (IQ4_XS values) are built on first use on each device
+    if (capturing(s))
+      return fail(GSQ_E_VALUE, "the %s table is not built on device %d and the stream is capturing: "
+                  "call gsq_prepare before capture", type_name(qt), dev);
     if (int rc = upload_qmv_table(st, qt, nullptr, nullptr)) return rc;
   }
   auto tt = st.qmv_tbls.find(qt);
@@ -121,35 +135,46 @@ int resolve(int qt, DevTables* tb, int* num_cus) {
   return GSQ_OK;
 }
 
-// The QMM workspace of the current device, allocated on the first QMM call there (a fixed
-// size: 2 partial slots of 256 x 256 floats and one counter per CU); counters start at zero.
-int qmm_workspace(QmmWorkspace* ws) {
+// Partial-tile capacity of a QMM workspace: 2 slots of up to 256 x 256 floats per CU (the
+// largest tile plan), and one arrival counter per CU.
+long long qmm_ws_part_bytes(int num_cus) { return 2ll * num_cus * 256 * 256 * (long long)sizeof(float); }
+
+// The QMM workspace of stream `s` on the current device, allocated on the first QMM call on
+// that stream (or by gsq_prepare); counters start at zero and every launch leaves them at zero.
+int qmm_workspace(hipStream_t s, QmmWorkspace* ws) {
   int dev;
   if (int rc = current_device(&dev)) return rc;
   std::lock_guard<std::mutex> lk(g_mu);
   DevState& st = g_dev[dev];
-  if (!st.qmm_ws.part) {
-    if (st.num_cus == 0) {
-      hipError_t e = hipDeviceGetAttribute(&st.num_cus, hipDeviceAttributeMultiprocessorCount, dev);
-      if (e != hipSuccess) return fail(GSQ_E_HIP, "hipDeviceGetAttribute: %s", hipGetErrorString(e));
-    }
-    const int groups = st.num_cus;
-    const size_t part_bytes = (size_t)2 * groups * 256 * 256 * sizeof(float);
-    float* part = nullptr;
-    int* cnt = nullptr;
-    hipError_t e = hipMalloc(&part, part_bytes);
-    if (e != hipSuccess) return fail(GSQ_E_HIP, "hipMalloc(QMM workspace): %s", hipGetErrorString(e));
-    e = hipMalloc(&cnt, (size_t)groups * sizeof(int));
-    if (e == hipSuccess) e = hipMemset(cnt, 0, (size_t)groups * sizeof(int));
-    if (e == hipSuccess) e = hipDeviceSynchronize();
-    if (e != hipSuccess) {
-      hipFree(part);
-      if (cnt) hipFree(cnt);
-      return fail(GSQ_E_HIP, "QMM workspace setup: %s", hipGetErrorString(e));
-    }
-    st.qmm_ws = {part, cnt, groups};
+  auto it = st.qmm_ws.find(s);
+  if (it != st.qmm_ws.end()) {
+    *ws = it->second;
+    return GSQ_OK;
   }
-  *ws = st.qmm_ws;
+  if (capturing(s))
+    return fail(GSQ_E_VALUE, "stream has no QMM workspace on device %d and is capturing: call gsq_prepare(stream) "
+                "before capture", dev);
+  if (st.qmm_ws.size() >= 64)
+    return fail(GSQ_E_VALUE, "QMM workspaces exist for 64 streams on device %d; reuse streams", dev);
+  if (st.num_cus == 0) {
+    hipError_t e = hipDeviceGetAttribute(&st.num_cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return fail(GSQ_E_HIP, "hipDeviceGetAttribute: %s", hipGetErrorString(e));
+  }
+  const int groups = st.num_cus;
+  const long long part_bytes = qmm_ws_part_bytes(groups);
+  float* part = nullptr;
+  int* cnt = nullptr;
+  hipError_t e = hipMalloc(&part, (size_t)part_bytes);
+  if (e != hipSuccess) return fail(GSQ_E_HIP, "hipMalloc(QMM workspace): %s", hipGetErrorString(e));
+  e = hipMalloc(&cnt, (size_t)groups * sizeof(int));
+  if (e == hipSuccess) e = hipMemset(cnt, 0, (size_t)groups * sizeof(int));
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    hipFree(part);
+    if (cnt) hipFree(cnt);
+    return fail(GSQ_E_HIP, "QMM workspace setup: %s", hipGetErrorString(e));
+  }
+  *ws = st.qmm_ws[s] = QmmWorkspace{part, cnt, groups, part_bytes};
   return GSQ_OK;
 }
 
@@ -232,6 +257,18 @@ int gsq_set_tables(int qt, const float* grid, int64_t entries, int64_t coords, c
   return GSQ_OK;
 }
 
+int gsq_prepare(void* stream) {
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (capturing(s)) return fail(GSQ_E_VALUE, "gsq_prepare must be called before the stream starts capturing");
+  for (int qt : {Q2_K, Q4_K, Q6_K, IQ4_XS}) {  // the types whose tables are fixed (built here)
+    DevTables tb;
+    int cus;
+    if (int rc = resolve(qt, &tb, &cus, s)) return rc;
+  }
+  QmmWorkspace ws;
+  return qmm_workspace(s, &ws);
+}
+
 int gsq_tables_ready(int qt) {
   if (block_bytes_of(qt) == 0) return 0;
   if (!is_grid_type(qt)) return 1;
@@ -248,7 +285,7 @@ int gsq_dequant(int qt, const void* packed, int64_t nblocks, float* out, void* s
   if (reinterpret_cast<uintptr_t>(out) & 15) return fail(GSQ_E_VALUE, "out must be 16-byte aligned");
   DevTables tb;
   int cus;
-  if (int rc = resolve(qt, &tb, &cus)) return rc;
+  if (int rc = resolve(qt, &tb, &cus, static_cast<hipStream_t>(stream))) return rc;
   hipError_t e = launch_dequant(qt, static_cast<const uint8_t*>(packed), nblocks, out, tb,
                                 static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(GSQ_E_HIP, "dequant launch: %s", hipGetErrorString(e));
@@ -265,7 +302,7 @@ int gsq_qmv(int qt, const void* packed, const void* x, int xdt, void* y, int ydt
   if (reinterpret_cast<uintptr_t>(x) & 15) return fail(GSQ_E_VALUE, "x must be 16-byte aligned");
   DevTables tb;
   int cus;
-  if (int rc = resolve(qt, &tb, &cus)) return rc;
+  if (int rc = resolve(qt, &tb, &cus, static_cast<hipStream_t>(stream))) return rc;
   hipError_t e = launch_qmv(qt, static_cast<const uint8_t*>(packed), x, xdt, y, ydt, M, N, (int)K, tb, cus,
                             static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(GSQ_E_HIP, "qmv launch: %s", hipGetErrorString(e));
@@ -278,9 +315,9 @@ int gsq_qmm(int qt, const void* packed, const void* x, int xdt, void* y, int ydt
   if (!x || !y) return fail(GSQ_E_VALUE, "NULL pointer");
   DevTables tb;
   int cus;
-  if (int rc = resolve(qt, &tb, &cus)) return rc;
+  if (int rc = resolve(qt, &tb, &cus, static_cast<hipStream_t>(stream))) return rc;
   QmmWorkspace ws;
-  if (int rc = qmm_workspace(&ws)) return rc;
+  if (int rc = qmm_workspace(static_cast<hipStream_t>(stream), &ws)) return rc;
   hipError_t e = launch_qmm(qt, static_cast<const uint8_t*>(packed), x, xdt, y, ydt, M, N, (int)K, tb, cus, ws,
                             static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(GSQ_E_HIP, "qmm launch: %s", hipGetErrorString(e));
@@ -301,7 +338,7 @@ int gsq_embedding(int qt, const void* packed, const void* ids, int ids_dtype, in
   if (reinterpret_cast<uintptr_t>(ids) & (ids_dtype == GSQ_IDS_I64 ? 7 : 3)) return fail(GSQ_E_VALUE, "misaligned ids");
   DevTables tb;
   int cus;
-  if (int rc = resolve(qt, &tb, &cus)) return rc;
+  if (int rc = resolve(qt, &tb, &cus, static_cast<hipStream_t>(stream))) return rc;
   hipError_t e = launch_embedding(qt, static_cast<const uint8_t*>(packed), ids, ids_dtype == GSQ_IDS_I64, n_ids, vocab,
                                   dims, out, out_dtype, tb, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(GSQ_E_HIP, "embedding launch: %s", hipGetErrorString(e));

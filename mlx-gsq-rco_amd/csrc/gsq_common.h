@@ -90,13 +90,15 @@ struct QmmTuning {
   int small_min_cols;
 };
 
-// Per-device QMM workspace, allocated once: fp32 partial tiles of workgroups that share an
-// output tile (2 slots of 256 x 256 floats per workgroup) and one arrival counter per
-// workgroup, kept at zero between launches.
+// QMM workspace: fp32 partial tiles of workgroups that share an output tile (2 slots per
+// workgroup, each sized to the launch plan's tile) and one arrival counter per workgroup, kept
+// at zero between launches. `part_bytes` bounds 2 * groups * slot bytes; `max_groups` bounds the
+// workgroups (counters). One workspace is never used by two launches that may overlap.
 struct QmmWorkspace {
   float* part;
   int* cnt;
   int max_groups;
+  long long part_bytes;
 };
 
 // Non-linear IQ4_XS values (k_decode.py:77).
@@ -105,6 +107,16 @@ __device__ __constant__ static const int8_t kIQ4Values[16] = {
 
 __device__ __forceinline__ float h2f(uint32_t bits16) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+
+// float32 -> bfloat16 bits, round to nearest even; a NaN stays a (quiet) NaN of the same sign
+// (adding the rounding bias to a NaN whose high mantissa bits are all ones would carry into
+// the sign and give -0 or +0).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float v) {
+  uint32_t b = __builtin_bit_cast(uint32_t, v);
+  if ((b & 0x7FFFFFFFu) > 0x7F800000u) return (b >> 16) | 0x0040u;
+  b += 0x7FFFu + ((b >> 16) & 1u);
+  return b >> 16;
 }
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));

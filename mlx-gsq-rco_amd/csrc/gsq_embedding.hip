@@ -14,13 +14,6 @@ namespace gsq {
 
 enum { EMB_F32 = 0, EMB_F16 = 1, EMB_BF16 = 2 };
 
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float v) {
-  uint32_t b = __builtin_bit_cast(uint32_t, v);
-  if ((b & 0x7FFFFFFFu) > 0x7F800000u) return (b >> 16) | 0x0040u;  // NaN stays a (quiet) NaN
-  b += 0x7FFFu + ((b >> 16) & 1u);
-  return b >> 16;
-}
-
 template <int T>
 __global__ void __launch_bounds__(256) embedding_kernel(const uint8_t* __restrict__ packed, const void* __restrict__ ids,
                                                         int ids64, int64_t n_ids, int64_t vocab, int64_t dims,

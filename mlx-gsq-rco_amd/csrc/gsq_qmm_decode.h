@@ -25,7 +25,9 @@
 namespace gsq {
 
 // fp16 pair {fma(a, h.lo, c), fma(a, h.hi, c)} with h an fp16 pair and a, c float: each result
-// is computed exactly and rounded once (v_fma_mixlo_f16 / v_fma_mixhi_f16)
+// is computed exactly and rounded once (v_fma_mixlo_f16 / v_fma_mixhi_f16). Its result must
+// pass through a compiler-visible VALU instruction (the codebook decoders' sign XOR) before an
+// MFMA reads it: the compiler inserts no wait states after asm (codes8 carries its own).
 // (the host pass never runs this device-only function; the VGPR asm constraints exist only in
 // the device compilation)
 __device__ __forceinline__ uint32_t mix2(float a, uint32_t h, float c) {
@@ -43,12 +45,28 @@ __device__ __forceinline__ uint32_t spread_hi(uint32_t q) { return __builtin_amd
 
 constexpr float kCode = 16777216.f;  // 2^24: an fp16 subnormal with bits q has value q * 2^-24
 
-// eight byte codes (two words) -> fp16 of a * code + c (a24 = a * 2^24)
+// eight byte codes (two words) -> fp16 of a * code + c (a24 = a * 2^24), as the four fp16
+// pairs of an MFMA B operand. The results go straight into v_mfma, which may read a VGPR only
+// two wait states after a VALU wrote it; the compiler cannot see that an asm statement is a
+// VALU write, so the eight conversions are one asm block that ends with those two wait states
+// (s_nop 1), and the outputs are early-clobber (written while inputs are still being read).
 __device__ __forceinline__ void codes8(const uint32_t (&q)[2], float a24, float c, uint32_t (&o)[4]) {
-  o[0] = mix2(a24, spread_lo(q[0]), c);
-  o[1] = mix2(a24, spread_hi(q[0]), c);
-  o[2] = mix2(a24, spread_lo(q[1]), c);
-  o[3] = mix2(a24, spread_hi(q[1]), c);
+  const uint32_t h0 = spread_lo(q[0]), h1 = spread_hi(q[0]), h2 = spread_lo(q[1]), h3 = spread_hi(q[1]);
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm("v_fma_mixlo_f16 %0, %4, %5, %6 op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixlo_f16 %1, %4, %7, %6 op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixlo_f16 %2, %4, %8, %6 op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixlo_f16 %3, %4, %9, %6 op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixhi_f16 %0, %4, %5, %6 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixhi_f16 %1, %4, %7, %6 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixhi_f16 %2, %4, %8, %6 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixhi_f16 %3, %4, %9, %6 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+      "s_nop 1"
+      : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3])
+      : "v"(a24), "v"(h0), "v"(c), "v"(h1), "v"(h2), "v"(h3));
+#else
+  o[0] = h0; o[1] = h1; o[2] = h2; o[3] = h3; (void)a24; (void)c;
+#endif
 }
 
 __device__ __forceinline__ const uint32_t* tbl_words(const uint8_t* tbl, uint32_t byte_off) {

@@ -29,6 +29,8 @@
 //    activation tiles and K ranges) lands on one XCD and shares its L2.
 // fp32 / bf16 activations use the generic kernel below.
 #pragma once
+#include <type_traits>
+
 #include "gsq_decode.h"
 #include "gsq_qmm_decode.h"
 
@@ -41,17 +43,13 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ void qmm_store_y(void* y, int dt, int64_t i, float v) {
   if (dt == QDT_F16) reinterpret_cast<_Float16*>(y)[i] = (_Float16)v;
-  else if (dt == QDT_BF16) {
-    uint32_t b = __builtin_bit_cast(uint32_t, v);
-    b += 0x7FFFu + ((b >> 16) & 1u);
-    reinterpret_cast<uint16_t*>(y)[i] = (uint16_t)(b >> 16);
-  } else reinterpret_cast<float*>(y)[i] = v;
+  else if (dt == QDT_BF16) reinterpret_cast<uint16_t*>(y)[i] = (uint16_t)f32_to_bf16_bits(v);
+  else reinterpret_cast<float*>(y)[i] = v;
 }
 
 // ---- MFMA kernel ----------------------------------------------------------------------
 constexpr int kQBN = 256;                   // weight rows per tile
 constexpr int kQLds = 160 * 1024;
-constexpr int kQSlotFloats = 256 * kQBN;    // one partial-sum slot (BM <= 256)
 
 // WV waves per workgroup (4: one per SIMD, or 8: two per SIMD), each owning kQBN / WV weight
 // rows of the tile.
@@ -190,7 +188,9 @@ struct QmmMfmaArgs {
   int xcd_remap;         // G is a multiple of 8
   const uint8_t* tbl;    // the type's table image (codebook + sign masks), or null
   int tbl_bytes;         // multiple of 16
-  float* part;           // 2 * G partial slots of kQSlotFloats
+  float* part;           // 2 * G partial slots of slot_floats
+  int slot_floats;       // floats per partial slot: MF * NB * 64 * WV * 4 (BM x 256)
+  long long part_bytes;  // capacity of `part`
   int* cnt;              // per-tile arrival counters, indexed by the tile's first workgroup
 };
 
@@ -199,9 +199,9 @@ struct QmmMfmaArgs {
 // device-coherent level (sc1) and buffer loads that bypass the caches (sc0 sc1): no L2
 // write-back or invalidate of unrelated data, and full cache lines per wave instruction.
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-constexpr int kQSlotBytes = kQSlotFloats * 4;
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t qmm_slot_rsrc(float* part, int slot) {
-  return __builtin_amdgcn_make_buffer_rsrc(part + (size_t)slot * kQSlotFloats, 0, kQSlotBytes, 0x00020000);
+// A slot holds one workgroup's partial tile: `slot_floats` floats (the plan's tile size).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t qmm_slot_rsrc(float* part, int slot, int slot_floats) {
+  return __builtin_amdgcn_make_buffer_rsrc(part + (size_t)slot * (size_t)slot_floats, 0, slot_floats * 4, 0x00020000);
 }
 __device__ __forceinline__ void qmm_st_coherent(__amdgpu_buffer_rsrc_t r, int off, float4_t v) {
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, off, 0, 16 /* sc1 */);
@@ -306,6 +306,7 @@ __global__ void __launch_bounds__(64 * WV, 1) qmm_mfma_kernel(QmmMfmaArgs args) 
   const long long row_bytes = args.row_bytes;
   const uint8_t* const tblg = args.tbl;
   float* const part = args.part;
+  const int slot_floats = args.slot_floats;
   int* const cnt = args.cnt;
   using Geo = QmmGeo<T, WV>;
   constexpr int BB = Geo::kBB, GW = Geo::kGW, GR = Geo::kGran, S = Geo::kSlot;
@@ -484,7 +485,7 @@ __global__ void __launch_bounds__(64 * WV, 1) qmm_mfma_kernel(QmmMfmaArgs args) 
     } else {
       // slot 2w: the tile this workgroup starts in; slot 2w + 1: the tile it ends in
       const int slot = 2 * w + (q0 == 0 ? 0 : 1);
-      const __amdgpu_buffer_rsrc_t ps = qmm_slot_rsrc(part, slot);
+      const __amdgpu_buffer_rsrc_t ps = qmm_slot_rsrc(part, slot, slot_floats);
       // every store has completed (device-coherent) before the arrival count is incremented;
       // 16-row blocks wholly past M (padding rows of the last activation tile) are not stored
 #pragma unroll
@@ -510,7 +511,7 @@ __global__ void __launch_bounds__(64 * WV, 1) qmm_mfma_kernel(QmmMfmaArgs args) 
           for (int t = 0; t < CH; ++t) sum[t] = (float4_t){0.f, 0.f, 0.f, 0.f};
           for (int v = wf; v <= wl; ++v) {
             const int vs = 2 * v + (tile == qmm_first_col(v, units, G) / nblk ? 0 : 1);
-            const __amdgpu_buffer_rsrc_t pv = qmm_slot_rsrc(part, vs);
+            const __amdgpu_buffer_rsrc_t pv = qmm_slot_rsrc(part, vs, slot_floats);
             float4_t ld[CH];
 #pragma unroll
             for (int t = 0; t < CH; ++t) ld[t] = qmm_ld_coherent(pv, ((ij0 + t) * TH + tid) * 16);
@@ -650,11 +651,18 @@ static bool qmm_grid_type(int qt) {
   return qt == IQ1_S || qt == IQ1_M || qt == IQ2_XXS || qt == IQ2_XS || qt == IQ2_S || qt == IQ3_XXS || qt == IQ3_S;
 }
 
+// Floats of one partial slot of the tiled kernel: every lane of the WV waves stores MF x NB
+// float4 accumulators (a BM x 256 tile).
+template <int T, int MF, int WV>
+constexpr int qmm_slot_floats() { return MF * QmmGeo<T, WV>::kNB * 64 * WV * 4; }
+
 template <int T, int MF, bool A4, int WV>
-static hipError_t launch_mfma_t(const QmmMfmaArgs& a, hipStream_t s) {
+static hipError_t launch_mfma_t(QmmMfmaArgs a, hipStream_t s) {
   if constexpr (!QmmPlan<T, MF, WV>::kValid) {
     return hipErrorInvalidValue;
   } else {
+    a.slot_floats = qmm_slot_floats<T, MF, WV>();
+    if (2ll * a.G * a.slot_floats * 4 > a.part_bytes) return hipErrorInvalidValue;
     auto k = qmm_mfma_kernel<T, MF, A4, WV>;
     static bool attr_set = false;
     if (!attr_set) {
@@ -688,28 +696,50 @@ static hipError_t launch_mfma_mf(const QmmMfmaArgs& a, bool a4, bool w8, hipStre
 // Plan and launch the MFMA kernel for type T: activation tile height (MF 16-row blocks) from M
 // (64 rows up to 64, 128 up to 128, else 256), then the stream-K grid:
 // one workgroup per CU, at most one per (tile, K column) unit.
+// Bytes of one partial slot of the plan launch_mfma_mf<T, mf> picks (8 waves where valid).
+template <int T>
+static long long qmm_slot_bytes(int mf, bool w8) {
+  auto pick = [&](auto mfc) -> long long {
+    constexpr int MF = decltype(mfc)::value;
+    if constexpr (QmmPlan<T, MF, 8>::kValid) {
+      if (w8) return 4ll * qmm_slot_floats<T, MF, 8>();
+    }
+    return 4ll * qmm_slot_floats<T, MF, 4>();
+  };
+  if (mf == 4) return pick(std::integral_constant<int, 4>{});
+  if (mf == 8) return pick(std::integral_constant<int, 8>{});
+  return pick(std::integral_constant<int, 16>{});
+}
+
 template <int T>
 static hipError_t launch_mfma(QmmMfmaArgs& a, int num_cus, const QmmWorkspace& ws, hipStream_t s) {
   if (a.tbl_bytes != qmm_tbl_bytes<T>()) return hipErrorInvalidValue;
   int mf = g_qmm_tuning.mf;
   if (mf == 0) mf = a.M <= 64 ? 4 : (a.M <= 128 ? 8 : 16);
   if (mf != 4 && mf != 8 && mf != 16) return hipErrorInvalidValue;
-  const int bm = 16 * mf;
-  a.mt = (a.M + bm - 1) / bm;
-  const long long units = (long long)a.mt * (((long long)a.N + kQBN - 1) / kQBN) * a.nblk;
-  if (units >= (1ll << 31)) return hipErrorInvalidValue;
-  a.units = (int)units;
+  const bool a4 = (reinterpret_cast<uintptr_t>(a.packed) & 3) == 0;
+  const bool w8 = g_qmm_tuning.waves != 4;
   // at least min_cols columns per workgroup: fewer workgroups share each tile when the
   // problem is small, which bounds the partial-tile traffic
   const int min_cols = g_qmm_tuning.min_cols > 0 ? g_qmm_tuning.min_cols : 2;
-  const int gmax = (a.units + min_cols - 1) / min_cols;
-  a.G = num_cus < gmax ? num_cus : gmax;
-  if (a.G > ws.max_groups) a.G = ws.max_groups;
+  for (;;) {
+    const int bm = 16 * mf;
+    a.mt = (a.M + bm - 1) / bm;
+    const long long units = (long long)a.mt * (((long long)a.N + kQBN - 1) / kQBN) * a.nblk;
+    if (units >= (1ll << 31)) return hipErrorInvalidValue;
+    a.units = (int)units;
+    const int gmax = (a.units + min_cols - 1) / min_cols;
+    a.G = num_cus < gmax ? num_cus : gmax;
+    if (a.G > ws.max_groups) a.G = ws.max_groups;
+    // a workspace too small for this tile height's partials at this grid: lower tiles
+    if (2ll * a.G * qmm_slot_bytes<T>(mf, w8) <= ws.part_bytes) break;
+    if (mf == 4) return hipErrorInvalidValue;
+    mf /= 2;
+  }
   a.xcd_remap = (a.G % 8 == 0) ? 1 : 0;
   a.part = ws.part;
+  a.part_bytes = ws.part_bytes;
   a.cnt = ws.cnt;
-  const bool a4 = (reinterpret_cast<uintptr_t>(a.packed) & 3) == 0;
-  const bool w8 = g_qmm_tuning.waves != 4;
   switch (mf) {
     case 4: return launch_mfma_mf<T, 4>(a, a4, w8, s);
     case 8: return launch_mfma_mf<T, 8>(a, a4, w8, s);
@@ -741,8 +771,11 @@ static hipError_t launch_qms(QmsArgs& a, int num_cus, const QmmWorkspace& ws, hi
   const int gmax = (a.units + min_cols - 1) / min_cols;
   a.G = num_cus < gmax ? num_cus : gmax;
   if (a.G > ws.max_groups) a.G = ws.max_groups;
+  // the partials of G workgroups must fit the workspace (slot: NB * 64 * WV float4)
+  while (a.G > 1 && 2ll * a.G * (nb * 64 * wv * 16) > ws.part_bytes) --a.G;
   a.xcd_remap = (a.G % 8 == 0) ? 1 : 0;
   a.part = ws.part;
+  a.part_bytes = ws.part_bytes;
   a.cnt = ws.cnt;
   const bool a4 = (reinterpret_cast<uintptr_t>(a.packed) & 3) == 0;
   if (wv == 8) return nb == 2 ? launch_qms_a4<T, 8, 2>(a, a4, s) : launch_qms_a4<T, 8, 1>(a, a4, s);

@@ -67,7 +67,9 @@ struct QmsArgs {
   int xcd_remap;       // G is a multiple of 8
   const uint8_t* tbl;  // the type's table image, or null
   int tbl_bytes;
-  float* part;         // 2 * G partial slots
+  float* part;         // 2 * G partial slots of slot_floats
+  int slot_floats;     // floats per partial slot: NB * 64 * WV * 4
+  long long part_bytes;  // capacity of `part`
   int* cnt;            // arrival counters, indexed by a group's first workgroup
 };
 
@@ -84,6 +86,7 @@ qms_kernel(QmsArgs args) {
   const long long row_bytes = args.row_bytes;
   const uint8_t* const tblg = args.tbl;
   float* const part = args.part;
+  const int slot_floats = args.slot_floats;
   int* const cnt = args.cnt;
   using Geo = QmsGeo<T, WV, NB>;
   using Plan = QmsPlan<T, WV, NB>;
@@ -194,7 +197,7 @@ qms_kernel(QmsArgs args) {
       }
     } else {
       const int slotp = 2 * w + (grp == ub / nblk ? 0 : 1);  // first group of this workgroup: slot 2w
-      const __amdgpu_buffer_rsrc_t ps = qmm_slot_rsrc(part, slotp);
+      const __amdgpu_buffer_rsrc_t ps = qmm_slot_rsrc(part, slotp, slot_floats);
 #pragma unroll
       for (int j = 0; j < NB; ++j) qmm_st_coherent(ps, (j * TH + tid) * 16, acc[j]);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -213,7 +216,7 @@ qms_kernel(QmsArgs args) {
           float4_t ld[4][NB];
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
-            const __amdgpu_buffer_rsrc_t pv = qmm_slot_rsrc(part, v + t == wf ? s0 : 2 * (v + t));
+            const __amdgpu_buffer_rsrc_t pv = qmm_slot_rsrc(part, v + t == wf ? s0 : 2 * (v + t), slot_floats);
 #pragma unroll
             for (int j = 0; j < NB; ++j) ld[t][j] = qmm_ld_coherent(pv, (j * TH + tid) * 16);
           }
@@ -223,7 +226,7 @@ qms_kernel(QmsArgs args) {
             for (int j = 0; j < NB; ++j) sum[j] += ld[t][j];
         }
         for (; v <= wl; ++v) {
-          const __amdgpu_buffer_rsrc_t pv = qmm_slot_rsrc(part, v == wf ? s0 : 2 * v);
+          const __amdgpu_buffer_rsrc_t pv = qmm_slot_rsrc(part, v == wf ? s0 : 2 * v, slot_floats);
 #pragma unroll
           for (int j = 0; j < NB; ++j) sum[j] += qmm_ld_coherent(pv, (j * TH + tid) * 16);
         }
@@ -244,10 +247,12 @@ qms_kernel(QmsArgs args) {
 }
 
 template <int T, bool A4, int WV, int NB>
-static hipError_t launch_qms_t(const QmsArgs& a, hipStream_t s) {
+static hipError_t launch_qms_t(QmsArgs a, hipStream_t s) {
   if constexpr (!QmsPlan<T, WV, NB>::kValid) {
     return hipErrorInvalidValue;
   } else {
+    a.slot_floats = NB * 64 * WV * 4;  // every lane stores NB float4 accumulators
+    if (2ll * a.G * a.slot_floats * 4 > a.part_bytes) return hipErrorInvalidValue;
     auto k = qms_kernel<T, A4, WV, NB>;
     static bool attr_set = false;
     if (!attr_set) {

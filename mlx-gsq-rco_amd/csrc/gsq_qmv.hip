@@ -85,26 +85,19 @@ __device__ __forceinline__ void dacc(uint32_t w, const XReg<MR, XS, NS>& x, int 
   }
 }
 
-// Small unsigned codes q (< 1024) placed in the low bits of an fp16 lane are the subnormal
-// values q * 2^-24, so a masked code pair is directly a v_dot2_f32_f16 operand: the fp16 x
-// fp16 products are exact in fp32 and the group scale absorbs the 2^24.
-constexpr float kSub = 16777216.f;  // 2^24
-
-// Split-precision activations (XS: fp32/bf16 split into fp16 hi + lo) have subnormal lo
-// parts, and subnormal x subnormal products lose bits in v_dot2, so those variants encode
-// codes as exact normal fp16 integers instead: (1024 + q) with the 1024 removed by one
-// v_pk_add_f16.
+// K-quant codes (small unsigned integers q < 1024, masked into the low bits of each fp16 lane)
+// become exact normal fp16 integers for v_dot2_f32_f16: (1024 + q) by OR-ing in the exponent,
+// then the 1024 removed by one v_pk_add_f16 (exact). The bare bits would be the fp16
+// subnormals q * 2^-24, but v_dot2_f32_f16 does not form products of subnormal operands
+// exactly on gfx950 (measured: relative errors up to ~5e-5 per product, far more once
+// accumulated), while every product of normal fp16 values is exact in fp32.
 template <bool XS>
 __device__ __forceinline__ uint32_t enc_codes(uint32_t codes) {
-  if constexpr (XS) {
-    const half2_t r = __builtin_bit_cast(half2_t, codes | 0x64006400u) - (half2_t){(_Float16)1024.f, (_Float16)1024.f};
-    return __builtin_bit_cast(uint32_t, r);
-  } else {
-    return codes;
-  }
+  const half2_t r = __builtin_bit_cast(half2_t, codes | 0x64006400u) - (half2_t){(_Float16)1024.f, (_Float16)1024.f};
+  return __builtin_bit_cast(uint32_t, r);
 }
 template <bool XS>
-__device__ __forceinline__ constexpr float enc_scale() { return XS ? 1.f : kSub; }
+__device__ __forceinline__ constexpr float enc_scale() { return 1.f; }
 
 // Both 16-bit halves shifted right by 8 (v_pk_lshrrev_b16): bytes 1 and 3 move to 0 and 2.
 typedef unsigned short ushort2_t __attribute__((ext_vector_type(2)));
@@ -625,11 +618,8 @@ __device__ __forceinline__ void load_x32(const void* x, int dt, int64_t i0, bool
 
 __device__ __forceinline__ void store_y(void* y, int dt, int64_t i, float v) {
   if (dt == DT_F16) reinterpret_cast<_Float16*>(y)[i] = (_Float16)v;
-  else if (dt == DT_BF16) {
-    uint32_t b = __builtin_bit_cast(uint32_t, v);
-    b += 0x7FFFu + ((b >> 16) & 1u);  // round to nearest even
-    reinterpret_cast<uint16_t*>(y)[i] = (uint16_t)(b >> 16);
-  } else reinterpret_cast<float*>(y)[i] = v;
+  else if (dt == DT_BF16) reinterpret_cast<uint16_t*>(y)[i] = (uint16_t)f32_to_bf16_bits(v);
+  else reinterpret_cast<float*>(y)[i] = v;
 }
 
 // Full-wave sum with DPP row operations; the total lands in lane 63.

@@ -25,6 +25,7 @@ EXPORTS = {
     "gsq_version": (_I32, []),
     "gsq_block_bytes": (_I32, [_I32]),
     "gsq_set_tables": (_I32, [_I32, _VP, _I64, _I64, _VP, _I64]),
+    "gsq_prepare": (_I32, [_VP]),
     "gsq_tables_ready": (_I32, [_I32]),
     "gsq_dequant": (_I32, [_I32, _VP, _I64, _VP, _VP]),
     "gsq_qmv": (_I32, [_I32, _VP, _VP, _I32, _VP, _I32, _I64, _I64, _I64, _VP]),
@@ -83,3 +84,13 @@ def ensure_tables(qtype: str, device: torch.device) -> None:
 
 def stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def prepare(device=None, stream=None) -> None:
+    """Build the fixed tables and the QMM workspace of ``stream`` (default: the current
+    stream) on ``device`` so that later calls on that stream allocate nothing; required
+    before capturing QMM calls on a stream into a HIP graph (``gsq_prepare``)."""
+    device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    with torch.cuda.device(device):
+        s = torch.cuda.current_stream(device) if stream is None else stream
+        check(lib().gsq_prepare(s.cuda_stream), "gsq_prepare")

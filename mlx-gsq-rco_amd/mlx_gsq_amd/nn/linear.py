@@ -2,16 +2,27 @@
 
 Drop-in counterpart of mlx_gsq/nn/linear.py:6-24 ``GSQLinear``: built from a
 ``PackedWeight``, it keeps the untouched GGUF payload resident on the device and exposes
-``packed_weight``, ``in_features``, ``out_features`` and ``qtype``. A single activation
-row goes to the fused QMV, more rows to the tiled QMM, as in the reference; the optional
-bias is added afterwards.
+``packed_weight``, ``in_features``, ``out_features`` and ``qtype``. The reference sends one
+activation row to the fused QMV and every larger batch to the tiled QMM; here batches below
+the QMM threshold (``QMM_MIN_ROWS`` rows) go through ``quantized_matvec``, whose routing
+keeps 2-3 rows on the vector kernel where that is faster on gfx950 and sends larger fp16
+batches to the small-batch QMM; from the threshold on, the tiled QMM. The results agree
+with the reference's within the operators' tolerances either way. The optional bias is
+added afterwards.
 """
 from __future__ import annotations
 
 import torch
 
-from ..runtime.kernels.qmm import quantized_matmul
+from ..runtime.kernels.qmm import QMM_MIN_ROWS, quantized_matmul
 from ..runtime.kernels.qmv import quantized_matvec
+
+
+def _apply(x, packed, qtype, out_features, in_features):
+    """One packed product, routed by batch size (see the module docstring)."""
+    rows = x.numel() // in_features
+    fn = quantized_matvec if rows < QMM_MIN_ROWS else quantized_matmul
+    return fn(x, packed, qtype=qtype, out_features=out_features, in_features=in_features)
 
 
 class GSQLinear(torch.nn.Module):
@@ -24,13 +35,7 @@ class GSQLinear(torch.nn.Module):
         self.qtype = weight.quantization_type
 
     def forward(self, x):
-        rows = x.numel() // self.in_features
-        if rows == 1:
-            y = quantized_matvec(x, self.packed_weight, qtype=self.qtype,
-                                 out_features=self.out_features, in_features=self.in_features)
-        else:
-            y = quantized_matmul(x, self.packed_weight, qtype=self.qtype,
-                                 out_features=self.out_features, in_features=self.in_features)
+        y = _apply(x, self.packed_weight, self.qtype, self.out_features, self.in_features)
         return y if self.bias is None else y + self.bias
 
     def extra_repr(self) -> str:
@@ -44,8 +49,8 @@ class GSQFusedLinear(torch.nn.Module):
     Packed rows are whole superblocks, row-major, so concatenating the matrices along the
     output dimension is a byte concatenation; it is done once here, on the weights' device.
     ``forward`` returns one output per weight (views of one result), computed exactly as
-    ``GSQLinear`` computes the concatenated matrix (one row → QMV, more → QMM). No counterpart
-    in the reference, whose model applies each projection on its own.
+    ``GSQLinear`` computes the concatenated matrix. No counterpart in the reference, whose
+    model applies each projection on its own.
     """
 
     def __init__(self, weights, biases=None):
@@ -69,13 +74,7 @@ class GSQFusedLinear(torch.nn.Module):
         self.biases = biases
 
     def forward(self, x):
-        rows = x.numel() // self.in_features
-        if rows == 1:
-            y = quantized_matvec(x, self.packed_weight, qtype=self.qtype,
-                                 out_features=self.out_features, in_features=self.in_features)
-        else:
-            y = quantized_matmul(x, self.packed_weight, qtype=self.qtype,
-                                 out_features=self.out_features, in_features=self.in_features)
+        y = _apply(x, self.packed_weight, self.qtype, self.out_features, self.in_features)
         outs = y.split(self.splits, dim=-1)
         if self.biases is None:
             return outs

@@ -414,7 +414,7 @@ def test_qmv_hip_graph_replays_match_eager():
 def test_qmm_hip_graph_replays_match_eager():
     """Tiled (stream-K split tiles) and small-batch QMM launches captured in a HIP graph give the
     eager results bit for bit on every replay: the split-tile counters reset themselves, so
-    nothing is cleared between calls (the first eager call allocates the workspace)."""
+    nothing is cleared between calls (gsq_prepare gives the capture stream its workspace)."""
     from mlx_gsq_amd import _lib
     from mlx_gsq_amd.formats import TYPE_IDS
     lib = _lib.lib()
@@ -435,6 +435,7 @@ def test_qmm_hip_graph_replays_match_eager():
     eager = [c[3].clone() for c in cases]
     graph = torch.cuda.CUDAGraph()
     cap = torch.cuda.Stream()
+    _lib.prepare(stream=cap)
     cap.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(cap):
         with torch.cuda.graph(graph, stream=cap):
@@ -443,7 +444,7 @@ def test_qmm_hip_graph_replays_match_eager():
     for rep in range(4):
         for c in cases:
             c[3].fill_(float("nan"))          # eager work between replays
-        launch_all(torch.cuda.current_stream().cuda_stream)  # eager QMM calls share the workspace
+        launch_all(torch.cuda.current_stream().cuda_stream)  # eager QMM calls between replays
         torch.cuda.synchronize()
         for c, e in zip(cases, eager):
             assert torch.equal(c[3], e), f"eager call before replay {rep} differs"

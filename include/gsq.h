@@ -78,6 +78,19 @@ int gsq_qmv(int qtype_id, const void* packed, const void* x, int x_dtype, void* 
 int gsq_qmm(int qtype_id, const void* packed, const void* x, int x_dtype, void* y, int y_dtype,
             int64_t M, int64_t N, int64_t K, void* stream);
 
+/* gsq_qmm without any allocation, for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. Split-tile partials and arrival counters live in a fixed device array of
+ * 32 MiB + 4 KiB that each device holds until the process ends (tile heights are lowered until
+ * the partials of one workgroup per CU fit; a device with more than 256 CUs is refused with
+ * GSQ_E_VALUE). Every call on a device shares that array, so calls that overlap on one device
+ * (several streams, concurrent graph nodes) race and give wrong results: serialize them. Fixed
+ * tables must exist first (gsq_prepare, gsq_set_tables); a call that would need to build one
+ * returns GSQ_E_VALUE instead. Results match gsq_qmm within the QMM tolerance (bit for bit
+ * where both pick the same tile plan, as for M <= 64). */
+int gsq_qmm_noalloc(int qtype_id, const void* packed, const void* x, int x_dtype, void* y, int y_dtype,
+                    int64_t M, int64_t N, int64_t K, void* stream);
+
 /* Packed embedding gather: out[t, :] = dequantized row ids[t] of a (vocab, dims) packed table,
  * rounded to out_dtype (GSQ_F32 / GSQ_F16 / GSQ_BF16, round-to-nearest-even from the exact
  * float32 value); ids are int32 (GSQ_IDS_I32) or int64 (GSQ_IDS_I64), n_ids of them; dims a

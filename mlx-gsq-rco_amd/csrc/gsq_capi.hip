@@ -59,11 +59,21 @@ bool is_grid_type(int t) {
 
 bool uses_ksigns(int t) { return t == IQ2_XXS || t == IQ2_XS || t == IQ3_XXS; }
 
+// Scratch of the allocation-free QMM entry point (gsq_qmm_noalloc): arrival counters (up to
+// 1024 workgroups) followed by the split-tile partials of up to 256 workgroups at 64-row
+// activation tiles (2 slots x 64 KiB each); the launch plan lowers the tile height until the
+// partials fit. Every call on a device shares that device's copy: counters are zero when the
+// code object loads and every launch leaves them at zero.
+constexpr size_t kNoAllocCounterBytes = 4096;
+constexpr size_t kNoAllocPartBytes = size_t(32) << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocCounterBytes + kNoAllocPartBytes];
+
 struct DevState {
   std::map<int, uint16_t*> grids;     // per grid type
   std::map<int, uint8_t*> qmv_tbls;   // per type with a QMV LDS table
   uint8_t* ksigns = nullptr;
   int num_cus = 0;
+  uint8_t* scratch = nullptr;         // this device's address of `scratch`
   // QMM workspaces, one per stream: launches on one stream run in order, so they may share
   // a workspace; launches on different streams may overlap and never share one
   std::map<hipStream_t, QmmWorkspace> qmm_ws;
@@ -102,8 +112,9 @@ int current_device(int* dev) {
 }
 
 // Resolve the device tables for `qt` on the current device (caller holds no lock). A fixed
-// table not built yet is built here unless `s` is capturing (gsq_prepare builds them first).
-int resolve(int qt, DevTables* tb, int* num_cus, hipStream_t s = nullptr) {
+// table not built yet is built here unless `s` is capturing or `may_alloc` is false
+// (gsq_prepare builds them first).
+int resolve(int qt, DevTables* tb, int* num_cus, hipStream_t s = nullptr, bool may_alloc = true) {
   int dev;
   if (int rc = current_device(&dev)) return rc;
   std::lock_guard<std::mutex> lk(g_mu);
@@ -128,6 +139,9 @@ int resolve(int qt, DevTables* tb, int* num_cus, hipStream_t s = nullptr) {
     if (capturing(s))
       return fail(GSQ_E_VALUE, "the %s table is not built on device %d and the stream is capturing: "
                   "call gsq_prepare before capture", type_name(qt), dev);
+    if (!may_alloc)
+      return fail(GSQ_E_VALUE, "the %s table is not built on device %d: call gsq_prepare before the "
+                  "allocation-free entry point", type_name(qt), dev);
     if (int rc = upload_qmv_table(st, qt, nullptr, nullptr)) return rc;
   }
   auto tt = st.qmv_tbls.find(qt);
@@ -175,6 +189,29 @@ int qmm_workspace(hipStream_t s, QmmWorkspace* ws) {
     return fail(GSQ_E_HIP, "QMM workspace setup: %s", hipGetErrorString(e));
   }
   *ws = st.qmm_ws[s] = QmmWorkspace{part, cnt, groups, part_bytes};
+  return GSQ_OK;
+}
+
+// This device's address of `scratch` (host code never passes the symbol itself: on the host it
+// names a shadow variable, not device memory); looked up once per device, with it current.
+int noalloc_scratch(uint8_t** p, int* num_cus) {
+  int dev;
+  if (int rc = current_device(&dev)) return rc;
+  std::lock_guard<std::mutex> lk(g_mu);
+  DevState& st = g_dev[dev];
+  if (st.num_cus == 0) {
+    hipError_t e = hipDeviceGetAttribute(&st.num_cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return fail(GSQ_E_HIP, "hipDeviceGetAttribute: %s", hipGetErrorString(e));
+  }
+  if (!st.scratch) {
+    void* ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(GSQ_E_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    st.scratch = static_cast<uint8_t*>(ptr);
+  }
+  *p = st.scratch;
+  *num_cus = st.num_cus;
   return GSQ_OK;
 }
 
@@ -266,7 +303,10 @@ int gsq_prepare(void* stream) {
     if (int rc = resolve(qt, &tb, &cus, s)) return rc;
   }
   QmmWorkspace ws;
-  return qmm_workspace(s, &ws);
+  if (int rc = qmm_workspace(s, &ws)) return rc;
+  uint8_t* sp;
+  int cus;
+  return noalloc_scratch(&sp, &cus);
 }
 
 int gsq_tables_ready(int qt) {
@@ -320,6 +360,29 @@ int gsq_qmm(int qt, const void* packed, const void* x, int xdt, void* y, int ydt
   if (int rc = qmm_workspace(static_cast<hipStream_t>(stream), &ws)) return rc;
   hipError_t e = launch_qmm(qt, static_cast<const uint8_t*>(packed), x, xdt, y, ydt, M, N, (int)K, tb, cus, ws,
                             static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(GSQ_E_HIP, "qmm launch: %s", hipGetErrorString(e));
+  return GSQ_OK;
+}
+
+int gsq_qmm_noalloc(int qt, const void* packed, const void* x, int xdt, void* y, int ydt, int64_t M, int64_t N,
+                    int64_t K, void* stream) {
+  if (int rc = check_common(qt, packed, M, N, K, xdt, ydt)) return rc;
+  if (!x || !y) return fail(GSQ_E_VALUE, "NULL pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  DevTables tb;
+  int cus;
+  if (int rc = resolve(qt, &tb, &cus, s, /*may_alloc=*/false)) return rc;
+  uint8_t* sp;
+  if (int rc = noalloc_scratch(&sp, &cus)) return rc;
+  // the partials of one workgroup per CU at the smallest tile plan (64-row tiles: 2 slots of
+  // 64 KiB) must fit the scratch
+  const long long need = 2ll * cus * 64 * 1024;
+  if (cus > (int)(kNoAllocCounterBytes / sizeof(int)) || need > (long long)kNoAllocPartBytes)
+    return fail(GSQ_E_VALUE, "gsq_qmm_noalloc: %d workgroups need %lld bytes of partial tiles; its scratch holds "
+                "%zu (use gsq_qmm)", cus, need, kNoAllocPartBytes);
+  QmmWorkspace ws{reinterpret_cast<float*>(sp + kNoAllocCounterBytes), reinterpret_cast<int*>(sp),
+                  (int)(kNoAllocCounterBytes / sizeof(int)), (long long)kNoAllocPartBytes};
+  hipError_t e = launch_qmm(qt, static_cast<const uint8_t*>(packed), x, xdt, y, ydt, M, N, (int)K, tb, cus, ws, s);
   if (e != hipSuccess) return fail(GSQ_E_HIP, "qmm launch: %s", hipGetErrorString(e));
   return GSQ_OK;
 }

@@ -30,6 +30,7 @@ EXPORTS = {
     "gsq_dequant": (_I32, [_I32, _VP, _I64, _VP, _VP]),
     "gsq_qmv": (_I32, [_I32, _VP, _VP, _I32, _VP, _I32, _I64, _I64, _I64, _VP]),
     "gsq_qmm": (_I32, [_I32, _VP, _VP, _I32, _VP, _I32, _I64, _I64, _I64, _VP]),
+    "gsq_qmm_noalloc": (_I32, [_I32, _VP, _VP, _I32, _VP, _I32, _I64, _I64, _I64, _VP]),
     "gsq_embedding": (_I32, [_I32, _VP, _VP, _I32, _I64, _I64, _I64, _VP, _I32, _VP]),
     "gsq_last_error": (ctypes.c_char_p, []),
 }

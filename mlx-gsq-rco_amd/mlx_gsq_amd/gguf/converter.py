@@ -1,162 +1,206 @@
-"""Lossless GGUF -> "mlx-gsq-packed-v1" Safetensors conversion and its SHA-256 verification.
+"""GGUF -> packed container conversion, lossless and verified by SHA-256.
 
-Counterpart of mlx_gsq/gguf/converter.py:22-186 with the same public names and container:
-every GGUF tensor becomes a 1-D U8 Safetensors tensor holding its untouched packed bytes (no
-dequantization), the header's ``__metadata__`` carries ``format``, ``source_format``,
-``architecture``, ``note`` and the compact JSON ``tensor_quantization`` map (qtype, qtype_id,
-gguf_shape, logical_shape = reversed, num_elements, block_elements, block_bytes), the header
-is padded with spaces to 8 bytes, and a sidecar ``<file>.manifest.json`` records the source
-and every tensor's extent (plus the verification hashes). The container is written to a
-``.partial`` file and renamed only when complete.
+Stands in for mlx_gsq/gguf/converter.py:59-186 (``convert_gguf_to_safetensors``,
+``verify_conversion``, ``convert_gguf_to_mlx``; same arguments, return values, sidecar
+manifest and exception types). The container layout is in ``container.py``.
+
+How it works here:
+
+* One read of the source. Each tensor's payload is copied from a read-only memory map of the
+  GGUF file into the container and hashed in the same pass; verification then re-reads only
+  the written container and compares its per-tensor digests with those of the copy.
+* Nothing half-written is left in place. The container and the sidecar manifest are written
+  to temporary files beside their targets, flushed to disk, and renamed over the targets only
+  when complete (and, with verification on, checked): a failed conversion leaves no container
+  and no stale manifest of its own.
+* ``verify_conversion`` on its own hashes the source ranges and the container's tensors over a
+  thread pool (``hashlib`` releases the GIL on large buffers).
+
+The sidecar ``<container>.manifest.json`` holds ``format``, ``container`` (file name),
+``source`` (path, file_size, gguf_version, architecture, name), ``tensor_count``, ``tensors``
+(name -> the reader's ``TensorInfo.as_dict()``) and, after verification, ``verification``
+(algorithm, status, tensor_count, all_packed_bytes_identical, tensor_hashes).
 """
 from __future__ import annotations
 
+import contextlib
 import hashlib
 import json
+import mmap
 import os
-import struct
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
-from .parser import QUANT_BLOCK_SIZES
+from . import container
 from .reader import GGUFReader
 
-FORMAT = "mlx-gsq-packed-v1"
-COPY_CHUNK_SIZE = 16 * 1024 * 1024
+FORMAT = container.FORMAT
+CHUNK = 64 * 1024 * 1024  # bytes per write and per hash update
+_HASH_THREADS = max(1, min(8, os.cpu_count() or 1))
 
 
-def _container_header(reader: GGUFReader) -> bytes:
-    quant = {}
-    entries = {}
-    cursor = 0
+def _sidecar(output: Path) -> Path:
+    return output.with_name(output.name + ".manifest.json")
+
+
+@contextlib.contextmanager
+def _replace_when_done(target: Path):
+    """Yield a temporary path beside ``target``; on a clean exit it is renamed over ``target``,
+    on any exception (KeyboardInterrupt included) it is deleted."""
+    fd, tmp = tempfile.mkstemp(dir=target.parent, prefix=f".{target.name}.", suffix=".tmp")
+    os.close(fd)
+    tmp = Path(tmp)
+    try:
+        yield tmp
+        os.replace(tmp, target)
+    finally:
+        if tmp.exists():
+            tmp.unlink()
+
+
+def _write_json(path: Path, doc: dict) -> None:
+    with _replace_when_done(path) as tmp:
+        tmp.write_text(json.dumps(doc, ensure_ascii=False, indent=2) + "\n")
+
+
+def _open_map(path: Path):
+    """Read-only map of a whole file (an empty file maps to an empty bytes object)."""
+    if path.stat().st_size == 0:
+        return contextlib.nullcontext(b"")
+    f = path.open("rb")
+    try:
+        return mmap.mmap(f.fileno(), 0, access=mmap.ACCESS_READ)
+    finally:
+        f.close()  # the map keeps its own reference to the file
+
+
+def _digest(buf, start: int, size: int) -> str:
+    h = hashlib.sha256()
+    with memoryview(buf) as mv:
+        for at in range(start, start + size, CHUNK):
+            with mv[at:min(at + CHUNK, start + size)] as part:
+                h.update(part)
+    return h.hexdigest()
+
+
+def _digests(path: Path, ranges) -> list:
+    """SHA-256 hex digest of each (offset, size) range of ``path``; ranges past the end of the
+    file raise ValueError."""
+    size = path.stat().st_size
+    for start, n in ranges:
+        if start < 0 or start + n > size:
+            raise ValueError(f"{path.name}: range [{start}, {start + n}) lies past the end of the file ({size})")
+    with _open_map(path) as buf:
+        with ThreadPoolExecutor(_HASH_THREADS) as pool:
+            return list(pool.map(lambda r: _digest(buf, *r), ranges))
+
+
+def _container_digests(path: Path, reader: GGUFReader) -> dict:
+    """Check the container's layout against the GGUF directory, then hash its tensors."""
+    header, data_start = container.read_header(path)
+    expected = data_start + sum(t.num_bytes for t in reader.tensors)
+    actual = path.stat().st_size
+    if actual != expected:
+        raise ValueError(f"{path.name} holds {actual} bytes; its GGUF tensors need {expected}")
+    ranges = []
     for t in reader.tensors:
-        per_block, block_bytes = QUANT_BLOCK_SIZES[int(t.quantization_type)]
-        quant[t.name] = {"qtype": t.quantization_type.name, "qtype_id": int(t.quantization_type),
-                         "gguf_shape": list(t.shape), "logical_shape": list(reversed(t.shape)),
-                         "num_elements": t.num_elements, "block_elements": per_block, "block_bytes": block_bytes}
-        entries[t.name] = {"dtype": "U8", "shape": [t.num_bytes], "data_offsets": [cursor, cursor + t.num_bytes]}
-        cursor += t.num_bytes
-    header = {"__metadata__": {
-        "format": FORMAT,
-        "source_format": "GGUF",
-        "architecture": str(reader.metadata.get("general.architecture", "")),
-        "note": "U8 tensors contain original GGUF packed bytes; custom kernels required",
-        "tensor_quantization": json.dumps(quant, separators=(",", ":")),
-    }}
-    header.update(entries)
-    raw = json.dumps(header, ensure_ascii=False, separators=(",", ":")).encode("utf-8")
-    return raw + b" " * (-len(raw) % 8)
+        entry = header.get(t.name)
+        if not isinstance(entry, dict) or entry.get("dtype") != "U8" or entry.get("shape") != [t.num_bytes]:
+            raise ValueError(f"{path.name}: tensor {t.name!r} is missing or is not U8[{t.num_bytes}]")
+        lo, hi = entry.get("data_offsets", (0, -1))
+        if hi - lo != t.num_bytes:
+            raise ValueError(f"{path.name}: tensor {t.name!r} has data offsets {lo}..{hi}")
+        ranges.append((data_start + lo, t.num_bytes))
+    return dict(zip((t.name for t in reader.tensors), _digests(path, ranges)))
+
+
+def _compare(reader: GGUFReader, want: dict, got: dict) -> None:
+    for t in reader.tensors:
+        if want[t.name] != got[t.name]:
+            raise ValueError(f"payload of {t.name!r} in the container is not the GGUF payload "
+                             f"(sha256 {got[t.name][:16]}… vs {want[t.name][:16]}…)")
+
+
+def _record(digests: dict) -> dict:
+    return {"algorithm": "sha256", "status": "passed", "tensor_count": len(digests),
+            "all_packed_bytes_identical": True, "tensor_hashes": dict(digests)}
 
 
 def build_manifest(reader: GGUFReader, output_name: str) -> dict:
+    """The sidecar manifest of a container named ``output_name`` converted from ``reader``."""
+    meta = reader.metadata
     return {
         "format": FORMAT,
         "container": output_name,
         "source": {"path": str(reader.path), "file_size": reader.file_size, "gguf_version": reader.version,
-                   "architecture": reader.metadata.get("general.architecture"),
-                   "name": reader.metadata.get("general.name")},
+                   "architecture": meta.get("general.architecture"), "name": meta.get("general.name")},
         "tensor_count": len(reader.tensors),
         "tensors": {t.name: t.as_dict() for t in reader.tensors},
     }
 
 
-def _manifest_path(output: Path) -> Path:
-    return output.with_suffix(output.suffix + ".manifest.json")
-
-
-def _copy(src, dst, offset: int, size: int, name: str) -> None:
-    src.seek(offset)
-    left = size
-    while left:
-        chunk = src.read(min(left, COPY_CHUNK_SIZE))
-        if not chunk:
-            raise IOError(f"short GGUF read for {name}")
-        dst.write(chunk)
-        left -= len(chunk)
-
-
 def convert_gguf_to_safetensors(input_path, output_path, *, overwrite: bool = False, verify: bool = True) -> Path:
-    """Stream the packed tensors of a GGUF file into a Safetensors container (see module doc);
-    with ``verify`` the result is checked tensor by tensor against the GGUF byte ranges and the
-    hashes are recorded in the manifest."""
+    """Copy every tensor of a GGUF file, byte for byte, into a packed container at
+    ``output_path`` and write its sidecar manifest; return the container's resolved path.
+    Raises FileExistsError if the container exists and ``overwrite`` is false, GGUFError for a
+    malformed source and ValueError if verification finds a difference."""
     reader = GGUFReader(input_path)
-    output = Path(output_path).expanduser().resolve()
-    if output.exists() and not overwrite:
-        raise FileExistsError(output)
-    output.parent.mkdir(parents=True, exist_ok=True)
-    partial = output.with_suffix(output.suffix + ".partial")
-    if partial.exists():
-        partial.unlink()
-    header = _container_header(reader)
-    try:
-        with reader.path.open("rb") as src, partial.open("xb") as dst:
-            dst.write(struct.pack("<Q", len(header)))
+    out = Path(output_path).expanduser().resolve()
+    if out.exists() and not overwrite:
+        raise FileExistsError(out)
+    out.parent.mkdir(parents=True, exist_ok=True)
+    header = container.build_header(reader.tensors, str(reader.metadata.get("general.architecture", "")))
+    copied = {}
+    with _replace_when_done(out) as tmp:
+        with _open_map(reader.path) as src, tmp.open("wb") as dst:
             dst.write(header)
-            for t in reader.tensors:
-                _copy(src, dst, t.absolute_offset, t.num_bytes, t.name)
+            with memoryview(src) as mv:
+                for t in reader.tensors:
+                    h = hashlib.sha256()
+                    for at in range(t.absolute_offset, t.absolute_offset + t.num_bytes, CHUNK):
+                        with mv[at:min(at + CHUNK, t.absolute_offset + t.num_bytes)] as part:
+                            h.update(part)
+                            dst.write(part)
+                    copied[t.name] = h.hexdigest()
             dst.flush()
             os.fsync(dst.fileno())
-        partial.replace(output)
-        mpath = _manifest_path(output)
-        mpath.write_text(json.dumps(build_manifest(reader, output.name), ensure_ascii=False, indent=2) + "\n")
         if verify:
-            verify_conversion(reader.path, output, mpath, record_hashes=True)
-    except BaseException:
-        if partial.exists():
-            partial.unlink()
-        raise
-    return output
-
-
-def _sha256(f, offset: int, size: int) -> str:
-    h = hashlib.sha256()
-    f.seek(offset)
-    left = size
-    while left:
-        chunk = f.read(min(left, COPY_CHUNK_SIZE))
-        if not chunk:
-            raise IOError("short read during verification")
-        h.update(chunk)
-        left -= len(chunk)
-    return h.hexdigest()
+            _compare(reader, copied, _container_digests(tmp, reader))
+    manifest = build_manifest(reader, out.name)
+    if verify:
+        manifest["verification"] = _record(copied)
+    _write_json(_sidecar(out), manifest)
+    return out
 
 
 def verify_conversion(input_path, output_path, manifest_path=None, *, record_hashes: bool = False) -> dict:
-    """Check the container's size, every entry (U8, one dimension of the tensor's byte count),
-    the manifest's tensor records and the SHA-256 of every tensor's bytes against the GGUF
-    source; raises ValueError on the first difference."""
+    """Check a container against its GGUF source: layout, every tensor's SHA-256, and the
+    manifest's tensor records. Returns the verification record (and stores it in the manifest
+    when ``record_hashes``); raises ValueError on the first difference."""
     reader = GGUFReader(input_path)
-    output = Path(output_path)
-    mpath = Path(manifest_path) if manifest_path else _manifest_path(output)
+    out = Path(output_path)
+    mpath = Path(manifest_path) if manifest_path else _sidecar(out)
     manifest = json.loads(mpath.read_text())
-    hashes = {}
-    with output.open("rb") as packed, reader.path.open("rb") as src:
-        header_len = struct.unpack("<Q", packed.read(8))[0]
-        header = json.loads(packed.read(header_len))
-        base = 8 + header_len
-        want_size = base + sum(t.num_bytes for t in reader.tensors)
-        if output.stat().st_size != want_size:
-            raise ValueError(f"safetensors size mismatch: {output.stat().st_size} != {want_size}")
-        for t in reader.tensors:
-            entry = header.get(t.name)
-            if not entry or entry["dtype"] != "U8" or entry["shape"] != [t.num_bytes]:
-                raise ValueError(f"invalid safetensors entry for {t.name}")
-            start, end = entry["data_offsets"]
-            digest = _sha256(src, t.absolute_offset, t.num_bytes)
-            if _sha256(packed, base + start, end - start) != digest:
-                raise ValueError(f"packed bytes differ for {t.name}")
-            hashes[t.name] = digest
-            rec = manifest["tensors"].get(t.name)
-            if not rec or any(rec.get(k) != v for k, v in t.as_dict().items()):
-                raise ValueError(f"manifest differs for {t.name}")
-    result = {"algorithm": "sha256", "status": "passed", "tensor_count": len(hashes),
-              "all_packed_bytes_identical": True, "tensor_hashes": hashes}
+    source = dict(zip((t.name for t in reader.tensors),
+                      _digests(reader.path, [(t.absolute_offset, t.num_bytes) for t in reader.tensors])))
+    _compare(reader, source, _container_digests(out, reader))
+    recorded = manifest.get("tensors", {})
+    for t in reader.tensors:
+        want = t.as_dict()
+        have = recorded.get(t.name) or {}
+        wrong = sorted(k for k, v in want.items() if have.get(k) != v)
+        if wrong:
+            raise ValueError(f"{mpath.name}: record of {t.name!r} disagrees with the GGUF file on {', '.join(wrong)}")
+    result = _record(source)
     if record_hashes:
         manifest["verification"] = result
-        mpath.write_text(json.dumps(manifest, ensure_ascii=False, indent=2) + "\n")
+        _write_json(mpath, manifest)
     return result
 
 
 def convert_gguf_to_mlx(input_path, output_dir=".", overwrite: bool = False) -> bool:
-    """Older entry point of the reference: converts into ``<output_dir>/model-packed.safetensors``."""
+    """Convert into ``<output_dir>/model-packed.safetensors`` (the reference's old entry point);
+    True on success, exceptions as ``convert_gguf_to_safetensors``."""
     convert_gguf_to_safetensors(input_path, Path(output_dir) / "model-packed.safetensors", overwrite=overwrite)
     return True

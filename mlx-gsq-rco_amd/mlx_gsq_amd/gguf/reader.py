@@ -1,32 +1,41 @@
-"""GGUF (v2 / v3) directory reader: metadata and tensor extents, no payload reads.
+"""GGUF (v2 / v3) header reader: typed metadata and validated tensor extents.
 
-Counterpart of mlx_gsq/gguf/parser.py:72-145 (``GGUFReader``, ``TensorInfo``, ``GGUFError``)
-with the same public names, fields and checks: magic, version 2 or 3, unique metadata keys and
-tensor names, a positive integer ``general.alignment`` (default 32), element counts that fill
-whole blocks, tensors inside the file and not overlapping. The header is parsed from a
-read-only memory map, so a multi-GB model costs only the pages of its header.
+Stands in for mlx_gsq/gguf/parser.py:45-144 (``GGUFReader``, ``TensorInfo``, ``GGUFError``):
+the same public names and fields, and it accepts and rejects the same files (bad magic,
+versions other than 2 and 3, repeated metadata keys or tensor names, an alignment that is not
+a positive integer, element counts that do not fill whole blocks, payloads outside the file or
+overlapping each other). Written from the published GGUF layout:
 
-The file layout is GGUF's published one: magic "GGUF", u32 version, u64 tensor count, u64
-metadata count, the metadata key/value pairs (u64-length UTF-8 key, u32 value type, value),
-then per tensor its name, u32 rank, u64 dims (innermost first), u32 GGML type and u64 offset
-from the data section, which starts at the next multiple of the alignment.
+    "GGUF" | u32 version | u64 n_tensors | u64 n_kv
+    n_kv x      ( str key | u32 type | value )
+    n_tensors x ( str name | u32 rank | rank x u64 dim (innermost first) | u32 ggml type | u64 offset )
+    zero padding to general.alignment (default 32), then the data section; tensor offsets
+    count from its start.
+
+Strings are u64 byte length + UTF-8; arrays are u32 item type + u64 count + items. Only the
+header pages of the file are touched: it is read through a read-only memory map, numeric arrays
+(tokenizer vocabularies run to 10^5 entries) are decoded in bulk with numpy.
 """
 from __future__ import annotations
 
-import json
+import math
 import mmap
 import struct
-from collections import defaultdict
 from dataclasses import dataclass
 from enum import IntEnum
 from pathlib import Path
-from typing import Any
+
+import numpy as np
 
 from .parser import GGMLQuantizationType, QUANT_BLOCK_SIZES
 
+MAGIC = b"GGUF"
+SUPPORTED_VERSIONS = (2, 3)
+DEFAULT_ALIGNMENT = 32
+
 
 class GGUFError(ValueError):
-    pass
+    """A file that is not a well-formed GGUF v2/v3 file."""
 
 
 class GGUFValueType(IntEnum):
@@ -34,12 +43,23 @@ class GGUFValueType(IntEnum):
     BOOL = 7; STRING = 8; ARRAY = 9; UINT64 = 10; INT64 = 11; FLOAT64 = 12
 
 
-# scalar value types -> struct format (little endian)
-_SCALARS = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 7: "<?", 10: "<Q", 11: "<q", 12: "<d"}
+# fixed-width value types -> their little-endian numpy dtype
+_FIXED = {
+    GGUFValueType.UINT8: np.dtype("<u1"), GGUFValueType.INT8: np.dtype("<i1"),
+    GGUFValueType.UINT16: np.dtype("<u2"), GGUFValueType.INT16: np.dtype("<i2"),
+    GGUFValueType.UINT32: np.dtype("<u4"), GGUFValueType.INT32: np.dtype("<i4"),
+    GGUFValueType.FLOAT32: np.dtype("<f4"), GGUFValueType.BOOL: np.dtype("?"),
+    GGUFValueType.UINT64: np.dtype("<u8"), GGUFValueType.INT64: np.dtype("<i8"),
+    GGUFValueType.FLOAT64: np.dtype("<f8"),
+}
+_U32 = struct.Struct("<I")
+_U64 = struct.Struct("<Q")
 
 
 @dataclass(frozen=True)
 class TensorInfo:
+    """One tensor's directory entry. ``shape`` is GGUF order (innermost first);
+    ``absolute_offset`` is the file offset of its first payload byte."""
     name: str
     shape: tuple
     quantization_type: GGMLQuantizationType
@@ -49,171 +69,143 @@ class TensorInfo:
     num_bytes: int
 
     def as_dict(self) -> dict:
-        return {
-            "name": self.name,
-            "gguf_shape": list(self.shape),
-            "logical_shape": list(reversed(self.shape)),
-            "quantization_type": self.quantization_type.name,
-            "quantization_type_id": int(self.quantization_type),
-            "offset": self.offset,
-            "absolute_offset": self.absolute_offset,
-            "num_elements": self.num_elements,
-            "num_bytes": self.num_bytes,
-        }
+        """The manifest record of this tensor (the packed container's per-tensor entry)."""
+        return dict(name=self.name, gguf_shape=list(self.shape), logical_shape=list(self.shape[::-1]),
+                    quantization_type=self.quantization_type.name,
+                    quantization_type_id=int(self.quantization_type), offset=self.offset,
+                    absolute_offset=self.absolute_offset, num_elements=self.num_elements,
+                    num_bytes=self.num_bytes)
 
 
-class _Cursor:
-    """Sequential little-endian reads from a buffer, with end-of-file checks."""
+class _HeaderBytes:
+    """Bounds-checked little-endian decoding at a moving position of a byte buffer."""
 
-    def __init__(self, buf):
-        self.buf, self.pos = buf, 0
+    __slots__ = ("mem", "at")
 
-    def take(self, n: int) -> bytes:
-        end = self.pos + n
-        if n < 0 or end > len(self.buf):
-            raise GGUFError("unexpected end of file")
-        raw = self.buf[self.pos:end]
-        self.pos = end
-        return raw
+    def __init__(self, mem: memoryview):
+        self.mem, self.at = mem, 0
 
-    def scalar(self, fmt: str):
-        return struct.unpack(fmt, self.take(struct.calcsize(fmt)))[0]
+    def _need(self, n: int) -> int:
+        start = self.at
+        if n < 0 or start + n > len(self.mem):
+            raise GGUFError(f"header ends early: {n} bytes wanted at offset {start}, file has {len(self.mem)}")
+        self.at = start + n
+        return start
 
-    def string(self) -> str:
-        n = self.scalar("<Q")
+    def u32(self) -> int:
+        return _U32.unpack_from(self.mem, self._need(4))[0]
+
+    def u64(self) -> int:
+        return _U64.unpack_from(self.mem, self._need(8))[0]
+
+    def text(self) -> str:
+        n = self.u64()
+        start = self._need(n)
         try:
-            return self.take(n).decode("utf-8")
+            return str(self.mem[start:start + n], "utf-8")
         except UnicodeDecodeError as e:
-            raise GGUFError(f"invalid UTF-8 string: {e}") from None
+            raise GGUFError(f"string at offset {start} is not UTF-8 ({e.reason})") from None
 
-    def value(self, kind: int):
-        if kind in _SCALARS:
-            return self.scalar(_SCALARS[kind])
-        if kind == GGUFValueType.STRING:
-            return self.string()
-        if kind == GGUFValueType.ARRAY:
-            sub = self.scalar("<I")
-            n = self.scalar("<Q")
-            if sub in _SCALARS and sub != GGUFValueType.BOOL:  # fixed-size items: one slice
-                size = struct.calcsize(_SCALARS[sub])
-                raw = self.take(size * n)
-                return list(struct.unpack("<" + str(n) + _SCALARS[sub][1], raw))
-            return [self.value(sub) for _ in range(n)]
-        raise GGUFError(f"unsupported metadata type {kind}")
+    def fixed(self, kind: GGUFValueType, count: int) -> np.ndarray:
+        dt = _FIXED[kind]
+        start = self._need(dt.itemsize * count)
+        return np.frombuffer(self.mem, dtype=dt, count=count, offset=start)
+
+    def value_type(self) -> GGUFValueType:
+        code = self.u32()
+        try:
+            return GGUFValueType(code)
+        except ValueError:
+            raise GGUFError(f"unknown metadata value type {code} at offset {self.at - 4}") from None
+
+    def value(self, kind: GGUFValueType):
+        if kind in _FIXED:
+            return self.fixed(kind, 1)[0].item()
+        if kind is GGUFValueType.STRING:
+            return self.text()
+        item = self.value_type()  # ARRAY
+        count = self.u64()
+        if item in _FIXED:
+            return self.fixed(item, count).tolist()
+        return [self.value(item) for _ in range(count)]
 
 
 class GGUFReader:
-    """Validated GGUF metadata and tensor extents of one file."""
+    """The validated header of one GGUF file: ``version``, ``metadata`` (key -> Python value),
+    ``tensors`` (directory order), ``data_offset`` and ``file_size``."""
 
     def __init__(self, path):
         self.path = Path(path).expanduser().resolve()
         self.file_size = self.path.stat().st_size
-        with self.path.open("rb") as f:
-            if self.file_size < 4:
-                raise GGUFError("not a GGUF file")
-            with mmap.mmap(f.fileno(), 0, access=mmap.ACCESS_READ) as mm:
-                self._parse(_Cursor(mm))  # slices of the map are copies: nothing outlives it
+        if self.file_size < len(MAGIC):
+            raise GGUFError(f"{self.path.name}: too short for a GGUF file")
+        with self.path.open("rb") as f, mmap.mmap(f.fileno(), 0, access=mmap.ACCESS_READ) as mm:
+            view = memoryview(mm)
+            try:
+                self._read_header(_HeaderBytes(view))
+            finally:
+                view.release()
+        self._by_name = {t.name: t for t in self.tensors}
 
-    def _parse(self, c: _Cursor) -> None:
-        if c.take(4) != b"GGUF":
-            raise GGUFError("not a GGUF file")
-        self.version = c.scalar("<I")
-        if self.version not in (2, 3):
-            raise GGUFError(f"unsupported GGUF version {self.version}")
-        n_tensors, n_kv = c.scalar("<Q"), c.scalar("<Q")
-        self.metadata: dict = {}
+    def _read_header(self, h: _HeaderBytes) -> None:
+        if bytes(h.mem[:4]) != MAGIC:
+            raise GGUFError(f"{self.path.name}: no GGUF magic")
+        h.at = 4
+        self.version = h.u32()
+        if self.version not in SUPPORTED_VERSIONS:
+            raise GGUFError(f"GGUF version {self.version} is not supported (2 and 3 are)")
+        n_tensors, n_kv = h.u64(), h.u64()
+        meta: dict = {}
         for _ in range(n_kv):
-            key = c.string()
-            if key in self.metadata:
-                raise GGUFError(f"duplicate metadata key {key}")
-            kind = c.scalar("<I")
-            try:
-                GGUFValueType(kind)
-            except ValueError:
-                raise GGUFError(f"unsupported metadata type {kind}") from None
-            self.metadata[key] = c.value(kind)
-        entries = []
-        seen = set()
+            key = h.text()
+            if key in meta:
+                raise GGUFError(f"metadata key {key!r} appears twice")
+            meta[key] = h.value(h.value_type())
+        self.metadata = meta
+        directory = []
         for _ in range(n_tensors):
-            name = c.string()
-            if name in seen:
-                raise GGUFError(f"duplicate tensor {name}")
-            seen.add(name)
-            rank = c.scalar("<I")
-            shape = tuple(c.scalar("<Q") for _ in range(rank))
-            type_id = c.scalar("<I")
+            name = h.text()
+            dims = tuple(h.fixed(GGUFValueType.UINT64, h.u32()).tolist())
+            code = h.u32()
             try:
-                qtype = GGMLQuantizationType(type_id)
+                qtype = GGMLQuantizationType(code)
             except ValueError:
-                raise GGUFError(f"unknown GGML type {type_id} for {name}") from None
-            entries.append((name, shape, qtype, c.scalar("<Q")))
-        align = self.metadata.get("general.alignment", 32)
-        if isinstance(align, bool) or not isinstance(align, int) or align < 1:
-            raise GGUFError("invalid alignment")
-        self.data_offset = -(-c.pos // align) * align
-        tensors, extents = [], []
-        for name, shape, qtype, offset in entries:
-            count = 1
-            for dim in shape:
-                count *= dim
+                raise GGUFError(f"tensor {name!r} has unknown GGML type {code}") from None
+            directory.append((name, dims, qtype, h.u64()))
+        align = meta.get("general.alignment", DEFAULT_ALIGNMENT)
+        if not isinstance(align, int) or align <= 0:
+            raise GGUFError(f"general.alignment must be a positive integer, not {align!r}")
+        self.data_offset = -(-h.at // align) * align
+        self.tensors = tuple(self._place(directory))
+
+    def _place(self, directory):
+        """TensorInfo per directory entry; every payload whole, inside the file, and disjoint."""
+        names = set()
+        placed = []
+        for name, dims, qtype, rel in directory:
+            if name in names:
+                raise GGUFError(f"tensor name {name!r} appears twice")
+            names.add(name)
+            count = math.prod(dims)
             per_block, block_bytes = QUANT_BLOCK_SIZES[int(qtype)]
-            if count % per_block:
-                raise GGUFError(f"invalid {qtype.name} element count for {name}")
-            nbytes = count // per_block * block_bytes
-            start = self.data_offset + offset
+            blocks, rest = divmod(count, per_block)
+            if rest:
+                raise GGUFError(f"tensor {name!r}: {count} elements do not fill whole {qtype.name} blocks "
+                                f"of {per_block}")
+            start = self.data_offset + rel
+            nbytes = blocks * block_bytes
             if start + nbytes > self.file_size:
-                raise GGUFError(f"tensor outside file: {name}")
-            extents.append((start, start + nbytes, name))
-            tensors.append(TensorInfo(name, shape, qtype, offset, start, count, nbytes))
-        extents.sort()
-        for (_, end, a), (start, _, b) in zip(extents, extents[1:]):
-            if end > start:
-                raise GGUFError(f"overlapping tensors: {a}, {b}")
-        self.tensors = tuple(tensors)
-        self._by_name = {t.name: t for t in tensors}
+                raise GGUFError(f"tensor {name!r}: bytes [{start}, {start + nbytes}) run past the end of "
+                                f"the file ({self.file_size})")
+            placed.append(TensorInfo(name, dims, qtype, rel, start, count, nbytes))
+        # disjoint payloads: in start order, no payload begins before every earlier one has ended
+        reach, holder = -1, None
+        for t in sorted(placed, key=lambda t: (t.absolute_offset, t.num_bytes)):
+            if t.absolute_offset < reach:
+                raise GGUFError(f"tensors {holder!r} and {t.name!r} share payload bytes")
+            if t.absolute_offset + t.num_bytes > reach:
+                reach, holder = t.absolute_offset + t.num_bytes, t.name
+        return placed
 
     def tensor(self, name: str) -> TensorInfo:
         return self._by_name[name]
-
-    def analysis(self) -> dict:
-        """Summary of the file: source, metadata (long arrays elided), totals, per-type
-        tensor/parameter/byte counts and every tensor's extent."""
-        dist = defaultdict(lambda: {"tensor_count": 0, "parameter_count": 0, "byte_count": 0})
-        for t in self.tensors:
-            row = dist[t.quantization_type.name]
-            row["tensor_count"] += 1
-            row["parameter_count"] += t.num_elements
-            row["byte_count"] += t.num_bytes
-        meta = {k: ({"kind": "array", "length": len(v)} if isinstance(v, list) and len(v) > 256 else v)
-                for k, v in self.metadata.items()}
-        return {
-            "schema_version": 1,
-            "source": {"path": str(self.path), "file_size": self.file_size, "gguf_version": self.version,
-                       "data_offset": self.data_offset},
-            "metadata": meta,
-            "summary": {"total_tensors": len(self.tensors),
-                        "total_parameters": sum(t.num_elements for t in self.tensors),
-                        "total_tensor_bytes": sum(t.num_bytes for t in self.tensors)},
-            "quantization_distribution": dict(sorted(dist.items())),
-            "tensors": [t.as_dict() for t in self.tensors],
-        }
-
-
-class GGUFModelAnalyzer:
-    @staticmethod
-    def parse(model_path) -> dict:
-        return GGUFReader(model_path).analysis()
-
-
-def write_analysis(model_path, output_path) -> dict:
-    result = GGUFReader(model_path).analysis()
-    Path(output_path).write_text(json.dumps(result, ensure_ascii=False, indent=2) + "\n")
-    return result
-
-
-def get_tensor_quant_distribution(model_path) -> dict:
-    return {name: row["tensor_count"] for name, row in GGUFReader(model_path).analysis()["quantization_distribution"].items()}
-
-
-def get_quant_distribution_with_params(model_path) -> dict:
-    return GGUFReader(model_path).analysis()["quantization_distribution"]

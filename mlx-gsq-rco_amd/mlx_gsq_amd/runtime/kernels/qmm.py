@@ -2,8 +2,10 @@
 
 Drop-in counterpart of mlx_gsq/runtime/kernels/qmm.py:559-594 ``quantized_matmul``:
 same name, keyword arguments (``kt`` is accepted for compatibility; the gfx950 kernel
-chooses its own K tiling), validation and exceptions. Each weight tile is decoded once
-into an fp16 LDS tile and fed to MFMA with fp32 accumulation (libgsq.so).
+chooses its own K tiling), validation and exceptions. Each wave decodes its own weight rows
+straight from the packed superblocks (DMA'd into LDS) into fp16 MFMA operands in registers,
+once per product, and multiplies them with fp16 activation tiles staged in LDS, accumulating in
+fp32 (libgsq.so; M <= 16 runs a small-batch kernel that decodes every weight once as well).
 """
 from __future__ import annotations
 

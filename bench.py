@@ -9,13 +9,14 @@ per product) step time is reported beside it.
 
 Printed JSON line (one, on stdout):
   value         whole-step throughput: algorithmic bytes of the 44 launches / graph step time
-  roofline      the dominant QMV launch (largest share of kernel time): its algorithmic bytes
+  roofline      the dominant QMV launch (Q6_K 17408x5120, the step's longest): its algorithmic bytes
                 / its time per launch (median of 5 loops of 128 back-to-back launches, HIP
                 events on the launch stream), against the 8 TB/s HBM peak; `traffic` comes from the committed
                 rocprofv3 counter summary (profiles/qmv_traffic.json) when it covers the
                 same kernel and shape, else null
   per_type      per-type GB/s and fraction of peak over its 4 shapes (kernel time)
-  per_launch_us median kernel time of every (type, shape)
+  per_launch_us time per launch of every (type, shape): median of 3 loops of 32 back-to-back
+                launches of that product alone over 8 rotating weight copies (HIP events)
   qmm           tiled QMM (configs[2]: IQ3_S and Q6_K, both shapes, M in {182, 512, 2048}):
                 TFLOP/s and fraction of the 2.5 PFLOP/s dense fp16 MFMA peak per case
   layer_crossover  configs[3]: QMV vs QMM time per projection of the mixed layer, M in 1..16
@@ -48,6 +49,8 @@ SHAPES = ((5120, 5120), (1024, 5120), (17408, 5120), (5120, 17408))
 METRIC = "QMV GB/s & % HBM peak (M=1); QMM TFLOPS & % MFMA peak (M=512); per type"
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qmv_traffic.json")
 ROOF_REPS, ROOF_REPEATS = 128, 5  # roofline kernel timing: 5 loops of 128 back-to-back launches
+CASE_REPS, CASE_REPEATS = 32, 3    # per-product timing: 3 loops of 32 back-to-back launches
+ROOF_CASE = ("Q6_K", 17408, 5120)  # the step's longest launch, whose rocprofv3 summary is committed
 
 
 def log(*a):
@@ -198,23 +201,16 @@ def run_qmv(steps, warmup, device):
         for c in qc.cases:
             qc.launch(c, sh)
     torch.cuda.synchronize()
-    # eager pass with an event pair around every launch: per-launch kernel time
-    nc = len(qc.cases)
-    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(nc)]
-           for _ in range(steps)]
+    # eager pass: one launch call per product, back to back
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     t0.record(stream)
     for s in range(steps):
-        for i, c in enumerate(qc.cases):
-            evs[s][i][0].record(stream)
+        for c in qc.cases:
             qc.launch(c, sh)
-            evs[s][i][1].record(stream)
     t1.record(stream)
     torch.cuda.synchronize()
     eager_ms = t0.elapsed_time(t1) / steps
-    per_launch = [statistics.median(evs[s][i][0].elapsed_time(evs[s][i][1]) for s in range(steps)) * 1e3
-                  for i in range(nc)]
     # graph: one step captured once, replayed `steps` times
     graph = torch.cuda.CUDAGraph()
     cap = torch.cuda.Stream(device)
@@ -235,6 +231,8 @@ def run_qmv(steps, warmup, device):
     g1.record(stream)
     torch.cuda.synchronize()
     graph_ms = g0.elapsed_time(g1) / steps
+    # per-product kernel time: loops of back-to-back launches of that product alone
+    per_launch = [case_loop(c[0], c[2], c[3], CASE_REPS, device, repeats=CASE_REPEATS) for c in qc.cases]
     return qc, per_launch, eager_ms, graph_ms
 
 
@@ -595,12 +593,13 @@ def main():
         us = sum(per_launch[i] for i in idx)
         gbs = b / (us * 1e-6) / 1e9
         per_type[q] = {"GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
-    # the roofline kernel: the longest launch of the sweep, timed on its own as 5 loops of 128
-    # back-to-back launches, median loop (the loop of --profile-case, which the committed kernel
-    # trace runs)
-    dom = max(range(len(qc.cases)), key=lambda i: per_launch[i])
-    dq, _, dn, dk = qc.cases[dom][:4]
+    # the roofline kernel: Q6_K 17408x5120, the longest launch of the step (checked below), timed
+    # on its own as 5 loops of 128 back-to-back launches, median loop (the loop of
+    # --profile-case, which the committed kernel trace runs)
+    dq, dn, dk = ROOF_CASE
     dom_case = f"{dq} {dn}x{dk}"
+    longest = max(range(len(qc.cases)), key=lambda i: per_launch[i])
+    longest_case = f"{qc.cases[longest][0]} {qc.cases[longest][2]}x{qc.cases[longest][3]}"
     dom_bytes = qmv_bytes(dq, dn, dk)
     dom_us = case_loop(dq, dn, dk, ROOF_REPS, device, repeats=ROOF_REPEATS)
     achieved = dom_bytes / (dom_us * 1e-6) / 1e9
@@ -615,7 +614,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(dom_case),
                      "kernel": f"qmv_kernel<{dq}> M=1", "case": dom_case, "bytes_per_launch": int(dom_bytes),
-                     "us_per_launch": round(dom_us, 3), "timing": f"median of {ROOF_REPEATS} loops of HIP events "
+                     "us_per_launch": round(dom_us, 3), "longest_launch_of_step": longest_case,
+                     "timing": f"median of {ROOF_REPEATS} loops of HIP events "
                      f"around {ROOF_REPS} back-to-back launches (8 rotating weight copies) on the launch stream"},
         "eager_ms_per_step": round(eager_ms, 4),
         "kernel_time_GBs": round(step_bytes / kernel_time / 1e9, 1),

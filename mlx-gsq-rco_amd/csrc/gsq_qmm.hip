@@ -1,10 +1,25 @@
 // QMM dispatch by type; the kernels are in gsq_qmm_impl.h, instantiated per type in
 // gsq_qmm_<type>.hip.
+#include <cstdio>
+#include <cstdlib>
+
 #include "gsq_common.h"
 
 namespace gsq {
 
-QmmTuning g_qmm_tuning = {0, 0, 0, 0, 0, 0, 0};
+// GSQ_QMM_TUNING="mf,min_cols,waves,small_max_m,small_waves,small_nb,small_min_cols" (a
+// prefix may be given; 0 keeps a field's default) overrides the launch plans, read once at
+// library load, for measuring plans without a rebuild.
+static QmmTuning qmm_tuning_from_env() {
+  QmmTuning t = {0, 0, 0, 0, 0, 0, 0};
+  if (const char* s = std::getenv("GSQ_QMM_TUNING")) {
+    int v[7] = {0, 0, 0, 0, 0, 0, 0};
+    std::sscanf(s, "%d,%d,%d,%d,%d,%d,%d", &v[0], &v[1], &v[2], &v[3], &v[4], &v[5], &v[6]);
+    t = {v[0], v[1], v[2], v[3], v[4], v[5], v[6]};
+  }
+  return t;
+}
+QmmTuning g_qmm_tuning = qmm_tuning_from_env();
 
 hipError_t launch_qmm_q2_k(const uint8_t* packed, const void* x, int xdt, void* y, int ydt, int64_t M,
     int64_t N, int K, const DevTables& tb, int num_cus, const QmmWorkspace& ws, hipStream_t s);

@@ -22,6 +22,7 @@ Printed JSON line (one, on stdout):
   layer_crossover  configs[3]: QMV vs QMM time per projection of the mixed layer, M in 1..16
   decode_stack  configs[4]: 448 GEMVs (64 layers, 8.34 GB) in one HIP graph: GB/s, tokens/s
   decode_stack_fused  the same products with q|k and gate|up fused (320 launches)
+  decode_stack_grouped  the same through GSQGroupedLinear / GSQLinear modules (fp16 outputs)
   cpu_baseline  the numpy oracle (dequant + float32 matmul) on the configs[1] products, all host threads
 
 Algorithmic bytes per QMV launch = N*(K/256)*block_bytes + M*K*2 (x fp16) + M*N*4 (y fp32).
@@ -452,6 +453,74 @@ def run_stack(device, layers=64, reps=10, fused=False):
     return res
 
 
+def run_stack_grouped(device, layers=64, reps=10):
+    """configs[4] through the modules a model uses: per layer GSQGroupedLinear(q, k, v) (q|k one
+    IQ2_XS launch, then v IQ4_XS), GSQLinear(o), GSQGroupedLinear(gate, up) (one IQ2_S launch)
+    and GSQLinear(down), at M=1 with fp16 outputs, the 64 layers captured in one HIP graph and
+    replayed."""
+    import torch
+    from mlx_gsq_amd import _lib
+    from mlx_gsq_amd.formats import BLOCK_BYTES, TYPE_IDS
+    from mlx_gsq_amd.nn import GSQGroupedLinear, GSQLinear
+    from mlx_gsq_amd.runtime.store import PackedWeight
+    total, n_mats = 0, [0]
+
+    def weight(q, n, k):
+        nonlocal total
+        data = make_device_packed(q, n, k, seed=7000 + n_mats[0], device=device)
+        n_mats[0] += 1
+        total += qmv_bytes(q, n, k)
+        return PackedWeight(name=f"m{n_mats[0]}", data=data, gguf_shape=(k, n), logical_shape=(n, k),
+                            quantization_type=q, quantization_type_id=TYPE_IDS[q], num_elements=n * k,
+                            num_bytes=n * (k // 256) * BLOCK_BYTES[q])
+    spec = {name: (q, n, k) for (name, q, n, k) in LAYER}
+    for q in {q for (_, q, _, _) in LAYER}:
+        _lib.ensure_tables(q, device)
+    mods = []
+    for _ in range(layers):
+        w = {name: weight(*spec[name]) for name in spec}
+        mods.append((GSQGroupedLinear([w["q"], w["k"], w["v"]]), GSQLinear(w["o"]),
+                     GSQGroupedLinear([w["gate"], w["up"]]), GSQLinear(w["down"])))
+    x5 = torch.randn(1, 5120, device=device).half()
+    x17 = torch.randn(1, 17408, device=device).half()
+
+    def step():
+        for qkv, o, gu, down in mods:
+            qkv(x5)
+            o(x5)
+            gu(x5)
+            down(x17)
+
+    step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream(device)
+    cap.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(cap):
+        step()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=cap):
+            step()
+    stream = torch.cuda.current_stream(device)
+    stream.wait_stream(cap)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    gbs = total / (ms * 1e-3) / 1e9
+    res = {"gemvs": 7 * layers, "launches": 5 * layers, "bytes": int(total), "ms_per_token": round(ms, 4),
+           "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "linear_tokens_per_s": round(1e3 / ms, 1),
+           "mix": "as decode_stack; GSQGroupedLinear(q,k,v) and (gate,up), fp16 outputs"}
+    del mods, graph
+    torch.cuda.empty_cache()
+    return res
+
+
 def qmm_profile_case(spec, reps, device):
     """Launch one QMM product TYPE:MxNxK `reps` times (for rocprofv3 runs)."""
     import torch
@@ -579,6 +648,7 @@ def main():
     crossover = {} if args.no_layer else run_crossover(device)
     stack = {} if args.no_layer else run_stack(device)
     stack_fused = {} if args.no_layer else run_stack(device, fused=True)
+    stack_grouped = {} if args.no_layer else run_stack_grouped(device)
     emb = {} if args.no_layer else run_embedding(device)
     from mlx_gsq_amd.formats import QTYPES
     step_bytes = qc.step_bytes()
@@ -626,6 +696,7 @@ def main():
         "layer_crossover": crossover,
         "decode_stack": stack,
         "decode_stack_fused": stack_fused,
+        "decode_stack_grouped": stack_grouped,
         "embedding": emb,
         "cpu_baseline": cpu,
     }

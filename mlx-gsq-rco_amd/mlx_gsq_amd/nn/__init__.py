@@ -1,5 +1,5 @@
 """Packed-weight modules."""
 from .embedding import GSQEmbedding
-from .linear import GSQFusedLinear, GSQLinear
+from .linear import GSQFusedLinear, GSQGroupedLinear, GSQLinear
 
-__all__ = ["GSQEmbedding", "GSQFusedLinear", "GSQLinear"]
+__all__ = ["GSQEmbedding", "GSQFusedLinear", "GSQGroupedLinear", "GSQLinear"]

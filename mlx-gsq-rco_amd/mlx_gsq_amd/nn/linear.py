@@ -83,3 +83,48 @@ class GSQFusedLinear(torch.nn.Module):
     def extra_repr(self) -> str:
         return f"in_features={self.in_features}, splits={self.splits}, qtype={self.qtype}"
 
+
+class GSQGroupedLinear(torch.nn.Module):
+    """Projections of one input whose weights differ in quantization type (q/k/v of a decoder
+    layer: IQ2_XS, IQ2_XS, IQ4_XS), applied as one group: the weights of each type are fused
+    into one launch (``GSQFusedLinear``), so a group costs one launch per type. ``forward``
+    returns one output per weight, in the order given; each is the one ``GSQFusedLinear`` gives
+    for its type's weights. The launches stay on the current stream: as parallel branches of a
+    captured HIP graph (side streams forked from and joined into the current stream) the
+    64-layer decode stack ran 16% slower than with the launches in sequence (4.91 against 4.24
+    ms per token). No counterpart in the reference, whose model applies each projection on its
+    own.
+    """
+
+    def __init__(self, weights, biases=None):
+        super().__init__()
+        weights = list(weights)
+        if not weights:
+            raise ValueError("no weights to group")
+        widths = {w.logical_shape[1] for w in weights}
+        if len(widths) != 1:
+            raise ValueError(f"grouped weights must share one input width, got {sorted(widths)}")
+        if biases is not None and len(biases) != len(weights):
+            raise ValueError("one bias (or None) per weight")
+        self.in_features = weights[0].logical_shape[1]
+        order = []  # quantization types in order of first appearance
+        for w in weights:
+            if w.quantization_type not in order:
+                order.append(w.quantization_type)
+        # parts[i] computes the weights slots[i] (indices into the given order)
+        self.slots = [[j for j, w in enumerate(weights) if w.quantization_type == q] for q in order]
+        self.parts = torch.nn.ModuleList(
+            GSQFusedLinear([weights[j] for j in slot],
+                           None if biases is None else [biases[j] for j in slot]) for slot in self.slots)
+        self.out_features = [w.logical_shape[0] for w in weights]
+
+    def forward(self, x):
+        outs = [None] * len(self.out_features)
+        for slot, part in zip(self.slots, self.parts):
+            for j, r in zip(slot, part(x)):
+                outs[j] = r
+        return tuple(outs)
+
+    def extra_repr(self) -> str:
+        return f"in_features={self.in_features}, out_features={self.out_features}, " \
+               f"qtypes={[p.qtype for p in self.parts]}"

@@ -167,3 +167,25 @@ def test_fused_linear_concatenates_rows_and_validates():
     with pytest.raises(ValueError):
         GSQFusedLinear([])
 
+
+def test_grouped_linear_groups_by_type_and_validates():
+    import torch
+    from mlx_gsq_amd import synth
+    from mlx_gsq_amd.nn import GSQGroupedLinear
+    from mlx_gsq_amd.runtime.store import PackedWeight
+
+    def pw(q, n, k, seed, qid, bb):
+        data = torch.from_numpy(synth.make_packed(q, n, k, seed=seed))
+        return PackedWeight(name=f"w{seed}", data=data, gguf_shape=(k, n), logical_shape=(n, k),
+                            quantization_type=q, quantization_type_id=qid, num_elements=n * k,
+                            num_bytes=n * (k // 256) * bb)
+    q, k, v = pw("IQ2_XS", 64, 512, 1, 17, 74), pw("IQ2_XS", 16, 512, 2, 17, 74), pw("IQ4_XS", 16, 512, 3, 23, 136)
+    g = GSQGroupedLinear([q, v, k])
+    assert g.slots == [[0, 2], [1]] and g.out_features == [64, 16, 16]
+    assert [p.qtype for p in g.parts] == ["IQ2_XS", "IQ4_XS"]
+    assert torch.equal(g.parts[0].packed_weight, torch.cat([q.data, k.data]))
+    with pytest.raises(ValueError):
+        GSQGroupedLinear([q, pw("IQ2_XS", 16, 1024, 4, 17, 74)])
+    with pytest.raises(ValueError):
+        GSQGroupedLinear([])
+

@@ -364,6 +364,50 @@ def test_fused_linear_matches_separate_projections(rows):
         assert rel_l2(o.cpu().numpy(), want) <= 1e-3
 
 
+@pytest.mark.parametrize("rows", [1, 3])
+def test_grouped_linear_mixed_types(rows):
+    """q/k/v with mixed types (IQ2_XS, IQ2_XS, IQ4_XS) as one group: every output equals the
+    per-type fused launch bit for bit (same kernels and plans) and the oracle within tolerance,
+    eagerly and on every replay of a captured graph."""
+    from mlx_gsq_amd.nn import GSQFusedLinear, GSQGroupedLinear
+    from mlx_gsq_amd.runtime.store import PackedWeight
+    K = 1024
+    spec = [("IQ2_XS", 17, 512, 21), ("IQ2_XS", 17, 128, 22), ("IQ4_XS", 23, 128, 23)]
+    ws, packs = [], []
+    for i, (q, qid, n, seed) in enumerate(spec):
+        p = synth.make_packed(q, n, K, seed=seed)
+        packs.append(p)
+        ws.append(PackedWeight(name=f"w{i}", data=dev(p), gguf_shape=(K, n), logical_shape=(n, K),
+                               quantization_type=q, quantization_type_id=qid, num_elements=n * K,
+                               num_bytes=p.size))
+    group = GSQGroupedLinear(ws)
+    qk = GSQFusedLinear(ws[:2])
+    vv = GSQFusedLinear(ws[2:])
+    x = dev(synth.make_x(rows, K, seed=8, dtype=np.float16))
+    outs = group(x)
+    want = list(qk(x)) + list(vv(x))
+    for o, w_, p, (q, _, n, _) in zip(outs, want, packs, spec):
+        assert torch.equal(o, w_)
+        ref = O.matmul_reference(x.float().cpu().numpy(), p, q, n, K, TABLES.get(q))
+        assert rel_l2(o.float().cpu().numpy(), ref) <= 1e-2
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        group(x)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=cap):
+            gout = group(x)
+    torch.cuda.current_stream().wait_stream(cap)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for o, w_ in zip(gout, want):
+            assert torch.equal(o, w_)
+        group(x)  # eager work between replays
+        torch.cuda.synchronize()
+
+
 def test_deterministic_repeat():
     from mlx_gsq_amd.runtime.kernels.qmv import quantized_matvec
     N, K = 2048, 5120

@@ -167,11 +167,11 @@ struct QmmDec<IQ4_XS, A4> {
 };
 
 // IQ3_S (iq3_s_decode.py:16-40): w = +-d*(1+2*s)*grid[gi][c], 9-bit grid index; sign masks
-// per nibble (two words) at the end of the table image
+// per nibble (two words) after the codebook
 template <bool A4>
 struct QmmDec<IQ3_S, A4> {
   static constexpr uint32_t kGridB = 512 * 4 * 2;
-  static constexpr uint32_t kMaskB = kGridB + 256 * 16;  // after the QMV kernel's byte masks
+  static constexpr uint32_t kMaskB = kGridB;
   __device__ __forceinline__ static void run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
     const float d = h2f(lds_u16(sb, sd + 0));
     const uint32_t sbyte = lds_u8(sb, sd + 106 + (g >> 1));
@@ -251,7 +251,7 @@ struct QmmDec<IQ2_XS, A4> {
   }
 };
 
-// IQ2_S (iq_lookup_decode.py:18-22): sign byte masks after the codebook
+// IQ2_S (iq_lookup_decode.py:18-22): sign masks per nibble (two words) after the codebook
 template <bool A4>
 struct QmmDec<IQ2_S, A4> {
   static constexpr uint32_t kGridB = 1024 * 8 * 2;
@@ -261,7 +261,14 @@ struct QmmDec<IQ2_S, A4> {
     const uint32_t qi = lds_u8(sb, sd + 2 + oo) | (hi << 8);
     const uint32_t sc = (lds_u8(sb, sd + 74 + g) >> (4 * (kq >> 1))) & 15u;
     const float d = h2f(lds_u16(sb, sd + 0)) * (0.5f + (float)sc) * 0.25f;
-    grid8<true>(tbl, qi, d, 0.f, tbl_words(tbl, kGridB + lds_u8(sb, sd + 34 + oo) * 16), o);
+    const uint32_t sg = lds_u8(sb, sd + 34 + oo);
+    const uint32_t* e = tbl_words(tbl, qi * 16);
+    const uint32_t* m0 = tbl_words(tbl, kGridB + (sg & 15u) * 8);
+    const uint32_t* m1 = tbl_words(tbl, kGridB + (sg >> 4) * 8);
+    const uint32_t ev[4] = {e[0], e[1], e[2], e[3]};
+    const uint32_t mv[4] = {m0[0], m0[1], m1[0], m1[1]};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = mix2(d, ev[i], 0.f) ^ mv[i];
   }
 };
 

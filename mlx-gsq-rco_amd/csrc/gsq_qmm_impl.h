@@ -77,9 +77,9 @@ constexpr int qmm_tbl_bytes() {
   return T == IQ1_S || T == IQ1_M ? 2048 * 8 * 2
        : T == IQ2_XXS            ? 256 * 8 * 2 + 128 * 16
        : T == IQ2_XS             ? 512 * 8 * 2 + 128 * 16
-       : T == IQ2_S              ? 1024 * 8 * 2 + 256 * 16
+       : T == IQ2_S              ? 1024 * 8 * 2 + 16 * 8
        : T == IQ3_XXS            ? 256 * 4 * 2 + 128 * 16
-       : T == IQ3_S              ? 512 * 4 * 2 + 256 * 16 + 16 * 8
+       : T == IQ3_S              ? 512 * 4 * 2 + 16 * 8
                                  : 0;
 }
 

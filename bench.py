@@ -23,6 +23,8 @@ Printed JSON line (one, on stdout):
   decode_stack  configs[4]: 448 GEMVs (64 layers, 8.34 GB) in one HIP graph: GB/s, tokens/s
   decode_stack_fused  the same products with q|k and gate|up fused (320 launches)
   decode_stack_grouped  the same through GSQGroupedLinear / GSQLinear modules (fp16 outputs)
+  model_decode  single-token decode of the whole 27B Qwen3.5-hybrid model (norms, GatedDeltaNet,
+                attention, MLP, lm_head) as one HIP graph per step: model tokens/s
   cpu_baseline  the numpy oracle (dequant + float32 matmul) on the configs[1] products, all host threads
 
 Algorithmic bytes per QMV launch = N*(K/256)*block_bytes + M*K*2 (x fp16) + M*N*4 (y fp32).
@@ -521,6 +523,117 @@ def run_stack_grouped(device, layers=64, reps=10):
     return res
 
 
+# packed type of each projection of the synthetic 27B checkpoint (the configs[4] mix extended to
+# the GatedDeltaNet projections, the embedding and the output head)
+MODEL_TYPES = {"attn_qkv": "IQ2_XS", "attn_gate": "IQ2_XS", "ssm_out": "IQ3_S", "attn_q": "IQ2_XS",
+               "attn_k": "IQ2_XS", "attn_v": "IQ4_XS", "attn_output": "IQ3_S", "ffn_gate": "IQ2_S",
+               "ffn_up": "IQ2_S", "ffn_down": "Q4_K", "output": "Q6_K", "token_embd": "IQ2_S"}
+
+
+class SyntheticQwen35Store:
+    """Random packed weights of the 27B Qwen3.5-hybrid shapes on the device, behind the store
+    interface build_qwen35 reads (weights are not meaningful; the step's work is)."""
+
+    def __init__(self, args, device):
+        import torch
+        from mlx_gsq_amd.formats import BLOCK_BYTES, TYPE_IDS
+        from mlx_gsq_amd.runtime.store import PackedWeight
+        self.device, self.weights, self.plains = device, {}, {}
+        self.packed_bytes = 0
+        a, H = args, args.hidden_size
+        g = torch.Generator(device=device)
+        g.manual_seed(11)
+
+        def packed(name, kind, n, k):
+            q = MODEL_TYPES[kind]
+            data = make_device_packed(q, n, k, seed=20000 + len(self.weights), device=device)
+            self.weights[name] = PackedWeight(name=name, data=data, gguf_shape=(k, n), logical_shape=(n, k),
+                                              quantization_type=q, quantization_type_id=TYPE_IDS[q],
+                                              num_elements=n * k, num_bytes=n * (k // 256) * BLOCK_BYTES[q])
+            self.packed_bytes += n * (k // 256) * BLOCK_BYTES[q]
+
+        def plain(name, *shape, fill=None):
+            t = torch.randn(*shape, device=device, generator=g) * 0.1
+            self.plains[name] = t + fill if fill is not None else t
+
+        packed("token_embd.weight", "token_embd", a.vocab_size, H)
+        packed("output.weight", "output", a.vocab_size, H)
+        plain("output_norm.weight", H, fill=1.0)
+        for i in range(a.num_hidden_layers):
+            p = f"blk.{i}."
+            plain(p + "attn_norm.weight", H, fill=1.0)
+            plain(p + "post_attention_norm.weight", H, fill=1.0)
+            packed(p + "ffn_gate.weight", "ffn_gate", a.intermediate_size, H)
+            packed(p + "ffn_up.weight", "ffn_up", a.intermediate_size, H)
+            packed(p + "ffn_down.weight", "ffn_down", H, a.intermediate_size)
+            if a.is_linear(i):
+                packed(p + "attn_qkv.weight", "attn_qkv", a.conv_dim, H)
+                packed(p + "attn_gate.weight", "attn_gate", a.value_dim, H)
+                packed(p + "ssm_out.weight", "ssm_out", H, a.value_dim)
+                plain(p + "ssm_alpha.weight", a.linear_num_value_heads, H)
+                plain(p + "ssm_beta.weight", a.linear_num_value_heads, H)
+                plain(p + "ssm_conv1d.weight", a.conv_dim, a.linear_conv_kernel_dim)
+                plain(p + "ssm_a", a.linear_num_value_heads, fill=-1.0)
+                plain(p + "ssm_dt.bias", a.linear_num_value_heads)
+                plain(p + "ssm_norm.weight", a.linear_value_head_dim, fill=1.0)
+            else:
+                packed(p + "attn_q.weight", "attn_q", a.num_attention_heads * a.head_dim * 2, H)
+                packed(p + "attn_k.weight", "attn_k", a.num_key_value_heads * a.head_dim, H)
+                packed(p + "attn_v.weight", "attn_v", a.num_key_value_heads * a.head_dim, H)
+                packed(p + "attn_output.weight", "attn_output", H, a.num_attention_heads * a.head_dim)
+                plain(p + "attn_q_norm.weight", a.head_dim, fill=1.0)
+                plain(p + "attn_k_norm.weight", a.head_dim, fill=1.0)
+
+    def weight(self, name):
+        return self.weights[name]
+
+    def materialize_plain(self, name):
+        return self.plains[name]
+
+
+def run_model_decode(device, max_len=1024, prompt=8, steps=32):
+    """§8(f) rank 4: single-token decode steps of the 27B Qwen3.5-hybrid model (64 layers, random
+    packed weights in the MODEL_TYPES mix, fp16 activations) as one HIP graph per step
+    (GraphDecoder), after an eager prefill of `prompt` tokens; model tokens/s, and the packed
+    bytes read per token over the step time."""
+    import torch
+    from mlx_gsq_amd import _lib
+    from mlx_gsq_amd.models import GraphDecoder, Qwen35Args, build_qwen35
+    args = Qwen35Args()
+    for q in set(MODEL_TYPES.values()):
+        _lib.ensure_tables(q, device)
+    store = SyntheticQwen35Store(args, device)
+    model = build_qwen35(store, dtype=torch.float16, args=args)
+    # bytes one token reads: every packed matrix except the embedding table (one row of it)
+    emb = store.weights["token_embd.weight"]
+    per_token = store.packed_bytes - emb.num_bytes + emb.num_bytes // args.vocab_size
+    cache = model.new_cache(batch=1, max_len=max_len, device=device)
+    ids = torch.randint(0, args.vocab_size, (1, prompt + steps + 1), device=device)
+    with torch.no_grad():
+        model(ids[:, :prompt], cache)
+        dec = GraphDecoder(model, cache)
+        dec.step(ids[:, prompt:prompt + 1])
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream(device)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(steps):
+            dec.step(ids[:, prompt + 1 + i:prompt + 2 + i])
+        e1.record(stream)
+        torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    res = {"model": "Qwen3.5-hybrid 27B shapes (64 layers: 48 GatedDeltaNet, 16 attention), synthetic weights",
+           "ms_per_token": round(ms, 4), "tokens_per_s": round(1e3 / ms, 1),
+           "packed_bytes_per_token": int(per_token),
+           "packed_GB/s": round(per_token / (ms * 1e-3) / 1e9, 1),
+           "frac": round(per_token / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+           "context": f"prefill {prompt} tokens, then {steps} timed graph steps (KV buffer {max_len})",
+           "types": MODEL_TYPES}
+    del dec, model, store, cache
+    torch.cuda.empty_cache()
+    return res
+
+
 def qmm_profile_case(spec, reps, device):
     """Launch one QMM product TYPE:MxNxK `reps` times (for rocprofv3 runs)."""
     import torch
@@ -649,6 +762,7 @@ def main():
     stack = {} if args.no_layer else run_stack(device)
     stack_fused = {} if args.no_layer else run_stack(device, fused=True)
     stack_grouped = {} if args.no_layer else run_stack_grouped(device)
+    model_decode = {} if args.no_layer else run_model_decode(device)
     emb = {} if args.no_layer else run_embedding(device)
     from mlx_gsq_amd.formats import QTYPES
     step_bytes = qc.step_bytes()
@@ -697,6 +811,7 @@ def main():
         "decode_stack": stack,
         "decode_stack_fused": stack_fused,
         "decode_stack_grouped": stack_grouped,
+        "model_decode": model_decode,
         "embedding": emb,
         "cpu_baseline": cpu,
     }

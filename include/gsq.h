@@ -100,6 +100,55 @@ int gsq_qmm_noalloc(int qtype_id, const void* packed, const void* x, int x_dtype
 int gsq_embedding(int qtype_id, const void* packed, const void* ids, int ids_dtype, int64_t n_ids,
                   int64_t vocab, int64_t dims, void* out, int out_dtype, void* stream);
 
+/* ---- the decode step around the projections (Qwen3.5-hybrid) ----
+ * Element-wise work of one decoder step fused into single launches. The reference runs it as
+ * mlx / mlx-lm operations inside mlx_gsq/models/qwen35.py (RMSNorm, SwiGLU MLP, the patched
+ * GatedDeltaNet :48-111); no entry point of its own corresponds. Tensors are row-major in one
+ * dtype (GSQ_F32 / GSQ_F16 / GSQ_BF16), math in float32, results rounded once. */
+
+/* Per row of `dim` values (a multiple of 8, at most 8192; all pointers 16-byte aligned): if
+ * delta is not NULL, x = round(x + delta) (written back); then y = round(x / sqrt(mean(x^2) +
+ * eps) * w). Replaces the residual add and RMSNorm of a layer. */
+int gsq_add_rms_norm(void* x, const void* delta, const void* w, void* y, int64_t rows, int64_t dim, float eps,
+                     int dtype, void* stream);
+
+/* out[r, i] = round(silu(gu[r, i]) * gu[r, n + i]) for rows of 2n values (gate then up).
+ * Replaces the SwiGLU of the MLP. */
+int gsq_swiglu(const void* gate_up, void* out, int64_t rows, int64_t n, int dtype, void* stream);
+
+/* One GatedDeltaNet token for `batch` rows (replaces the conv / gated_delta_update / gated
+ * norm part of qwen35.py:58-108 for one token, and the in_proj_a / in_proj_b projections):
+ * per row, the depthwise causal convolution (kernel conv_kernel, state conv_state [batch,
+ * conv_kernel-1, conv_dim] shifted in place, weights conv_w [conv_dim, conv_kernel]) and SiLU
+ * of the new qkv row (conv_dim = 2 * key_heads * head_k_dim + value_heads * head_v_dim), into
+ * `work` (batch x conv_dim float32, scratch); q and k RMS-normalized per head (eps 1e-6) times
+ * head_k_dim^-1 and ^-1/2; value head h reads q/k head h % key_heads (GGUF order); a and b =
+ * x . w_ab rows h and value_heads + h (w_ab [2 value_heads, hidden]), rounded to the dtype;
+ * beta = sigmoid(b), decay = exp(ssm_a * softplus(a + dt_bias)); the float32 state rec_state
+ * [batch, value_heads, head_k_dim, head_v_dim] updated in place (S = decay S; S += k (beta (v -
+ * S^T k))^T) and o = S^T q; out = round(o / rms(o) * norm_w * silu(z)) with eps over each
+ * head's head_v_dim values. Strides are in elements between batch rows. head_k_dim a multiple
+ * of 4 up to 128, head_v_dim 64..256 in steps of 64, conv_kernel 2..8. */
+int gsq_gdn_step(const void* qkv, int64_t qkv_stride, const void* z, int64_t z_stride, const void* x,
+                 int64_t x_stride, const void* w_ab, int64_t hidden, void* conv_state, const void* conv_w,
+                 const float* ssm_a, const float* dt_bias, float* rec_state, const void* norm_w, void* out,
+                 int64_t out_stride, float* work, int64_t batch, int64_t key_heads, int64_t value_heads,
+                 int64_t head_k_dim, int64_t head_v_dim, int64_t conv_kernel, float eps, int dtype, void* stream);
+
+/* One new token of gated grouped-query attention for `batch` rows (replaces the attention of a
+ * full-attention layer at decode, qwen35.py's mlx-lm attention): per query head h (kv head
+ * h / (heads / kv_heads)), q = round(rms_norm(q) * q_norm_w) from the q half of qg's head
+ * block [q | gate] and k likewise from k with k_norm_w (eps), both rotated on their first
+ * rotary_dim dims (rotate-half, angle pos * inv_freq[i]) and rounded; k and v written at *pos
+ * into k_cache / v_cache [batch, kv_heads, max_len, head_dim]; softmax over positions 0..*pos of
+ * q . K / sqrt(head_dim); out = round(sum p V * sigmoid(gate)). *pos is read on the device
+ * (< max_len, at most 32768). head_dim a multiple of 4 up to 256. Strides in elements. */
+int gsq_attn_decode(const void* qg, int64_t qg_stride, const void* k, int64_t k_stride, const void* v,
+                    int64_t v_stride, const void* q_norm_w, const void* k_norm_w, const double* inv_freq,
+                    void* k_cache, void* v_cache, const int64_t* pos, void* out, int64_t out_stride, int64_t batch,
+                    int64_t heads, int64_t kv_heads, int64_t head_dim, int64_t rotary_dim, int64_t max_len,
+                    float eps, int dtype, void* stream);
+
 /* Message of the last failed call on this thread ("" if none). */
 const char* gsq_last_error(void);
 

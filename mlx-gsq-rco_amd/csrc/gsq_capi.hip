@@ -21,6 +21,11 @@ hipError_t launch_qmm(int qt, const uint8_t* packed, const void* x, int xdt, voi
                       int K, const DevTables& tb, int num_cus, const QmmWorkspace& ws, hipStream_t s);
 hipError_t launch_embedding(int qt, const uint8_t* packed, const void* ids, int ids64, int64_t n_ids, int64_t vocab,
                             int64_t dims, void* out, int odt, const DevTables& t, hipStream_t s);
+hipError_t launch_add_rms_norm(int dt, void* x, const void* delta, const void* w, void* y, int64_t rows, int dim,
+                               float eps, hipStream_t s);
+hipError_t launch_swiglu(int dt, const void* gu, void* out, int64_t rows, int n, hipStream_t s);
+hipError_t launch_gdn_step(int dt, const GdnArgs& a, hipStream_t s);
+hipError_t launch_attn_decode(int dt, const AttnArgs& a, hipStream_t s);
 int qmv_table_bytes(int qt);
 bool build_qmv_table(int qt, const uint16_t* grid16, const uint8_t* ksigns, std::vector<uint8_t>& out);
 }  // namespace gsq
@@ -405,6 +410,87 @@ int gsq_embedding(int qt, const void* packed, const void* ids, int ids_dtype, in
   hipError_t e = launch_embedding(qt, static_cast<const uint8_t*>(packed), ids, ids_dtype == GSQ_IDS_I64, n_ids, vocab,
                                   dims, out, out_dtype, tb, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(GSQ_E_HIP, "embedding launch: %s", hipGetErrorString(e));
+  return GSQ_OK;
+}
+
+int gsq_add_rms_norm(void* x, const void* delta, const void* w, void* y, int64_t rows, int64_t dim, float eps,
+                     int dtype, void* stream) {
+  if (dtype != GSQ_F32 && dtype != GSQ_F16 && dtype != GSQ_BF16) return fail(GSQ_E_TYPE, "unsupported dtype code %d", dtype);
+  if (rows < 0 || dim <= 0 || rows >= (1ll << 31)) return fail(GSQ_E_VALUE, "invalid shape");
+  if (rows == 0) return GSQ_OK;
+  if (!x || !w || !y) return fail(GSQ_E_VALUE, "NULL pointer");
+  if (!(eps >= 0.f)) return fail(GSQ_E_VALUE, "eps must be >= 0");
+  if (dim % 8 || dim > 8192) return fail(GSQ_E_VALUE, "row length must be a multiple of 8 up to 8192");
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(delta) | reinterpret_cast<uintptr_t>(w) |
+       reinterpret_cast<uintptr_t>(y)) & 15)
+    return fail(GSQ_E_VALUE, "x, delta, w and y must be 16-byte aligned");
+  hipError_t e = launch_add_rms_norm(dtype, x, delta, w, y, rows, (int)dim, eps, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(GSQ_E_HIP, "add_rms_norm launch: %s", hipGetErrorString(e));
+  return GSQ_OK;
+}
+
+int gsq_swiglu(const void* gate_up, void* out, int64_t rows, int64_t n, int dtype, void* stream) {
+  if (dtype != GSQ_F32 && dtype != GSQ_F16 && dtype != GSQ_BF16) return fail(GSQ_E_TYPE, "unsupported dtype code %d", dtype);
+  if (rows < 0 || n <= 0 || n >= (1ll << 30)) return fail(GSQ_E_VALUE, "invalid shape");
+  if (rows == 0) return GSQ_OK;
+  if (!gate_up || !out) return fail(GSQ_E_VALUE, "NULL pointer");
+  hipError_t e = launch_swiglu(dtype, gate_up, out, rows, (int)n, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(GSQ_E_HIP, "swiglu launch: %s", hipGetErrorString(e));
+  return GSQ_OK;
+}
+
+int gsq_gdn_step(const void* qkv, int64_t qkv_stride, const void* z, int64_t z_stride, const void* x,
+                 int64_t x_stride, const void* w_ab, int64_t hidden, void* conv_state, const void* conv_w,
+                 const float* ssm_a, const float* dt_bias, float* rec_state, const void* norm_w, void* out,
+                 int64_t out_stride, float* work, int64_t batch, int64_t key_heads, int64_t value_heads,
+                 int64_t head_k_dim, int64_t head_v_dim, int64_t conv_kernel, float eps, int dtype, void* stream) {
+  if (dtype != GSQ_F32 && dtype != GSQ_F16 && dtype != GSQ_BF16) return fail(GSQ_E_TYPE, "unsupported dtype code %d", dtype);
+  if (batch < 0 || batch > 65535) return fail(GSQ_E_VALUE, "batch must be 0..65535");
+  if (batch == 0) return GSQ_OK;
+  if (key_heads <= 0 || value_heads <= 0 || value_heads % key_heads || value_heads > 65535)
+    return fail(GSQ_E_VALUE, "value heads must be a positive multiple of key heads (at most 65535)");
+  if (head_k_dim <= 0 || head_k_dim > 128 || head_k_dim % 4) return fail(GSQ_E_VALUE, "key head dim must be a multiple of 4 up to 128");
+  if (head_v_dim <= 0 || head_v_dim % 64 || head_v_dim > 256) return fail(GSQ_E_VALUE, "value head dim must be 64, 128, 192 or 256");
+  if (conv_kernel < 2 || conv_kernel > 8) return fail(GSQ_E_VALUE, "convolution kernel must be 2..8");
+  if (hidden <= 0 || hidden >= (1ll << 30)) return fail(GSQ_E_VALUE, "invalid hidden size");
+  if (!qkv || !z || !x || !w_ab || !conv_state || !conv_w || !ssm_a || !dt_bias || !rec_state || !norm_w || !out || !work)
+    return fail(GSQ_E_VALUE, "NULL pointer");
+  if (!(eps >= 0.f)) return fail(GSQ_E_VALUE, "eps must be >= 0");
+  GdnArgs a;
+  a.qkv = qkv; a.z = z; a.x = x; a.w_ab = w_ab; a.conv = conv_state; a.conv_w = conv_w; a.ssm_a = ssm_a;
+  a.dt_bias = dt_bias; a.rec = rec_state; a.norm_w = norm_w; a.out = out; a.work = work;
+  a.qkv_stride = qkv_stride; a.z_stride = z_stride; a.x_stride = x_stride; a.out_stride = out_stride;
+  a.B = (int)batch; a.Hk = (int)key_heads; a.Hv = (int)value_heads; a.dk = (int)head_k_dim; a.dv = (int)head_v_dim;
+  a.K = (int)conv_kernel; a.hidden = (int)hidden; a.eps = eps;
+  hipError_t e = launch_gdn_step(dtype, a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(GSQ_E_HIP, "gdn_step launch: %s", hipGetErrorString(e));
+  return GSQ_OK;
+}
+
+int gsq_attn_decode(const void* qg, int64_t qg_stride, const void* k, int64_t k_stride, const void* v,
+                    int64_t v_stride, const void* q_norm_w, const void* k_norm_w, const double* inv_freq,
+                    void* k_cache, void* v_cache, const int64_t* pos, void* out, int64_t out_stride, int64_t batch,
+                    int64_t heads, int64_t kv_heads, int64_t head_dim, int64_t rotary_dim, int64_t max_len,
+                    float eps, int dtype, void* stream) {
+  if (dtype != GSQ_F32 && dtype != GSQ_F16 && dtype != GSQ_BF16) return fail(GSQ_E_TYPE, "unsupported dtype code %d", dtype);
+  if (batch < 0 || batch > 65535) return fail(GSQ_E_VALUE, "batch must be 0..65535");
+  if (batch == 0) return GSQ_OK;
+  if (kv_heads <= 0 || heads <= 0 || heads % kv_heads || heads > 65535)
+    return fail(GSQ_E_VALUE, "heads must be a positive multiple of kv heads (at most 65535)");
+  if (head_dim <= 0 || head_dim > 256 || head_dim % 4) return fail(GSQ_E_VALUE, "head dim must be a multiple of 4 up to 256");
+  if (rotary_dim < 0 || rotary_dim > head_dim || rotary_dim % 2) return fail(GSQ_E_VALUE, "invalid rotary dim");
+  if (max_len <= 0 || max_len > 32768) return fail(GSQ_E_VALUE, "cache length must be 1..32768");
+  if (!qg || !k || !v || !q_norm_w || !k_norm_w || (!inv_freq && rotary_dim) || !k_cache || !v_cache || !pos || !out)
+    return fail(GSQ_E_VALUE, "NULL pointer");
+  if (!(eps >= 0.f)) return fail(GSQ_E_VALUE, "eps must be >= 0");
+  AttnArgs a;
+  a.qg = qg; a.k = k; a.v = v; a.q_norm_w = q_norm_w; a.k_norm_w = k_norm_w; a.inv_freq = inv_freq;
+  a.kc = k_cache; a.vc = v_cache; a.pos = pos; a.out = out;
+  a.qg_stride = qg_stride; a.k_stride = k_stride; a.v_stride = v_stride; a.out_stride = out_stride;
+  a.B = (int)batch; a.H = (int)heads; a.Hkv = (int)kv_heads; a.hd = (int)head_dim; a.rd = (int)rotary_dim;
+  a.L = (int)max_len; a.eps = eps;
+  hipError_t e = launch_attn_decode(dtype, a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(GSQ_E_HIP, "attn_decode launch: %s", hipGetErrorString(e));
   return GSQ_OK;
 }
 

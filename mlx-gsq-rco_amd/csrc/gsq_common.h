@@ -90,6 +90,42 @@ struct QmmTuning {
   int small_min_cols;
 };
 
+// Arguments of one GatedDeltaNet token step (gsq_gdn_step; kernels in gsq_model.hip).
+struct GdnArgs {
+  const void* qkv;  // [B] rows of conv_dim (row stride qkv_stride elements)
+  const void* z;    // [B] rows of Hv*dv (row stride z_stride)
+  const void* x;    // [B] rows of the layer input, hidden values (row stride x_stride)
+  const void* w_ab; // [2 Hv, hidden]: the a rows, then the b rows
+  void* conv;       // [B, K-1, conv_dim] convolution state (activation dtype)
+  const void* conv_w;  // [conv_dim, K]
+  const float* ssm_a;  // [Hv] = -exp(A_log)
+  const float* dt_bias;  // [Hv]
+  float* rec;          // [B, Hv, dk, dv] recurrent state
+  const void* norm_w;  // [dv]
+  void* out;           // [B] rows of Hv*dv (row stride out_stride)
+  float* work;         // [B, conv_dim] convolution outputs (after SiLU)
+  int64_t qkv_stride, z_stride, x_stride, out_stride;
+  int B, Hk, Hv, dk, dv, K, hidden;
+  float eps;
+};
+
+// Arguments of one single-token gated attention (gsq_attn_decode; kernel in gsq_model.hip).
+struct AttnArgs {
+  const void* qg;   // [B] rows of H * 2hd: per head q then gate (row stride qg_stride)
+  const void* k;    // [B] rows of Hkv * hd (row stride k_stride)
+  const void* v;    // [B] rows of Hkv * hd (row stride v_stride)
+  const void* q_norm_w;  // [hd]
+  const void* k_norm_w;  // [hd]
+  const double* inv_freq;  // [rd / 2]
+  void* kc;         // [B, Hkv, L, hd]
+  void* vc;         // [B, Hkv, L, hd]
+  const int64_t* pos;  // position of the new token (device)
+  void* out;        // [B] rows of H * hd (row stride out_stride)
+  int64_t qg_stride, k_stride, v_stride, out_stride;
+  int B, H, Hkv, hd, rd, L;
+  float eps;
+};
+
 // QMM workspace: fp32 partial tiles of workgroups that share an output tile (2 slots per
 // workgroup, each sized to the launch plan's tile) and one arrival counter per workgroup, kept
 // at zero between launches. `part_bytes` bounds 2 * groups * slot bytes; `max_groups` bounds the

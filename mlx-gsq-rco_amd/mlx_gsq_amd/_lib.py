@@ -20,7 +20,7 @@ DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 ID_CODES = {torch.int32: 0, torch.int64: 1}
 
 # Every symbol include/gsq.h declares, with its ctypes signature.
-_I64, _I32, _VP = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p
+_I64, _I32, _VP, _F32 = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_float
 EXPORTS = {
     "gsq_version": (_I32, []),
     "gsq_block_bytes": (_I32, [_I32]),
@@ -32,6 +32,12 @@ EXPORTS = {
     "gsq_qmm": (_I32, [_I32, _VP, _VP, _I32, _VP, _I32, _I64, _I64, _I64, _VP]),
     "gsq_qmm_noalloc": (_I32, [_I32, _VP, _VP, _I32, _VP, _I32, _I64, _I64, _I64, _VP]),
     "gsq_embedding": (_I32, [_I32, _VP, _VP, _I32, _I64, _I64, _I64, _VP, _I32, _VP]),
+    "gsq_add_rms_norm": (_I32, [_VP, _VP, _VP, _VP, _I64, _I64, _F32, _I32, _VP]),
+    "gsq_swiglu": (_I32, [_VP, _VP, _I64, _I64, _I32, _VP]),
+    "gsq_attn_decode": (_I32, [_VP, _I64, _VP, _I64, _VP, _I64, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64,
+                               _I64, _I64, _I64, _I64, _F32, _I32, _VP]),
+    "gsq_gdn_step": (_I32, [_VP, _I64, _VP, _I64, _VP, _I64, _VP, _I64, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I64,
+                            _VP, _I64, _I64, _I64, _I64, _I64, _I64, _F32, _I32, _VP]),
     "gsq_last_error": (ctypes.c_char_p, []),
 }
 

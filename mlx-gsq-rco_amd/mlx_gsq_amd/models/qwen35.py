@@ -29,6 +29,12 @@ projections is written here on torch ops, following the same layer structure:
 Decoding keeps a cache per layer in fixed device buffers (convolution and fp32 recurrent
 state; K/V up to ``max_len`` positions, masked by a device-side position), so a whole
 single-token step can be captured once in a HIP graph and replayed (``GraphDecoder``).
+
+On a GPU the residual adds + RMSNorms, the SwiGLU, each GatedDeltaNet token and each
+single-token attention run as fused libgsq.so kernels (runtime/kernels/model_ops.py); gate and
+up, qkv and z, q and k are one packed launch each where they share a quantization type. The torch
+formulation below computes the same values and is what CPU tensors run (the structure test
+runs the model on the CPU with dense stand-ins for the packed layers).
 """
 from __future__ import annotations
 
@@ -88,6 +94,16 @@ def rms_norm(x, weight, eps):
     return y.to(x.dtype)
 
 
+def add_rms_norm(x, delta, weight, eps):
+    """x += delta in place (when given); returns rms_norm(x, weight, eps)."""
+    if x.is_cuda:
+        from ..runtime.kernels import model_ops
+        return model_ops.add_rms_norm(x, delta, weight, eps)
+    if delta is not None:
+        x.add_(delta)
+    return rms_norm(x, weight, eps)
+
+
 class Qwen35Cache:
     """Per-layer decode state in fixed device buffers, and the position of the next token.
 
@@ -122,13 +138,12 @@ class GatedDeltaNet(torch.nn.Module):
     """Linear-attention layer with the GGUF (cyclic) value-to-Q/K head routing
     (reference qwen35.py:48-111)."""
 
-    def __init__(self, args: Qwen35Args, layer: int, in_proj_qkv, in_proj_z, out_proj, w_a, w_b, conv_w, ssm_a,
-                 dt_bias, norm_w):
+    def __init__(self, args: Qwen35Args, layer: int, in_proj_qkvz, out_proj, w_a, w_b, conv_w, ssm_a, dt_bias,
+                 norm_w):
         super().__init__()
         self.args, self.layer = args, layer
-        self.in_proj_qkv, self.in_proj_z, self.out_proj = in_proj_qkv, in_proj_z, out_proj
-        self.register_buffer("w_a", w_a)        # (Hv, hidden)
-        self.register_buffer("w_b", w_b)        # (Hv, hidden)
+        self.in_proj_qkvz, self.out_proj = in_proj_qkvz, out_proj  # in_proj_qkvz: [qkv | z]
+        self.register_buffer("w_ab", torch.cat([w_a, w_b]))  # (2 Hv, hidden): a then b
         self.register_buffer("conv_w", conv_w)  # (conv_dim, kernel)
         self.register_buffer("ssm_a", ssm_a.float())    # (Hv,) = -exp(A_log)
         self.register_buffer("dt_bias", dt_bias.float())  # (Hv,)
@@ -140,10 +155,18 @@ class GatedDeltaNet(torch.nn.Module):
         hk, hv = a_.linear_num_key_heads, a_.linear_num_value_heads
         dk, dv = a_.linear_key_head_dim, a_.linear_value_head_dim
         kw = a_.linear_conv_kernel_dim
-        qkv = self.in_proj_qkv(x)                        # (B, S, conv_dim)
-        z = self.in_proj_z(x).view(B, S, hv, dv)
-        b = F.linear(x, self.w_b).float()                # (B, S, Hv)
-        a = F.linear(x, self.w_a).float()
+        qkvz = self.in_proj_qkvz(x)
+        qkv, z = qkvz[..., :a_.conv_dim], qkvz[..., a_.conv_dim:]   # (B, S, conv_dim), (B, S, Hv * dv)
+        if x.is_cuda:  # the a / b projections happen inside the fused step
+            from ..runtime.kernels import model_ops
+            outs = [model_ops.gdn_step(qkv[:, t], z[:, t], x[:, t], self.w_ab, cache.conv[self.layer], self.conv_w,
+                                       self.ssm_a, self.dt_bias, cache.rec[self.layer], self.norm_w,
+                                       key_heads=hk, value_heads=hv, head_k_dim=dk, head_v_dim=dv,
+                                       eps=a_.rms_norm_eps) for t in range(S)]
+            out = outs[0][:, None] if S == 1 else torch.stack(outs, dim=1)
+            return self.out_proj(out)
+        z = z.view(B, S, hv, dv)
+        a, b = F.linear(x, self.w_ab).float().split(hv, dim=-1)  # (B, S, Hv) each
         # depthwise causal convolution over [3 cached inputs, S new ones]
         conv_in = torch.cat([cache.conv[self.layer], qkv.to(cache.conv[self.layer].dtype)], dim=1)
         cache.conv[self.layer].copy_(conv_in[:, S:])
@@ -184,10 +207,10 @@ def _rotate_half(x):
 class FullAttention(torch.nn.Module):
     """Gated grouped-query attention with partial rotary embedding over the cached K/V."""
 
-    def __init__(self, args: Qwen35Args, layer: int, q_proj, k_proj, v_proj, o_proj, q_norm_w, k_norm_w):
+    def __init__(self, args: Qwen35Args, layer: int, qk_proj, v_proj, o_proj, q_norm_w, k_norm_w):
         super().__init__()
         self.args, self.layer = args, layer
-        self.q_proj, self.k_proj, self.v_proj, self.o_proj = q_proj, k_proj, v_proj, o_proj
+        self.qk_proj, self.v_proj, self.o_proj = qk_proj, v_proj, o_proj  # qk_proj: [q_proj | k_proj]
         self.register_buffer("q_norm_w", q_norm_w)
         self.register_buffer("k_norm_w", k_norm_w)
         rd = args.rotary_dim
@@ -209,11 +232,20 @@ class FullAttention(torch.nn.Module):
         a_ = self.args
         B, S, _ = x.shape
         H, Hkv, hd = a_.num_attention_heads, a_.num_key_value_heads, a_.head_dim
-        qg = self.q_proj(x).view(B, S, H, 2 * hd)
+        qk = self.qk_proj(x)
+        v = self.v_proj(x)
+        if x.is_cuda and S == 1:
+            from ..runtime.kernels import model_ops
+            out = model_ops.attn_decode(qk[:, 0, :H * 2 * hd], qk[:, 0, H * 2 * hd:], v[:, 0], self.q_norm_w,
+                                        self.k_norm_w, self.inv_freq, cache.k[self.layer], cache.v[self.layer],
+                                        cache.pos, heads=H, kv_heads=Hkv, head_dim=hd, rotary_dim=a_.rotary_dim,
+                                        eps=a_.rms_norm_eps)
+            return self.o_proj(out.view(B, 1, H * hd))
+        qg = qk[..., :H * 2 * hd].reshape(B, S, H, 2 * hd)
         q, gate = qg[..., :hd], qg[..., hd:].reshape(B, S, H * hd)
         q = rms_norm(q, self.q_norm_w, a_.rms_norm_eps)
-        k = rms_norm(self.k_proj(x).view(B, S, Hkv, hd), self.k_norm_w, a_.rms_norm_eps)
-        v = self.v_proj(x).view(B, S, Hkv, hd)
+        k = rms_norm(qk[..., H * 2 * hd:].reshape(B, S, Hkv, hd), self.k_norm_w, a_.rms_norm_eps)
+        v = v.view(B, S, Hkv, hd)
         pos = cache.pos + torch.arange(S, device=x.device)             # (S,)
         q = self._rope(q, pos)
         k = self._rope(k, pos)
@@ -234,18 +266,29 @@ class FullAttention(torch.nn.Module):
 
 
 class Qwen35Layer(torch.nn.Module):
-    def __init__(self, args, mixer, input_norm_w, post_norm_w, gate, up, down):
+    """Pre-norm mixer and SwiGLU MLP. ``forward(x, delta, cache)`` first adds the previous
+    layer's pending MLP output ``delta`` into the residual stream ``x`` (in place, fused with
+    this layer's input norm) and returns this layer's MLP output, to be added the same way by
+    the next layer or the final norm."""
+
+    def __init__(self, args, mixer, input_norm_w, post_norm_w, gate_up, down):
         super().__init__()
         self.args, self.mixer = args, mixer
         self.register_buffer("input_norm_w", input_norm_w)
         self.register_buffer("post_norm_w", post_norm_w)
-        self.gate, self.up, self.down = gate, up, down
+        self.gate_up, self.down = gate_up, down  # gate_up: [gate | up] of the MLP in one product
 
-    def forward(self, x, cache):
+    def forward(self, x, delta, cache):
         eps = self.args.rms_norm_eps
-        x = x + self.mixer(rms_norm(x, self.input_norm_w, eps), cache)
-        h = rms_norm(x, self.post_norm_w, eps)
-        return x + self.down((F.silu(self.gate(h).float()) * self.up(h).float()).to(x.dtype))
+        m = self.mixer(add_rms_norm(x, delta, self.input_norm_w, eps), cache)
+        gu = self.gate_up(add_rms_norm(x, m, self.post_norm_w, eps))
+        if gu.is_cuda:
+            from ..runtime.kernels import model_ops
+            act = model_ops.swiglu(gu)
+        else:
+            g, u = gu.split(gu.shape[-1] // 2, dim=-1)
+            act = (F.silu(g.float()) * u.float()).to(gu.dtype)
+        return self.down(act)
 
 
 class Qwen35Model(torch.nn.Module):
@@ -265,26 +308,49 @@ class Qwen35Model(torch.nn.Module):
         B, S = ids.shape
         if cache.length + S > cache.max_len:
             raise ValueError(f"cache holds {cache.max_len} positions; {cache.length} used, {S} more asked")
-        x = self.embed(ids).to(self.dtype).view(B, S, -1)
+        x = self.embed(ids).to(self.dtype).reshape(B, S, -1).contiguous()
+        delta = None
         for layer in self.layers:
-            x = layer(x, cache)
-        logits = self.lm_head(rms_norm(x, self.norm_w, self.args.rms_norm_eps))
+            delta = layer(x, delta, cache)
+        logits = self.lm_head(add_rms_norm(x, delta, self.norm_w, self.args.rms_norm_eps))
         cache.pos.add_(S)
         cache.length += S
         return logits
 
 
-def build_qwen35(store, dtype=torch.float16, args: Qwen35Args | None = None, linear=None, embedding=None):
+class _SideBySide(torch.nn.Module):
+    """Several projections of one input, outputs concatenated on the last axis."""
+
+    def __init__(self, mods):
+        super().__init__()
+        self.mods = torch.nn.ModuleList(mods)
+
+    def forward(self, x):
+        return torch.cat([m(x) for m in self.mods], dim=-1)
+
+
+def build_qwen35(store, dtype=torch.float16, args: Qwen35Args | None = None, linear=None, embedding=None,
+                 fused=None):
     """The model of ``store`` (a ``PackedModelStore`` with the reference's GGUF tensor names,
-    qwen35.py:114-152) on the store's device. ``linear(weight)`` and ``embedding(weight, dtype)``
-    build the packed modules (``GSQLinear`` / ``GSQEmbedding`` by default)."""
-    from ..nn import GSQEmbedding, GSQLinear
+    qwen35.py:114-152) on the store's device. ``linear(weight)``, ``fused(weights)`` (the
+    outputs of several weights side by side) and ``embedding(weight, dtype)`` build the packed
+    modules (``GSQLinear``, ``GSQFusedLinear(..., concat=True)``, ``GSQEmbedding`` by default)."""
+    from ..nn import GSQEmbedding, GSQFusedLinear, GSQLinear
     args = args or Qwen35Args()
     linear = linear or GSQLinear
+    fused = fused or (lambda ws: GSQFusedLinear(ws, concat=True))
     embedding = embedding or (lambda w, dt: GSQEmbedding(w, dtype=dt))
 
     def plain(name, dt=dtype):
         return store.materialize_plain(name).to(dt)
+
+    def joint(names):
+        """One module whose output is the named projections' outputs side by side: one packed
+        launch when they share a quantization type."""
+        ws = [store.weight(n) for n in names]
+        if len({w.quantization_type for w in ws}) == 1:
+            return fused(ws)
+        return _SideBySide([linear(w) for w in ws])
 
     layers = []
     for i in range(args.num_hidden_layers):
@@ -292,18 +358,18 @@ def build_qwen35(store, dtype=torch.float16, args: Qwen35Args | None = None, lin
         if args.is_linear(i):
             conv = plain(p + "ssm_conv1d.weight")
             mixer = GatedDeltaNet(
-                args, i, linear(store.weight(p + "attn_qkv.weight")), linear(store.weight(p + "attn_gate.weight")),
+                args, i, joint([p + "attn_qkv.weight", p + "attn_gate.weight"]),
                 linear(store.weight(p + "ssm_out.weight")), plain(p + "ssm_alpha.weight"),
                 plain(p + "ssm_beta.weight"), conv.reshape(conv.shape[0], conv.shape[-1]),
                 plain(p + "ssm_a", torch.float32), plain(p + "ssm_dt.bias", torch.float32),
                 plain(p + "ssm_norm.weight"))
         else:
             mixer = FullAttention(
-                args, i, linear(store.weight(p + "attn_q.weight")), linear(store.weight(p + "attn_k.weight")),
+                args, i, joint([p + "attn_q.weight", p + "attn_k.weight"]),
                 linear(store.weight(p + "attn_v.weight")), linear(store.weight(p + "attn_output.weight")),
                 plain(p + "attn_q_norm.weight"), plain(p + "attn_k_norm.weight"))
         layers.append(Qwen35Layer(args, mixer, plain(p + "attn_norm.weight"), plain(p + "post_attention_norm.weight"),
-                                  linear(store.weight(p + "ffn_gate.weight")), linear(store.weight(p + "ffn_up.weight")),
+                                  fused([store.weight(p + "ffn_gate.weight"), store.weight(p + "ffn_up.weight")]),
                                   linear(store.weight(p + "ffn_down.weight"))))
     return Qwen35Model(args, embedding(store.weight("token_embd.weight"), dtype), layers,
                        plain("output_norm.weight"), linear(store.weight("output.weight")), dtype)

@@ -48,16 +48,18 @@ class GSQFusedLinear(torch.nn.Module):
 
     Packed rows are whole superblocks, row-major, so concatenating the matrices along the
     output dimension is a byte concatenation; it is done once here, on the weights' device.
-    ``forward`` returns one output per weight (views of one result), computed exactly as
-    ``GSQLinear`` computes the concatenated matrix. No counterpart in the reference, whose
-    model applies each projection on its own.
+    ``forward`` returns one output per weight (views of one result), or with ``concat=True`` the
+    one tensor of all outputs side by side, computed exactly as ``GSQLinear`` computes the
+    concatenated matrix. No counterpart in the reference, whose model applies each projection
+    on its own.
     """
 
-    def __init__(self, weights, biases=None):
+    def __init__(self, weights, biases=None, concat=False):
         super().__init__()
         weights = list(weights)
         if not weights:
             raise ValueError("no weights to fuse")
+        self.concat = concat
         qtypes = {w.quantization_type for w in weights}
         widths = {w.logical_shape[1] for w in weights}
         if len(qtypes) != 1:
@@ -75,6 +77,11 @@ class GSQFusedLinear(torch.nn.Module):
 
     def forward(self, x):
         y = _apply(x, self.packed_weight, self.qtype, self.out_features, self.in_features)
+        if self.concat:  # one tensor of the concatenated outputs
+            if self.biases is not None:
+                y = y + torch.cat([torch.zeros(n, dtype=y.dtype, device=y.device) if b is None else b
+                                   for n, b in zip(self.splits, self.biases)])
+            return y
         outs = y.split(self.splits, dim=-1)
         if self.biases is None:
             return outs

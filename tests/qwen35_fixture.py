@@ -122,13 +122,17 @@ class DenseLinear(torch.nn.Module):
 
 
 def dense_factories(store):
+    """(linear, fused, embedding) factories of build_qwen35 over the dense dequantized weights."""
     def linear(weight):
         return DenseLinear(store.dense[weight.name])
+
+    def fused(weights):
+        return DenseLinear(np.concatenate([store.dense[w.name] for w in weights]))
 
     def embedding(weight, dtype):
         table = torch.from_numpy(store.dense[weight.name])
         return lambda ids: table[ids].to(dtype)
-    return linear, embedding
+    return linear, fused, embedding
 
 
 def hf_model(store):

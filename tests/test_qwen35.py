@@ -27,8 +27,8 @@ def store_and_ref():
 
 def test_cpu_prefill_and_decode_match_hf(store_and_ref):
     store, ref = store_and_ref
-    linear, embedding = dense_factories(store)
-    model = build_qwen35(store, dtype=torch.float32, args=ARGS, linear=linear, embedding=embedding)
+    linear, fused, embedding = dense_factories(store)
+    model = build_qwen35(store, dtype=torch.float32, args=ARGS, linear=linear, fused=fused, embedding=embedding)
     with torch.no_grad():
         cache = model.new_cache(batch=1, max_len=16)
         pre = model(torch.tensor([IDS]), cache)
@@ -52,8 +52,8 @@ def test_cpu_head_routing_is_cyclic(store_and_ref):
     """With value heads routed by h // 2 (mlx-lm's generic grouping) instead of h % 2 the
     result differs from HF-with-permuted-heads: the check above is sensitive to the routing."""
     store, ref = store_and_ref
-    linear, embedding = dense_factories(store)
-    model = build_qwen35(store, dtype=torch.float32, args=ARGS, linear=linear, embedding=embedding)
+    linear, fused, embedding = dense_factories(store)
+    model = build_qwen35(store, dtype=torch.float32, args=ARGS, linear=linear, fused=fused, embedding=embedding)
     orig = torch.Tensor.repeat
 
     def grouped(self, *sizes):
@@ -93,3 +93,101 @@ def test_gpu_decode_matches_hf_and_graph_replays(store_and_ref):
             out = dec.step(ids[:, i:i + 1]).float().cpu()
             assert torch.equal(out[0, 0], eager[0, i]), i
         assert cache.length == len(IDS)
+
+
+class _Given(torch.nn.Module):
+    """Stands in for a projection: returns the tensor set for the current step."""
+
+    def __init__(self):
+        super().__init__()
+        self.value = None
+
+    def forward(self, x):
+        return self.value
+
+
+@pytest.mark.gpu
+def test_gpu_fused_ops_match_torch_formulation():
+    """The fused kernels (add + RMSNorm, SwiGLU, GatedDeltaNet token) against the model's torch
+    formulation run on the CPU in float32, at the 27B head shapes (16 key / 48 value heads of
+    128, conv 4) for 3 tokens of 2 batch rows."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from mlx_gsq_amd.models.qwen35 import GatedDeltaNet, Qwen35Args, Qwen35Cache, rms_norm
+    from mlx_gsq_amd.runtime.kernels import model_ops
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(5)
+    # add + RMSNorm and SwiGLU
+    x = torch.randn(3, 5120, generator=g).half()
+    d = torch.randn(3, 5120, generator=g).half()
+    w = (1 + 0.1 * torch.randn(5120, generator=g)).half()
+    xg = x.to(dev)
+    y = model_ops.add_rms_norm(xg, d.to(dev), w.to(dev), 1e-6).cpu()
+    xs = x + d
+    assert torch.equal(xg.cpu(), xs)
+    assert rel_l2(y.float().numpy(), rms_norm(xs.float(), w.float(), 1e-6).numpy()) <= 1e-3
+    gu = torch.randn(3, 2, 1024, generator=g).half()
+    s = model_ops.swiglu(gu.to(dev)).cpu()
+    want = torch.nn.functional.silu(gu[..., :512].float()) * gu[..., 512:].float()
+    assert rel_l2(s.float().numpy(), want.numpy()) <= 1e-3
+    # GatedDeltaNet token steps
+    a = Qwen35Args(num_hidden_layers=1)
+    B, C, hv = 2, a.conv_dim, a.linear_num_value_heads
+    params = dict(w_a=torch.randn(hv, 64, generator=g) / 8, w_b=torch.randn(hv, 64, generator=g) / 8,
+                  conv_w=0.5 * torch.randn(C, 4, generator=g), ssm_a=-torch.rand(hv, generator=g) * 8 - 1,
+                  dt_bias=torch.randn(hv, generator=g), norm_w=1 + 0.1 * torch.randn(a.linear_value_head_dim, generator=g))
+
+    def module(device, dtype):
+        p = {k: (v.to(device, dtype) if k not in ("ssm_a", "dt_bias") else v.to(device)) for k, v in params.items()}
+        m = GatedDeltaNet(a, 0, _Given(), torch.nn.Identity(), p["w_a"], p["w_b"], p["conv_w"], p["ssm_a"],
+                          p["dt_bias"], p["norm_w"])
+        return m, Qwen35Cache(a, B, 8, device, dtype)
+    cpu, ccache = module("cpu", torch.float32)
+    gpu, gcache = module(dev, torch.float16)
+    for t in range(3):
+        qkv = torch.randn(B, 1, C, generator=g).half()
+        z = torch.randn(B, 1, a.value_dim, generator=g).half()
+        h = torch.randn(B, 1, 64, generator=g).half()
+        cpu.in_proj_qkvz.value = torch.cat([qkv, z], dim=-1).float()
+        gpu.in_proj_qkvz.value = torch.cat([qkv, z], dim=-1).to(dev)
+        want = cpu(h.float(), ccache)
+        got = gpu(h.to(dev), gcache).float().cpu()
+        assert torch.isfinite(got).all()
+        assert rel_l2(got.numpy(), want.numpy()) <= 5e-3, t
+        assert rel_l2(gcache.rec[0].cpu().numpy(), ccache.rec[0].numpy()) <= 1e-3, t
+        assert torch.equal(gcache.conv[0].cpu().float(), ccache.conv[0])
+
+
+@pytest.mark.gpu
+def test_gpu_attention_decode_matches_torch_formulation():
+    """The fused single-token attention against the torch formulation (CPU, float32) at the 27B
+    head shapes (24 query / 4 KV heads of 256, rotary 64) over 5 positions of 2 batch rows,
+    caches included."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from mlx_gsq_amd.models.qwen35 import FullAttention, Qwen35Args, Qwen35Cache
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(9)
+    a = Qwen35Args(num_hidden_layers=4)
+    B, H, Hkv, hd = 2, a.num_attention_heads, a.num_key_value_heads, a.head_dim
+    qn, kn = 1 + 0.1 * torch.randn(hd, generator=g), 1 + 0.1 * torch.randn(hd, generator=g)
+
+    def module(device, dtype):
+        m = FullAttention(a, 3, _Given(), _Given(), torch.nn.Identity(), qn.to(device, dtype), kn.to(device, dtype))
+        return m, Qwen35Cache(a, B, 16, device, dtype)
+    cpu, ccache = module("cpu", torch.float32)
+    gpu, gcache = module(dev, torch.float16)
+    for t in range(5):
+        qk = torch.randn(B, 1, H * 2 * hd + Hkv * hd, generator=g).half()
+        v = torch.randn(B, 1, Hkv * hd, generator=g).half()
+        cpu.qk_proj.value, cpu.v_proj.value = qk.float(), v.float()
+        gpu.qk_proj.value, gpu.v_proj.value = qk.to(dev), v.to(dev)
+        want = cpu(torch.zeros(B, 1, 8), ccache)
+        got = gpu(torch.zeros(B, 1, 8, device=dev, dtype=torch.float16), gcache).float().cpu()
+        ccache.pos.add_(1)
+        gcache.pos.add_(1)
+        assert torch.isfinite(got).all()
+        assert rel_l2(got.numpy(), want.numpy()) <= 5e-3, t
+        for c in (3,):
+            assert rel_l2(gcache.k[c][:, :, :t + 1].float().cpu().numpy(), ccache.k[c][:, :, :t + 1].numpy()) <= 2e-3
+            assert torch.equal(gcache.v[c][:, :, :t + 1].float().cpu(), ccache.v[c][:, :, :t + 1])

@@ -123,16 +123,38 @@ struct LdsV4 {
   }
 };
 
+// Sign bits applied with bit operations: bit k of a group's 32 sign bits flips weight k. The fp16
+// pair of weights 2w, 2w+1 takes its sign bits (15 and 31) from bits 2w and 2w+1: two packed
+// 16-bit halves [bits 0-15 | bits 1-16] and [bits 16-31 | bits 17-31] of the sign word, shifted
+// left by 15 - 2(w mod 8) per half, put those bits at 15 and 31; v_bfi then replaces the sign
+// bits of the codebook pair (codebook values are positive, so this equals the XOR of a mask).
+struct SignBits {
+  uint32_t z[2];
+  __device__ __forceinline__ explicit SignBits(uint32_t s) {
+    const uint32_t t = s >> 1;
+    z[0] = __builtin_amdgcn_perm(t, s, 0x05040100u);
+    z[1] = __builtin_amdgcn_perm(t, s, 0x07060302u);
+  }
+  template <int W>
+  __device__ __forceinline__ uint32_t apply(uint32_t g) const {
+    constexpr unsigned short sh = 15 - 2 * (W & 7);
+    const uint32_t m = __builtin_bit_cast(uint32_t, __builtin_bit_cast(ushort2_t, z[W >> 3]) << (ushort2_t){sh, sh});
+    return (m & 0x80008000u) | (g & 0x7FFF7FFFu);
+  }
+};
+
 // ---- per-type decode + dot -----------------------------------------------------------
-// Qmv<T>::kTbl is the size of the type's LDS table: an exact byte image prepared on the host
-// (build_qmv_table below) and copied into LDS with DMA at kernel start. Codebooks are fp16;
-// sign tables hold XOR masks that flip the fp16 sign bits of a pair of codebook values.
+// Qmv<T>::kTbl is the size of the type's table image, an exact byte image prepared on the host
+// (build_qmv_table below); its first kLds bytes are copied into LDS with DMA at kernel start.
+// Codebooks are fp16; sign tables hold XOR masks that flip the fp16 sign bits of a pair of
+// codebook values.
 template <int T> struct Qmv;
 
 template <> struct Qmv<Q4_K> {
   static constexpr int kPair = PAIR_K;
   static constexpr int kSums = 1;
   static constexpr int kTbl = 0;
+  static constexpr int kLds = kTbl;  // bytes of it the QMV decoder keeps in LDS
   template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t*, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
@@ -171,6 +193,7 @@ template <> struct Qmv<Q2_K> {
   static constexpr int kPair = PAIR_K;
   static constexpr int kSums = 2;
   static constexpr int kTbl = 0;
+  static constexpr int kLds = kTbl;  // bytes of it the QMV decoder keeps in LDS
   template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t*, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
@@ -206,6 +229,7 @@ template <> struct Qmv<Q6_K> {
   static constexpr int kPair = PAIR_K;
   static constexpr int kSums = 2;
   static constexpr int kTbl = 0;
+  static constexpr int kLds = kTbl;  // bytes of it the QMV decoder keeps in LDS
   // Group g = plane g % 4 of 128-weight chunk g / 4: weight e takes nibble plane / 2 of ql byte
   // 64 chunk + 32 (plane % 2) + e and bits 2 plane of qh byte 128 + 32 chunk + e (k_decode.py:
   // 51-64). Each word of 4 weights is one funnel shift out of the ql stream (nibble to bits
@@ -251,6 +275,7 @@ template <> struct Qmv<IQ4_XS> {
   static constexpr int kPair = PAIR_16;
   static constexpr int kSums = 0;
   static constexpr int kTbl = 1024;  // 256 fp16 pairs (kvalues[lo nibble], kvalues[hi nibble])
+  static constexpr int kLds = kTbl;  // bytes of it the QMV decoder keeps in LDS
   template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
@@ -283,8 +308,11 @@ template <> struct Qmv<IQ3_S> {
   static constexpr int kSums = 0;
   static constexpr int kGridB = 512 * 4 * 2;
   // grid + 16 nibble sign masks (two words each: a 128-byte table whose reads never conflict;
-  // 256 byte masks of four words were 2-4% slower on the 17408-row shapes)
+  // 256 byte masks of four words were 2-4% slower on the 17408-row shapes, and signs from bit
+  // operations as in IQ2_S, 8 more VALU instructions per 32 weights here, 4% slower at
+  // 5120x17408 and even elsewhere)
   static constexpr int kTbl = kGridB + 16 * 8;
+  static constexpr int kLds = kTbl;  // bytes of it the QMV decoder keeps in LDS
   template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
@@ -299,7 +327,7 @@ template <> struct Qmv<IQ3_S> {
     float acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = 0.f;
-const LdsV2 nm{tbl + kGridB};
+    const LdsV2 nm{tbl + kGridB};
     uint2 Ns[8], Gs[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {  // all table reads of the group in flight before the first use
@@ -321,6 +349,7 @@ template <> struct Qmv<IQ3_XXS> {
   static constexpr int kSums = 0;
   static constexpr int kGridB = 256 * 4 * 2;
   static constexpr int kTbl = kGridB + 128 * 16;
+  static constexpr int kLds = kTbl;  // bytes of it the QMV decoder keeps in LDS
   template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
@@ -359,6 +388,7 @@ template <> struct Qmv<IQ2_XXS> {
   static constexpr int kSums = 0;
   static constexpr int kGridB = 256 * 8 * 2;
   static constexpr int kTbl = kGridB + 128 * 16;
+  static constexpr int kLds = kTbl;  // bytes of it the QMV decoder keeps in LDS
   template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
@@ -396,6 +426,7 @@ template <> struct Qmv<IQ2_XS> {
   static constexpr int kSums = 0;
   static constexpr int kGridB = 512 * 8 * 2;
   static constexpr int kTbl = kGridB + 128 * 16;
+  static constexpr int kLds = kTbl;  // bytes of it the QMV decoder keeps in LDS
   template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
@@ -435,8 +466,11 @@ template <> struct Qmv<IQ2_S> {
   static constexpr int kPair = PAIR_NAT;
   static constexpr int kSums = 0;
   static constexpr int kGridB = 1024 * 8 * 2;
-  // grid + 16 nibble sign masks (two words each, as IQ3_S: 4% faster than 256 byte masks)
+  // table image: grid + 16 nibble sign masks (the QMM decoder's); QMV applies the signs with
+  // bit operations (SignBits: a third fewer LDS reads per group, 0-2% faster than the nibble
+  // masks) and copies only the grid
   static constexpr int kTbl = kGridB + 16 * 8;
+  static constexpr int kLds = kGridB;
   template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
@@ -449,25 +483,19 @@ template <> struct Qmv<IQ2_S> {
     float a0[MR], a1[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) { a0[m] = 0.f; a1[m] = 0.f; }
-    uint4 Ms[4], Gs[4];
-const LdsV2 nm{tbl + kGridB};
+    uint4 Gs[4];
 #pragma unroll
-    for (int l = 0; l < 4; ++l) {  // all table reads of the group in flight before the first use
+    for (int l = 0; l < 4; ++l)  // all table reads of the group in flight before the first use
       Gs[l] = grid[bfe(qs, 8 * l, 8) | (bfe(qh, 2 * l, 2) << 8)];
-      const uint2 lo = nm[bfe(sg, 8 * l, 4)], hi = nm[bfe(sg, 8 * l + 4, 4)];
-      Ms[l] = make_uint4(lo.x, lo.y, hi.x, hi.y);
-    }
-#pragma unroll
-    for (int l = 0; l < 4; ++l) {
-      const uint4 M = Ms[l], G = Gs[l];
-      if (l < 2) {
-        dacc<MR, XS>(G.x ^ M.x, x, 4 * l, a0); dacc<MR, XS>(G.y ^ M.y, x, 4 * l + 1, a0);
-        dacc<MR, XS>(G.z ^ M.z, x, 4 * l + 2, a0); dacc<MR, XS>(G.w ^ M.w, x, 4 * l + 3, a0);
-      } else {
-        dacc<MR, XS>(G.x ^ M.x, x, 4 * l, a1); dacc<MR, XS>(G.y ^ M.y, x, 4 * l + 1, a1);
-        dacc<MR, XS>(G.z ^ M.z, x, 4 * l + 2, a1); dacc<MR, XS>(G.w ^ M.w, x, 4 * l + 3, a1);
-      }
-    }
+    const SignBits sbits(sg);
+    dacc<MR, XS>(sbits.apply<0>(Gs[0].x), x, 0, a0);   dacc<MR, XS>(sbits.apply<1>(Gs[0].y), x, 1, a0);
+    dacc<MR, XS>(sbits.apply<2>(Gs[0].z), x, 2, a0);   dacc<MR, XS>(sbits.apply<3>(Gs[0].w), x, 3, a0);
+    dacc<MR, XS>(sbits.apply<4>(Gs[1].x), x, 4, a0);   dacc<MR, XS>(sbits.apply<5>(Gs[1].y), x, 5, a0);
+    dacc<MR, XS>(sbits.apply<6>(Gs[1].z), x, 6, a0);   dacc<MR, XS>(sbits.apply<7>(Gs[1].w), x, 7, a0);
+    dacc<MR, XS>(sbits.apply<8>(Gs[2].x), x, 8, a1);   dacc<MR, XS>(sbits.apply<9>(Gs[2].y), x, 9, a1);
+    dacc<MR, XS>(sbits.apply<10>(Gs[2].z), x, 10, a1); dacc<MR, XS>(sbits.apply<11>(Gs[2].w), x, 11, a1);
+    dacc<MR, XS>(sbits.apply<12>(Gs[3].x), x, 12, a1); dacc<MR, XS>(sbits.apply<13>(Gs[3].y), x, 13, a1);
+    dacc<MR, XS>(sbits.apply<14>(Gs[3].z), x, 14, a1); dacc<MR, XS>(sbits.apply<15>(Gs[3].w), x, 15, a1);
     const float d0 = dh * (0.5f + (float)(sb & 15u)) * 0.25f, d1 = dh * (0.5f + (float)(sb >> 4)) * 0.25f;
 #pragma unroll
     for (int m = 0; m < MR; ++m) out[m] += d0 * a0[m] + d1 * a1[m];
@@ -478,6 +506,7 @@ template <> struct Qmv<IQ1_S> {
   static constexpr int kPair = PAIR_NAT;
   static constexpr int kSums = 1;
   static constexpr int kTbl = 2048 * 8 * 2;
+  static constexpr int kLds = kTbl;  // bytes of it the QMV decoder keeps in LDS
   template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
@@ -511,6 +540,7 @@ template <> struct Qmv<IQ1_M> {
   static constexpr int kPair = PAIR_NAT;
   static constexpr int kSums = 4;
   static constexpr int kTbl = 2048 * 8 * 2;
+  static constexpr int kLds = kTbl;  // bytes of it the QMV decoder keeps in LDS
   template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
@@ -772,7 +802,7 @@ __global__ void __launch_bounds__(qmv_max_threads(qmv_weight(MR, GL, XS))) qmv_k
   const int tid = threadIdx.x, lane = tid & 63, nw = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   // layout offsets count from the table's start; dynamic LDS starts where the table ends
-  uint8_t* tbl = QmvTblLds<P::kTbl>::get();
+  uint8_t* tbl = QmvTblLds<P::kLds>::get();
   uint8_t* dyn = smem - a.tbl_bytes;
   uint8_t* xst = dyn + a.x_off;
   float* red = reinterpret_cast<float*>(dyn + a.red_off);   // [rows_per_wg][MR][W]
@@ -800,7 +830,7 @@ __global__ void __launch_bounds__(qmv_max_threads(qmv_weight(MR, GL, XS))) qmv_k
   // item; the ring fills up gradually (below). A wave that queued its whole ring at once would
   // stall in DMA issue (the CU's memory queue is full at kernel start) before its first item's
   // decode, and would put the first items of the waves behind it back.
-  if constexpr (P::kTbl > 0) dma_copy(a.tb.qmv_tbl, P::kTbl, tbl, wave, nw, lane);
+  if constexpr (P::kLds > 0) dma_copy(a.tb.qmv_tbl, P::kLds, tbl, wave, nw, lane);
   if (a.x_lds) dma_copy(a.x, a.x_bytes, xst, wave, nw, lane);
   int issued = 0;  // items issued so far (wave-uniform)
   if (nitems > 0) {
@@ -922,7 +952,7 @@ static hipError_t launch_qmv_t(const QmvArgs& a, int grid, int threads, size_t l
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       160 * 1024 - Qmv<T>::kTbl);
+                                       160 * 1024 - Qmv<T>::kLds);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
@@ -932,6 +962,8 @@ static hipError_t launch_qmv_t(const QmvArgs& a, int grid, int threads, size_t l
 
 template <int T>
 static int qmv_tbl_bytes() { return Qmv<T>::kTbl; }
+template <int T>
+static int qmv_lds_tbl_bytes() { return Qmv<T>::kLds; }
 
 // Slices per wave of each variant: activation registers per lane stay near 60 (fp16, one
 // activation row: 3 slices x 20) to keep 16 waves per CU resident.
@@ -972,6 +1004,19 @@ int qmv_table_bytes(int qt) {
     case IQ2_XXS: return qmv_tbl_bytes<IQ2_XXS>(); case IQ2_XS: return qmv_tbl_bytes<IQ2_XS>();
     case IQ2_S: return qmv_tbl_bytes<IQ2_S>(); case IQ1_S: return qmv_tbl_bytes<IQ1_S>();
     case IQ1_M: return qmv_tbl_bytes<IQ1_M>();
+    default: return -1;
+  }
+}
+
+// Bytes of the table image the QMV kernel copies into LDS (a prefix of the image).
+static int qmv_lds_table_bytes(int qt) {
+  switch (qt) {
+    case Q2_K: return qmv_lds_tbl_bytes<Q2_K>(); case Q4_K: return qmv_lds_tbl_bytes<Q4_K>();
+    case Q6_K: return qmv_lds_tbl_bytes<Q6_K>(); case IQ4_XS: return qmv_lds_tbl_bytes<IQ4_XS>();
+    case IQ3_S: return qmv_lds_tbl_bytes<IQ3_S>(); case IQ3_XXS: return qmv_lds_tbl_bytes<IQ3_XXS>();
+    case IQ2_XXS: return qmv_lds_tbl_bytes<IQ2_XXS>(); case IQ2_XS: return qmv_lds_tbl_bytes<IQ2_XS>();
+    case IQ2_S: return qmv_lds_tbl_bytes<IQ2_S>(); case IQ1_S: return qmv_lds_tbl_bytes<IQ1_S>();
+    case IQ1_M: return qmv_lds_tbl_bytes<IQ1_M>();
     default: return -1;
   }
 }
@@ -1060,7 +1105,7 @@ static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, 
   a.W = (a.nslices + gl - 1) / gl;
   const int wpc = g_qmv_tuning.wg_per_cu < 1 ? 1 : g_qmv_tuning.wg_per_cu;
   const int max_waves = qmv_max_threads(qmv_weight(mr, gl, xs)) / 64;
-  a.tbl_bytes = (qmv_table_bytes(qt) + 15) & ~15;
+  a.tbl_bytes = (qmv_lds_table_bytes(qt) + 15) & ~15;
   if (a.tbl_bytes > 0 && !tb.qmv_tbl) return hipErrorInvalidValue;
   const int lds_cap = kLdsBytes / wpc;
   a.x_bytes = M * K * (xdt == DT_F32 ? 4 : 2);

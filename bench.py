@@ -33,6 +33,7 @@ Extra modes for counter collection (rocprofv3 --pmc runs):
   --profile-case Q6_K:17408x5120   only launches of that product (rotating 8 weight copies)
   --copy-bytes N                   only a plain device-to-device copy of N bytes
   --qmm-profile-case IQ3_S:512x17408x5120   only launches of that QMM product
+  --model-decode                   only the model_decode leg (for kernel traces of the step)
 """
 from __future__ import annotations
 
@@ -736,6 +737,7 @@ def main():
     ap.add_argument("--profile-case", default=None, help="TYPE:NxK, launch only that product")
     ap.add_argument("--copy-bytes", type=int, default=0, help="run only a plain copy of this many bytes")
     ap.add_argument("--qmm-profile-case", default=None, help="TYPE:MxNxK, launch only that QMM product")
+    ap.add_argument("--model-decode", action="store_true", help="run only the Qwen3.5-hybrid decode-step leg")
     ap.add_argument("--reps", type=int, default=20)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -743,7 +745,8 @@ def main():
               "(QMV/QMM would shard along N with no exchange; see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
     # the CPU baseline runs first, in fresh worker processes, before anything touches the GPU
-    cpu = None if (args.no_cpu or args.copy_bytes or args.profile_case or args.qmm_profile_case) else cpu_baseline()
+    cpu = None if (args.no_cpu or args.copy_bytes or args.profile_case or args.qmm_profile_case
+                   or args.model_decode) else cpu_baseline()
     import torch
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
@@ -755,6 +758,11 @@ def main():
         return
     if args.qmm_profile_case:
         qmm_profile_case(args.qmm_profile_case, args.reps, device)
+        return
+    if args.model_decode:
+        from mlx_gsq_amd import tables
+        tables.set_tables(tables.synthetic_tables(0))
+        print(json.dumps({"model_decode": run_model_decode(device)}), flush=True)
         return
     qc, per_launch, eager_ms, graph_ms = run_qmv(args.steps, args.warmup, device)
     qmm = {} if args.no_qmm else run_qmm(device)

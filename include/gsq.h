@@ -70,6 +70,22 @@ int gsq_dequant(int qtype_id, const void* packed, int64_t nblocks, float* out, v
 int gsq_qmv(int qtype_id, const void* packed, const void* x, int x_dtype, void* y, int y_dtype,
             int64_t M, int64_t N, int64_t K, void* stream);
 
+/* One fp16 activation row that the QMV kernel forms itself before the product (a decode
+ * step's norm or MLP activation fused into the projection that consumes it; no counterpart in
+ * the reference, whose model runs them as separate mlx operations in
+ * mlx_gsq/models/qwen35.py). y[1, N] = row * W[N, K]^T with
+ *   GSQ_PRE_ADD_RMSNORM: s = round(x + pre_a) (pre_a may be NULL: s = x), written to res_out
+ *     when not NULL (res_out must not alias x or pre_a); row = round(s / sqrt(mean(s^2) + eps)
+ *     * pre_w), as gsq_add_rms_norm computes it;
+ *   GSQ_PRE_SWIGLU: x holds [gate | up] (2K values); row = round(silu(gate) * up), as
+ *     gsq_swiglu computes it (pre_a, pre_w, eps, res_out unused).
+ * The row is written to x_out when not NULL. All vectors fp16, 16-byte aligned; K a multiple
+ * of 8 up to 32768. */
+#define GSQ_PRE_ADD_RMSNORM 1
+#define GSQ_PRE_SWIGLU 2
+int gsq_qmv_pre(int qtype_id, const void* packed, int pre_op, const void* x, const void* pre_a, const void* pre_w,
+                float eps, void* res_out, void* x_out, void* y, int y_dtype, int64_t N, int64_t K, void* stream);
+
 /* Same product with the tiled MFMA kernel (prefill, large M). Replaces quantized_matmul
  * (mlx_gsq/runtime/kernels/qmm.py:559-594). Workgroups that share an output tile exchange
  * fp32 partials through a workspace the library keeps per (device, stream) and allocates on

@@ -15,6 +15,8 @@
 namespace gsq {
 hipError_t launch_dequant(int qt, const uint8_t* packed, int64_t nblocks, float* out, const DevTables& t,
                           hipStream_t s);
+hipError_t launch_qmv_pre(int qt, const uint8_t* packed, const void* x, void* y, int ydt, int64_t N, int K,
+                          const QmvPre& pre, const DevTables& tb, int num_cus, hipStream_t s);
 hipError_t launch_qmv(int qt, const uint8_t* packed, const void* x, int xdt, void* y, int ydt, int64_t M, int64_t N,
                       int K, const DevTables& tb, int num_cus, hipStream_t s);
 hipError_t launch_qmm(int qt, const uint8_t* packed, const void* x, int xdt, void* y, int ydt, int64_t M, int64_t N,
@@ -350,6 +352,35 @@ int gsq_qmv(int qt, const void* packed, const void* x, int xdt, void* y, int ydt
   if (int rc = resolve(qt, &tb, &cus, static_cast<hipStream_t>(stream))) return rc;
   hipError_t e = launch_qmv(qt, static_cast<const uint8_t*>(packed), x, xdt, y, ydt, M, N, (int)K, tb, cus,
                             static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(GSQ_E_HIP, "qmv launch: %s", hipGetErrorString(e));
+  return GSQ_OK;
+}
+
+int gsq_qmv_pre(int qt, const void* packed, int pre_op, const void* x, const void* pre_a, const void* pre_w,
+                float eps, void* res_out, void* x_out, void* y, int ydt, int64_t N, int64_t K, void* stream) {
+  if (int rc = check_common(qt, packed, 1, N, K, GSQ_F16, ydt)) return rc;
+  if (pre_op != GSQ_PRE_ADD_RMSNORM && pre_op != GSQ_PRE_SWIGLU) return fail(GSQ_E_VALUE, "unknown pre_op %d", pre_op);
+  if (!x || !y) return fail(GSQ_E_VALUE, "NULL pointer");
+  if (pre_op == GSQ_PRE_ADD_RMSNORM && !pre_w) return fail(GSQ_E_VALUE, "the norm weight is NULL");
+  if (pre_op == GSQ_PRE_ADD_RMSNORM && !(eps >= 0.f)) return fail(GSQ_E_VALUE, "eps must be >= 0");
+  if (K % 8 || K > 32768) return fail(GSQ_E_VALUE, "K must be a multiple of 8 up to 32768 (got %lld)", (long long)K);
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(pre_a) | reinterpret_cast<uintptr_t>(pre_w) |
+       reinterpret_cast<uintptr_t>(res_out) | reinterpret_cast<uintptr_t>(x_out)) & 15)
+    return fail(GSQ_E_VALUE, "x, pre_a, pre_w, res_out and x_out must be 16-byte aligned");
+  if (res_out && (res_out == x || res_out == pre_a))
+    return fail(GSQ_E_VALUE, "res_out must not alias x or pre_a (other workgroups still read them)");
+  QmvPre pre;
+  pre.op = pre_op == GSQ_PRE_ADD_RMSNORM ? QMV_PRE_ADD_NORM : QMV_PRE_SWIGLU;
+  pre.a = pre_op == GSQ_PRE_SWIGLU ? x : pre_a;
+  pre.w = pre_w;
+  pre.res = pre_op == GSQ_PRE_ADD_RMSNORM ? res_out : nullptr;
+  pre.out = x_out;
+  pre.eps = eps;
+  DevTables tb;
+  int cus;
+  if (int rc = resolve(qt, &tb, &cus, static_cast<hipStream_t>(stream))) return rc;
+  hipError_t e = launch_qmv_pre(qt, static_cast<const uint8_t*>(packed), x, y, ydt, N, (int)K, pre, tb, cus,
+                                static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(GSQ_E_HIP, "qmv launch: %s", hipGetErrorString(e));
   return GSQ_OK;
 }

@@ -64,6 +64,22 @@ struct DevTables {
 // most ring items a wave issues per main-loop step, whether the activations may be staged in
 // LDS (else every wave reads its slices from global memory), and whether 2.5-slice rows may be
 // decoded two items at a time.
+// Fused activation prologue of a one-row fp16 QMV (gsq_qmv_pre): the kernel forms its input
+// row itself before the product.
+//   QMV_PRE_ADD_NORM: row = x (+ a), rounded to fp16, written to res (when given); input =
+//     round(row / rms(row) * w), written to out (when given). eps: the norm's epsilon.
+//   QMV_PRE_SWIGLU: x = [gate | up] (2K values); input = round(silu(gate) * up), written to out
+//     (when given).
+enum { QMV_PRE_NONE = 0, QMV_PRE_ADD_NORM = 1, QMV_PRE_SWIGLU = 2 };
+struct QmvPre {
+  int op = QMV_PRE_NONE;
+  const void* a = nullptr;
+  const void* w = nullptr;
+  void* res = nullptr;
+  void* out = nullptr;
+  float eps = 0.f;
+};
+
 struct QmvTuning {
   int waves;
   int inflight_bytes;

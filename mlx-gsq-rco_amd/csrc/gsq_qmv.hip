@@ -52,6 +52,7 @@ struct QmvArgs {
   int pair;         // items decoded in pairs (the PR variant of qmv_kernel)
   int tbl_bytes, x_off, x_bytes, x_lds, red_off, ring_off;  // LDS layout
   DevTables tb;
+  QmvPre pre;       // fused activation prologue (one fp16 row)
 };
 
 enum { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
@@ -786,6 +787,83 @@ struct QmvTblLds<0> {
   __device__ __forceinline__ static uint8_t* get() { return nullptr; }
 };
 
+// ---- fused activation prologue (one fp16 row, activations staged in LDS) ----------------
+__device__ __forceinline__ void h8_unpack(const uint4 q, float (&f)[8]) {
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = h2f(w[i] & 0xFFFFu);
+    f[2 * i + 1] = h2f(w[i] >> 16);
+  }
+}
+__device__ __forceinline__ uint4 h8_pack(const float (&f)[8]) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) w[i] = pack_h2(f[2 * i], f[2 * i + 1]);
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// Forms the kernel's input row in the LDS activation stage xst (K fp16 values), after the
+// prologue barrier, with the same arithmetic and roundings as the separate add + RMSNorm and
+// SwiGLU kernels; workgroup 0 also writes the row(s) the caller asked for. Chunk c of 8
+// values belongs to the same thread in every pass, so passes need no barrier between them
+// except the norm's sum. Ends with a barrier: every wave then reads its activations.
+__device__ __forceinline__ void qmv_pre(const QmvArgs& a, uint8_t* xst, float* red, int tid, int nt) {
+  const int nch = a.K >> 3;
+  uint4* xs = reinterpret_cast<uint4*>(xst);
+  const bool w0 = blockIdx.x == 0;
+  if (a.pre.op == QMV_PRE_SWIGLU) {
+    const uint4* gu = static_cast<const uint4*>(a.pre.a);  // gate (K values), then up (K)
+    for (int c = tid; c < nch; c += nt) {
+      float g[8], u[8], o[8];
+      h8_unpack(gu[c], g);
+      h8_unpack(gu[nch + c], u);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = g[e] / (1.f + expf(-g[e])) * u[e];
+      const uint4 r = h8_pack(o);
+      xs[c] = r;
+      if (w0 && a.pre.out) static_cast<uint4*>(a.pre.out)[c] = r;
+    }
+  } else {
+    const uint4* d = static_cast<const uint4*>(a.pre.a);
+    const uint4* w = static_cast<const uint4*>(a.pre.w);
+    const uint4 w_first = tid < nch ? w[tid] : make_uint4(0u, 0u, 0u, 0u);  // in flight during the sum
+    float ss = 0.f;
+    for (int c = tid; c < nch; c += nt) {
+      float v[8];
+      h8_unpack(xs[c], v);
+      if (d) {
+        float dv[8];
+        h8_unpack(d[c], dv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (float)(_Float16)(v[e] + dv[e]);  // stored rounded
+        xs[c] = h8_pack(v);
+      }
+      if (w0 && a.pre.res) static_cast<uint4*>(a.pre.res)[c] = h8_pack(v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    float tot = 0.f;
+    for (int i = 0; i < (nt >> 6); ++i) tot += red[i];
+    const float rinv = 1.f / sqrtf(tot / (float)a.K + a.pre.eps);
+    for (int c = tid; c < nch; c += nt) {
+      float v[8], wv[8], o[8];
+      h8_unpack(xs[c], v);
+      h8_unpack(c == tid ? w_first : w[c], wv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = v[e] * rinv * wv[e];
+      const uint4 r = h8_pack(o);
+      xs[c] = r;
+      if (w0 && a.pre.out) static_cast<uint4*>(a.pre.out)[c] = r;
+    }
+  }
+  __syncthreads();
+}
+
 // PR (one fp16 activation row, K = 5120: 20 superblocks = 2.5 slices per row, one wave per
 // row): the wave's items are decoded two at a time as five full slices instead of 2 x 3 with
 // half of every third slice idle: slices 0 and 1 of items t and t + 1, then one slice whose
@@ -831,7 +909,7 @@ __global__ void __launch_bounds__(qmv_max_threads(qmv_weight(MR, GL, XS))) qmv_k
   // stall in DMA issue (the CU's memory queue is full at kernel start) before its first item's
   // decode, and would put the first items of the waves behind it back.
   if constexpr (P::kLds > 0) dma_copy(a.tb.qmv_tbl, P::kLds, tbl, wave, nw, lane);
-  if (a.x_lds) dma_copy(a.x, a.x_bytes, xst, wave, nw, lane);
+  if (a.x_lds && a.pre.op != QMV_PRE_SWIGLU) dma_copy(a.x, a.x_bytes, xst, wave, nw, lane);
   int issued = 0;  // items issued so far (wave-uniform)
   if (nitems > 0) {
     dma_item(base, item_bytes, a.cdma, ring, lane);
@@ -839,6 +917,9 @@ __global__ void __launch_bounds__(qmv_max_threads(qmv_weight(MR, GL, XS))) qmv_k
   }
   wait_vmcnt(issued * a.cdma);  // this wave's share of the table and activations has landed
   __syncthreads();              // ... and every other wave's share
+  if constexpr (MR == 1 && !XS) {
+    if (a.pre.op != QMV_PRE_NONE) qmv_pre(a, xst, red, tid, blockDim.x);
+  }
 
   XReg<MR, XS, P::kSums> xr[GL];
 #pragma unroll
@@ -1090,9 +1171,13 @@ static int qmv_rows_per_launch(int xdt) { return xdt == DT_F16 ? 4 : 2; }
 // Launch plan for up to 4 activation rows: one workgroup of nw waves per CU, each owning about
 // N / #CU consecutive rows; W waves per row (ceil(slices / GL)), nw / W row slots.
 static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, int xdt, void* y, int ydt, int mr,
-                                  int M, int64_t N, int K, const DevTables& tb, int num_cus, hipStream_t s) {
+                                  int M, int64_t N, int K, const DevTables& tb, int num_cus, hipStream_t s,
+                                  const QmvPre& pre = QmvPre()) {
   QmvArgs a;
   a.packed = packed; a.x = x; a.y = y; a.N = N; a.K = K; a.M = M; a.x_dtype = xdt; a.y_dtype = ydt; a.tb = tb;
+  a.pre = pre;
+  const bool has_pre = pre.op != QMV_PRE_NONE;
+  if (has_pre && (M != 1 || xdt != DT_F16 || (K & 7))) return hipErrorInvalidValue;
   const int bb = block_bytes_of(qt);
   a.nblk = K / 256;
   a.row_bytes = a.nblk * bb;
@@ -1125,9 +1210,13 @@ static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, 
   const int item_bytes = (a.nblk < 8 * gl ? a.nblk : 8 * gl) * bb;
   a.cdma = (item_bytes + 19 + 1023) / 1024;
   a.sbuf = a.cdma * 1024;
-  const int red_bytes = (a.rows_per_wg * mr * a.W * 4 + 15) & ~15;
-  // activations go to LDS only if the ring keeps at least 3 items per wave
-  a.x_lds = (g_qmv_tuning.x_lds && a.tbl_bytes + a.x_bytes + red_bytes + nw * 3 * a.sbuf <= lds_cap) ? 1 : 0;
+  // row sums; the fused prologue also sums per wave there (16 floats)
+  int red_bytes = (a.rows_per_wg * mr * a.W * 4 + 15) & ~15;
+  if (has_pre && red_bytes < 64) red_bytes = 64;
+  // activations go to LDS only if the ring keeps at least 3 items per wave (always with a
+  // fused prologue, which forms them there)
+  a.x_lds = (has_pre || (g_qmv_tuning.x_lds && a.tbl_bytes + a.x_bytes + red_bytes + nw * 3 * a.sbuf <= lds_cap))
+                ? 1 : 0;
   a.x_off = a.tbl_bytes;
   a.red_off = a.x_off + (a.x_lds ? a.x_bytes : 0);
   a.ring_off = a.red_off + red_bytes;
@@ -1173,6 +1262,12 @@ static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, 
 }
 
 // y[M, N] = x[M, K] W^T: activation rows go out in launches of up to 4 (2 for fp32/bf16).
+// One fp16 activation row formed by a fused prologue (QmvPre) from x and the prologue's inputs.
+hipError_t launch_qmv_pre(int qt, const uint8_t* packed, const void* x, void* y, int ydt, int64_t N, int K,
+                          const QmvPre& pre, const DevTables& tb, int num_cus, hipStream_t s) {
+  return launch_qmv_rows(qt, packed, x, DT_F16, y, ydt, 1, 1, N, K, tb, num_cus, s, pre);
+}
+
 hipError_t launch_qmv(int qt, const uint8_t* packed, const void* x, int xdt, void* y, int ydt, int64_t M, int64_t N,
                       int K, const DevTables& tb, int num_cus, hipStream_t s) {
   // rows per launch: the widest variant whose waves per row (one per GL slices) fit a workgroup

@@ -32,7 +32,9 @@ single-token step can be captured once in a HIP graph and replayed (``GraphDecod
 
 On a GPU the residual adds + RMSNorms, the SwiGLU, each GatedDeltaNet token and each
 single-token attention run as fused libgsq.so kernels (runtime/kernels/model_ops.py); gate and
-up, qkv and z, q and k are one packed launch each where they share a quantization type. The torch
+up, qkv and z, q and k are one packed launch each where they share a quantization type. For
+one token of one sequence the norms and the SwiGLU go further, into the prologue of the packed
+projection that consumes them (``forward_pre``, libgsq ``gsq_qmv_pre``). The torch
 formulation below computes the same values and is what CPU tensors run (the structure test
 runs the model on the CPU with dense stand-ins for the packed layers).
 """
@@ -149,13 +151,19 @@ class GatedDeltaNet(torch.nn.Module):
         self.register_buffer("dt_bias", dt_bias.float())  # (Hv,)
         self.register_buffer("norm_w", norm_w)  # (head_v_dim,)
 
-    def forward(self, x, cache: Qwen35Cache):
+    @property
+    def first_proj(self):
+        """The projection of the layer input (its input norm can be fused into it)."""
+        return self.in_proj_qkvz
+
+    def forward(self, x, cache: Qwen35Cache, first=None):
+        """``first``: ``in_proj_qkvz(x)`` when the caller has computed it already."""
         a_ = self.args
         B, S, _ = x.shape
         hk, hv = a_.linear_num_key_heads, a_.linear_num_value_heads
         dk, dv = a_.linear_key_head_dim, a_.linear_value_head_dim
         kw = a_.linear_conv_kernel_dim
-        qkvz = self.in_proj_qkvz(x)
+        qkvz = self.in_proj_qkvz(x) if first is None else first
         qkv, z = qkvz[..., :a_.conv_dim], qkvz[..., a_.conv_dim:]   # (B, S, conv_dim), (B, S, Hv * dv)
         if x.is_cuda:  # the a / b projections happen inside the fused step
             from ..runtime.kernels import model_ops
@@ -228,11 +236,17 @@ class FullAttention(torch.nn.Module):
         xr = xr * cos + _rotate_half(xr) * sin
         return torch.cat([xr.to(x.dtype), x[..., rd:]], dim=-1)
 
-    def forward(self, x, cache: Qwen35Cache):
+    @property
+    def first_proj(self):
+        """The projection of the layer input (its input norm can be fused into it)."""
+        return self.qk_proj
+
+    def forward(self, x, cache: Qwen35Cache, first=None):
+        """``first``: ``qk_proj(x)`` when the caller has computed it already."""
         a_ = self.args
         B, S, _ = x.shape
         H, Hkv, hd = a_.num_attention_heads, a_.num_key_value_heads, a_.head_dim
-        qk = self.qk_proj(x)
+        qk = self.qk_proj(x) if first is None else first
         v = self.v_proj(x)
         if x.is_cuda and S == 1:
             from ..runtime.kernels import model_ops
@@ -265,11 +279,24 @@ class FullAttention(torch.nn.Module):
         return self.o_proj(out.to(x.dtype))
 
 
+def _can_pre(m) -> bool:
+    """Whether module m can form its input row itself (``forward_pre``)."""
+    return hasattr(m, "forward_pre") and getattr(m, "pre_ok", True)
+
+
+def _fused_row(x, *mods) -> bool:
+    """One fp16 row on a GPU, through modules that can form their input row themselves."""
+    return x.is_cuda and x.dtype == torch.float16 and x.shape[0] * x.shape[1] == 1 and all(map(_can_pre, mods))
+
+
 class Qwen35Layer(torch.nn.Module):
     """Pre-norm mixer and SwiGLU MLP. ``forward(x, delta, cache)`` first adds the previous
-    layer's pending MLP output ``delta`` into the residual stream ``x`` (in place, fused with
-    this layer's input norm) and returns this layer's MLP output, to be added the same way by
-    the next layer or the final norm."""
+    layer's pending MLP output ``delta`` into the residual stream ``x`` (fused with this layer's
+    input norm) and returns ``(x, m)``: the residual stream and this layer's MLP output, to be
+    added the same way by the next layer or the final norm. The residual stream is ``x`` itself,
+    updated in place, except for one fp16 row on a GPU with packed projections: there the norms
+    and the SwiGLU run inside the projections that consume them (``forward_pre``), which write
+    the updated stream to a new buffer (other workgroups of the launch still read ``x``)."""
 
     def __init__(self, args, mixer, input_norm_w, post_norm_w, gate_up, down):
         super().__init__()
@@ -280,6 +307,15 @@ class Qwen35Layer(torch.nn.Module):
 
     def forward(self, x, delta, cache):
         eps = self.args.rms_norm_eps
+        if _fused_row(x, self.mixer.first_proj, self.gate_up, self.down):
+            h = torch.empty_like(x)                 # the normalized layer input
+            x1 = x if delta is None else torch.empty_like(x)
+            first = self.mixer.first_proj.forward_pre(x, "add_rms_norm", pre_a=delta, pre_w=self.input_norm_w,
+                                                      eps=eps, res_out=None if delta is None else x1, x_out=h)
+            m = self.mixer(h, cache, first=first)
+            x2 = torch.empty_like(x)
+            gu = self.gate_up.forward_pre(x1, "add_rms_norm", pre_a=m, pre_w=self.post_norm_w, eps=eps, res_out=x2)
+            return x2, self.down.forward_pre(gu, "swiglu")
         m = self.mixer(add_rms_norm(x, delta, self.input_norm_w, eps), cache)
         gu = self.gate_up(add_rms_norm(x, m, self.post_norm_w, eps))
         if gu.is_cuda:
@@ -288,7 +324,7 @@ class Qwen35Layer(torch.nn.Module):
         else:
             g, u = gu.split(gu.shape[-1] // 2, dim=-1)
             act = (F.silu(g.float()) * u.float()).to(gu.dtype)
-        return self.down(act)
+        return x, self.down(act)
 
 
 class Qwen35Model(torch.nn.Module):
@@ -311,8 +347,12 @@ class Qwen35Model(torch.nn.Module):
         x = self.embed(ids).to(self.dtype).reshape(B, S, -1).contiguous()
         delta = None
         for layer in self.layers:
-            delta = layer(x, delta, cache)
-        logits = self.lm_head(add_rms_norm(x, delta, self.norm_w, self.args.rms_norm_eps))
+            x, delta = layer(x, delta, cache)
+        eps = self.args.rms_norm_eps
+        if _fused_row(x, self.lm_head):
+            logits = self.lm_head.forward_pre(x, "add_rms_norm", pre_a=delta, pre_w=self.norm_w, eps=eps)
+        else:
+            logits = self.lm_head(add_rms_norm(x, delta, self.norm_w, eps))
         cache.pos.add_(S)
         cache.length += S
         return logits
@@ -327,6 +367,16 @@ class _SideBySide(torch.nn.Module):
 
     def forward(self, x):
         return torch.cat([m(x) for m in self.mods], dim=-1)
+
+    @property
+    def pre_ok(self) -> bool:
+        return all(map(_can_pre, self.mods))
+
+    def forward_pre(self, x, pre, x_out=None, **kw):
+        """The first projection forms the row (and writes it to ``x_out``); the others read it."""
+        h = x.new_empty(x.shape[:-1] + (self.mods[0].in_features,)) if x_out is None else x_out
+        first = self.mods[0].forward_pre(x, pre, x_out=h, **kw)
+        return torch.cat([first] + [m(h) for m in self.mods[1:]], dim=-1)
 
 
 def build_qwen35(store, dtype=torch.float16, args: Qwen35Args | None = None, linear=None, embedding=None,

@@ -15,7 +15,7 @@ from __future__ import annotations
 import torch
 
 from ..runtime.kernels.qmm import QMM_MIN_ROWS, quantized_matmul
-from ..runtime.kernels.qmv import quantized_matvec
+from ..runtime.kernels.qmv import quantized_matvec, quantized_matvec_pre
 
 
 def _apply(x, packed, qtype, out_features, in_features):
@@ -36,6 +36,13 @@ class GSQLinear(torch.nn.Module):
 
     def forward(self, x):
         y = _apply(x, self.packed_weight, self.qtype, self.out_features, self.in_features)
+        return y if self.bias is None else y + self.bias
+
+    def forward_pre(self, x, pre, **kw):
+        """The product of one fp16 row the kernel forms itself from ``x`` (``pre`` =
+        "add_rms_norm" or "swiglu", keywords as ``quantized_matvec_pre``)."""
+        y = quantized_matvec_pre(x, self.packed_weight, qtype=self.qtype, out_features=self.out_features,
+                                 in_features=self.in_features, pre=pre, **kw)
         return y if self.bias is None else y + self.bias
 
     def extra_repr(self) -> str:
@@ -76,7 +83,16 @@ class GSQFusedLinear(torch.nn.Module):
         self.biases = biases
 
     def forward(self, x):
-        y = _apply(x, self.packed_weight, self.qtype, self.out_features, self.in_features)
+        return self._outputs(_apply(x, self.packed_weight, self.qtype, self.out_features, self.in_features))
+
+    def forward_pre(self, x, pre, **kw):
+        """As ``forward``, on one fp16 row the kernel forms itself from ``x`` (``pre`` =
+        "add_rms_norm" or "swiglu", keywords as ``quantized_matvec_pre``)."""
+        return self._outputs(quantized_matvec_pre(x, self.packed_weight, qtype=self.qtype,
+                                                  out_features=self.out_features, in_features=self.in_features,
+                                                  pre=pre, **kw))
+
+    def _outputs(self, y):
         if self.concat:  # one tensor of the concatenated outputs
             if self.biases is not None:
                 y = y + torch.cat([torch.zeros(n, dtype=y.dtype, device=y.device) if b is None else b

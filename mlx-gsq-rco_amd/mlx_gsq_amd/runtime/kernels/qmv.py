@@ -16,7 +16,7 @@ from ...gguf.parser import GGMLQuantizationType, QUANT_BLOCK_SIZES
 from .qmm import QMM_MIN_ROWS, quantized_matmul
 
 
-def _validate(x, packed, qtype, out_features, in_features):
+def _validate_width(packed, qtype, out_features, in_features):
     type_id = int(GGMLQuantizationType[qtype])  # KeyError for unknown names, as qmv.py:540
     block_elements, block_bytes = QUANT_BLOCK_SIZES[type_id]
     if block_elements != 256 or in_features % 256:
@@ -24,6 +24,10 @@ def _validate(x, packed, qtype, out_features, in_features):
     expected = out_features * (in_features // 256) * block_bytes
     if packed.numel() != expected:
         raise ValueError(f"packed size {packed.numel()} != expected {expected}")
+
+
+def _validate(x, packed, qtype, out_features, in_features):
+    _validate_width(packed, qtype, out_features, in_features)
     if x.shape[-1] != in_features:
         raise ValueError("input feature size mismatch")
 
@@ -84,3 +88,56 @@ def quantized_matvec(x, packed, *, qtype: str, out_features: int, in_features: i
                                           rows, out_features, in_features, _lib.stream_handle(x.device)),
                        "quantized_matvec")
     return y.reshape(*original, out_features)
+
+
+PRE_OPS = {"add_rms_norm": 1, "swiglu": 2}  # GSQ_PRE_ADD_RMSNORM, GSQ_PRE_SWIGLU
+
+
+def quantized_matvec_pre(x, packed, *, qtype: str, out_features: int, in_features: int, pre: str, pre_a=None,
+                         pre_w=None, eps: float = 0.0, res_out=None, x_out=None, out_dtype=None):
+    """y = row @ W.T for one fp16 activation row that the QMV kernel forms itself (libgsq
+    ``gsq_qmv_pre``; no counterpart in the reference, whose model runs these as separate
+    operations):
+
+    * ``pre="add_rms_norm"``: ``s = x + pre_a`` (``pre_a`` may be None), rounded to fp16 and
+      written to ``res_out`` when given (a different buffer from ``x`` and ``pre_a``); ``row =
+      rms_norm(s) * pre_w`` with ``eps``, as ``model_ops.add_rms_norm`` computes it;
+    * ``pre="swiglu"``: ``x`` holds ``[gate | up]`` (``2 * in_features`` values); ``row =
+      silu(gate) * up``, as ``model_ops.swiglu`` computes it.
+
+    The row is also written to ``x_out`` when given. ``x`` and the vectors are fp16 and hold
+    exactly one row (any leading shape of size 1); the result has shape ``x.shape[:-1] +
+    (out_features,)``.
+    """
+    if pre not in PRE_OPS:
+        raise ValueError(f"unknown pre op {pre!r}")
+    _validate_width(packed, qtype, out_features, in_features)
+    if qtype not in QTYPES:
+        raise KeyError(qtype)
+    _check_tensors(x, packed)
+    width = 2 * in_features if pre == "swiglu" else in_features
+    if x.dtype != torch.float16 or x.shape[-1] != width or x.numel() != width:
+        raise ValueError(f"x must be one fp16 row of {width} values")
+    for name, t in (("pre_a", pre_a), ("pre_w", pre_w), ("res_out", res_out), ("x_out", x_out)):
+        if t is None:
+            continue
+        if t.dtype != torch.float16 or t.numel() != in_features or not t.is_contiguous() or t.device != x.device:
+            raise ValueError(f"{name} must be a contiguous fp16 vector of {in_features} values on x's device")
+    if pre == "add_rms_norm" and pre_w is None:
+        raise ValueError("add_rms_norm needs the norm weight pre_w")
+    odt = out_dtype or x.dtype
+    flat = x.contiguous()
+    packed = packed.contiguous()
+    y = torch.empty(x.shape[:-1] + (out_features,), dtype=odt, device=x.device)
+
+    def ptr(t):
+        return None if t is None else t.data_ptr()
+    _lib.ensure_tables(qtype, x.device)
+    with torch.cuda.device(x.device):
+        _lib.check(_lib.lib().gsq_qmv_pre(TYPE_IDS[qtype], packed.data_ptr(), PRE_OPS[pre], flat.data_ptr(),
+                                          ptr(pre_a), ptr(pre_w), float(eps), ptr(res_out), ptr(x_out), y.data_ptr(),
+                                          _lib.DTYPE_CODES[odt], out_features, in_features,
+                                          _lib.stream_handle(x.device)),
+                   "quantized_matvec_pre")
+    return y
+

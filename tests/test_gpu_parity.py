@@ -364,6 +364,45 @@ def test_fused_linear_matches_separate_projections(rows):
         assert rel_l2(o.cpu().numpy(), want) <= 1e-3
 
 
+@pytest.mark.parametrize("qtype", ["IQ2_S", "IQ2_XS", "IQ1_M", "Q4_K", "Q6_K"])
+def test_qmv_pre_matches_separate_kernels(qtype):
+    """gsq_qmv_pre: the residual add + RMSNorm (K = 5120) and the SwiGLU (K = 17408) formed in
+    the QMV prologue against the separate kernels (the residual bit for bit, the row within one
+    fp16 rounding: the norm's sum runs in another order), the product on the row it wrote bit
+    for bit against the plain QMV and within tolerance against the oracle."""
+    from mlx_gsq_amd.runtime.kernels import model_ops
+    from mlx_gsq_amd.runtime.kernels.qmv import quantized_matvec, quantized_matvec_pre
+    g = torch.Generator().manual_seed(11)
+    for pre, n, k in (("add_rms_norm", 1536, 5120), ("swiglu", 1024, 17408)):
+        packed = synth.make_packed(qtype, n, k, seed=5)
+        pd = dev(packed)
+        kw = dict(qtype=qtype, out_features=n, in_features=k, out_dtype=torch.float32)
+        row = torch.empty(1, k, dtype=torch.float16, device="cuda")
+        if pre == "add_rms_norm":
+            x = torch.randn(1, k, generator=g).half().cuda()
+            d = torch.randn(1, k, generator=g).half().cuda()
+            w = (1 + 0.1 * torch.randn(k, generator=g)).half().cuda()
+            res = torch.empty_like(x)
+            y = quantized_matvec_pre(x, pd, pre=pre, pre_a=d, pre_w=w, eps=1e-6, res_out=res, x_out=row, **kw)
+            xs = x.clone()
+            want_row = model_ops.add_rms_norm(xs, d, w, 1e-6)
+            assert torch.equal(res, xs)
+            with pytest.raises(ValueError):  # the residual must go to a new buffer
+                quantized_matvec_pre(x, pd, pre=pre, pre_a=d, pre_w=w, eps=1e-6, res_out=x, **kw)
+            # without the add and without outputs asked for
+            y0 = quantized_matvec_pre(x, pd, pre=pre, pre_w=w, eps=1e-6, **kw)
+            row0 = model_ops.add_rms_norm(x.clone(), None, w, 1e-6)
+            assert rel_l2(y0.cpu().numpy(), quantized_matvec(row0, pd, **kw).cpu().numpy()) <= 1e-3
+        else:
+            x = torch.randn(1, 2 * k, generator=g).half().cuda()
+            y = quantized_matvec_pre(x, pd, pre=pre, x_out=row, **kw)
+            want_row = model_ops.swiglu(x)
+        assert torch.allclose(row.float(), want_row.float(), rtol=1e-3, atol=1e-6), pre
+        assert torch.equal(y, quantized_matvec(row, pd, **kw)), pre
+        ref = O.matmul_reference(row.float().cpu().numpy(), packed, qtype, n, k, TABLES.get(qtype))
+        assert rel_l2(y.cpu().numpy(), ref) <= 1e-3, pre
+
+
 @pytest.mark.parametrize("rows", [1, 3])
 def test_grouped_linear_mixed_types(rows):
     """q/k/v with mixed types (IQ2_XS, IQ2_XS, IQ4_XS) as one group: every output equals the

@@ -80,11 +80,16 @@ int gsq_qmv(int qtype_id, const void* packed, const void* x, int x_dtype, void* 
  *   GSQ_PRE_SWIGLU: x holds [gate | up] (2K values); row = round(silu(gate) * up), as
  *     gsq_swiglu computes it (pre_a, pre_w, eps, res_out unused).
  * The row is written to x_out when not NULL. All vectors fp16, 16-byte aligned; K a multiple
- * of 8 up to 32768. */
+ * of 8 up to 32768. With conv_rows > 0 (fp16 y), output rows r < conv_rows also run a
+ * depthwise causal convolution (the GatedDeltaNet's, of the qkv rows of its input projection):
+ * state conv_state [conv_kernel - 1, conv_rows] fp16 shifted in place with the new input
+ * round(y[r]), weights conv_w [conv_rows, conv_kernel] fp16, conv_out[r] = silu(sum) in float32,
+ * as gsq_gdn_step's convolution computes it (pass its conv_state as NULL afterwards). */
 #define GSQ_PRE_ADD_RMSNORM 1
 #define GSQ_PRE_SWIGLU 2
 int gsq_qmv_pre(int qtype_id, const void* packed, int pre_op, const void* x, const void* pre_a, const void* pre_w,
-                float eps, void* res_out, void* x_out, void* y, int y_dtype, int64_t N, int64_t K, void* stream);
+                float eps, void* res_out, void* x_out, void* y, int y_dtype, int64_t N, int64_t K, void* conv_state,
+                const void* conv_w, int64_t conv_rows, int64_t conv_kernel, float* conv_out, void* stream);
 
 /* Same product with the tiled MFMA kernel (prefill, large M). Replaces quantized_matmul
  * (mlx_gsq/runtime/kernels/qmm.py:559-594). Workgroups that share an output tile exchange
@@ -144,7 +149,9 @@ int gsq_swiglu(const void* gate_up, void* out, int64_t rows, int64_t n, int dtyp
  * [batch, value_heads, head_k_dim, head_v_dim] updated in place (S = decay S; S += k (beta (v -
  * S^T k))^T) and o = S^T q; out = round(o / rms(o) * norm_w * silu(z)) with eps over each
  * head's head_v_dim values. Strides are in elements between batch rows. head_k_dim a multiple
- * of 4 up to 128, head_v_dim 64..256 in steps of 64, conv_kernel 2..8. */
+ * of 4 up to 128, head_v_dim 64..256 in steps of 64, conv_kernel 2..8. conv_state NULL: the
+ * convolution has run already (gsq_qmv_pre's epilogue) and `work` holds its outputs; qkv and
+ * conv_w are then not read. */
 int gsq_gdn_step(const void* qkv, int64_t qkv_stride, const void* z, int64_t z_stride, const void* x,
                  int64_t x_stride, const void* w_ab, int64_t hidden, void* conv_state, const void* conv_w,
                  const float* ssm_a, const float* dt_bias, float* rec_state, const void* norm_w, void* out,

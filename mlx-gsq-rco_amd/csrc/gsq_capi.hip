@@ -357,9 +357,16 @@ int gsq_qmv(int qt, const void* packed, const void* x, int xdt, void* y, int ydt
 }
 
 int gsq_qmv_pre(int qt, const void* packed, int pre_op, const void* x, const void* pre_a, const void* pre_w,
-                float eps, void* res_out, void* x_out, void* y, int ydt, int64_t N, int64_t K, void* stream) {
+                float eps, void* res_out, void* x_out, void* y, int ydt, int64_t N, int64_t K, void* conv_state,
+                const void* conv_w, int64_t conv_rows, int64_t conv_kernel, float* conv_out, void* stream) {
   if (int rc = check_common(qt, packed, 1, N, K, GSQ_F16, ydt)) return rc;
   if (pre_op != GSQ_PRE_ADD_RMSNORM && pre_op != GSQ_PRE_SWIGLU) return fail(GSQ_E_VALUE, "unknown pre_op %d", pre_op);
+  if (conv_rows < 0 || conv_rows > N) return fail(GSQ_E_VALUE, "conv_rows must be 0..N");
+  if (conv_rows > 0) {
+    if (!conv_state || !conv_w || !conv_out) return fail(GSQ_E_VALUE, "convolution pointer is NULL");
+    if (conv_kernel < 2 || conv_kernel > 8) return fail(GSQ_E_VALUE, "convolution kernel must be 2..8");
+    if (ydt != GSQ_F16) return fail(GSQ_E_VALUE, "the convolution epilogue needs fp16 y");
+  }
   if (!x || !y) return fail(GSQ_E_VALUE, "NULL pointer");
   if (pre_op == GSQ_PRE_ADD_RMSNORM && !pre_w) return fail(GSQ_E_VALUE, "the norm weight is NULL");
   if (pre_op == GSQ_PRE_ADD_RMSNORM && !(eps >= 0.f)) return fail(GSQ_E_VALUE, "eps must be >= 0");
@@ -376,6 +383,13 @@ int gsq_qmv_pre(int qt, const void* packed, int pre_op, const void* x, const voi
   pre.res = pre_op == GSQ_PRE_ADD_RMSNORM ? res_out : nullptr;
   pre.out = x_out;
   pre.eps = eps;
+  if (conv_rows > 0) {
+    pre.conv_state = conv_state;
+    pre.conv_w = conv_w;
+    pre.conv_out = conv_out;
+    pre.conv_rows = (int)conv_rows;
+    pre.conv_k = (int)conv_kernel;
+  }
   DevTables tb;
   int cus;
   if (int rc = resolve(qt, &tb, &cus, static_cast<hipStream_t>(stream))) return rc;
@@ -484,8 +498,9 @@ int gsq_gdn_step(const void* qkv, int64_t qkv_stride, const void* z, int64_t z_s
   if (head_v_dim <= 0 || head_v_dim % 64 || head_v_dim > 256) return fail(GSQ_E_VALUE, "value head dim must be 64, 128, 192 or 256");
   if (conv_kernel < 2 || conv_kernel > 8) return fail(GSQ_E_VALUE, "convolution kernel must be 2..8");
   if (hidden <= 0 || hidden >= (1ll << 30)) return fail(GSQ_E_VALUE, "invalid hidden size");
-  if (!qkv || !z || !x || !w_ab || !conv_state || !conv_w || !ssm_a || !dt_bias || !rec_state || !norm_w || !out || !work)
+  if (!z || !x || !w_ab || !ssm_a || !dt_bias || !rec_state || !norm_w || !out || !work)
     return fail(GSQ_E_VALUE, "NULL pointer");
+  if (conv_state && (!qkv || !conv_w)) return fail(GSQ_E_VALUE, "NULL pointer");
   if (!(eps >= 0.f)) return fail(GSQ_E_VALUE, "eps must be >= 0");
   GdnArgs a;
   a.qkv = qkv; a.z = z; a.x = x; a.w_ab = w_ab; a.conv = conv_state; a.conv_w = conv_w; a.ssm_a = ssm_a;

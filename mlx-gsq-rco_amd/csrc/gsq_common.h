@@ -78,6 +78,14 @@ struct QmvPre {
   void* res = nullptr;
   void* out = nullptr;
   float eps = 0.f;
+  // convolution epilogue (conv_rows > 0): output rows r < conv_rows are the channels of a
+  // depthwise causal convolution of kernel conv_k with state conv_state [conv_k - 1, conv_rows]
+  // (fp16, shifted in place) and weights conv_w [conv_rows, conv_k] (fp16); conv_out[r] =
+  // silu(convolution) in fp32. The row's fp16 output is the convolution's new input.
+  void* conv_state = nullptr;
+  const void* conv_w = nullptr;
+  float* conv_out = nullptr;
+  int conv_rows = 0, conv_k = 0;
 };
 
 struct QmvTuning {

@@ -514,14 +514,16 @@ hipError_t launch_gdn_step(int dt, const GdnArgs& a, hipStream_t s) {
   const int conv_dim = 2 * a.Hk * a.dk + a.Hv * a.dv;
   const dim3 cgrid((unsigned)((conv_dim + 255) / 256), (unsigned)a.B), rgrid((unsigned)a.Hv, (unsigned)a.B);
   const dim3 rblock((unsigned)(kGdnRowGroups * a.dv));
+  // without a convolution state, `work` already holds the convolution outputs
+  const bool conv = a.conv != nullptr;
   if (dt == MD_F16) {
-    hipLaunchKernelGGL(gdn_conv_kernel<MD_F16>, cgrid, dim3(256), 0, s, a);
+    if (conv) hipLaunchKernelGGL(gdn_conv_kernel<MD_F16>, cgrid, dim3(256), 0, s, a);
     hipLaunchKernelGGL(gdn_rec_kernel<MD_F16>, rgrid, rblock, 0, s, a);
   } else if (dt == MD_BF16) {
-    hipLaunchKernelGGL(gdn_conv_kernel<MD_BF16>, cgrid, dim3(256), 0, s, a);
+    if (conv) hipLaunchKernelGGL(gdn_conv_kernel<MD_BF16>, cgrid, dim3(256), 0, s, a);
     hipLaunchKernelGGL(gdn_rec_kernel<MD_BF16>, rgrid, rblock, 0, s, a);
   } else {
-    hipLaunchKernelGGL(gdn_conv_kernel<MD_F32>, cgrid, dim3(256), 0, s, a);
+    if (conv) hipLaunchKernelGGL(gdn_conv_kernel<MD_F32>, cgrid, dim3(256), 0, s, a);
     hipLaunchKernelGGL(gdn_rec_kernel<MD_F32>, rgrid, rblock, 0, s, a);
   }
   return hipGetLastError();

@@ -51,6 +51,7 @@ struct QmvArgs {
   int fill;         // most ring items issued per main-loop step (per item pair: 2 x fill)
   int pair;         // items decoded in pairs (the PR variant of qmv_kernel)
   int tbl_bytes, x_off, x_bytes, x_lds, red_off, ring_off;  // LDS layout
+  int conv_lds, conv_off;  // prefetched convolution inputs (16 bytes per row of the workgroup)
   DevTables tb;
   QmvPre pre;       // fused activation prologue (one fp16 row)
 };
@@ -864,14 +865,59 @@ __device__ __forceinline__ void qmv_pre(const QmvArgs& a, uint8_t* xst, float* r
   __syncthreads();
 }
 
+// Convolution inputs of the workgroup's rows (kernel 4, the model's), fetched in the prologue
+// into LDS (16 bytes per row: the 3 cached inputs and the 4 weights, fp16) so that the epilogue
+// does not wait for memory; through LDS, not registers, which the main loop needs.
+__device__ __forceinline__ void qmv_conv_prefetch(const QmvArgs& a, int64_t r, uint4& v) {
+  const QmvPre& p = a.pre;
+  const uint16_t* st = static_cast<const uint16_t*>(p.conv_state) + r;
+  const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.conv_w) + r * 4);
+  v = make_uint4((uint32_t)st[0] | ((uint32_t)st[p.conv_rows] << 16), st[2 * (int64_t)p.conv_rows], w.x, w.y);
+}
+
+// Convolution epilogue of output row r (QmvPre conv_*), after its fp16 output y was formed: the
+// arithmetic of the separate GatedDeltaNet convolution kernel, for one channel. cp: the row's
+// prefetched inputs, or null.
+__device__ __forceinline__ void qmv_post_conv(const QmvArgs& a, int64_t r, float y, const uint4* cp) {
+  const QmvPre& p = a.pre;
+  const int C = p.conv_rows, K = p.conv_k;
+  _Float16* st = static_cast<_Float16*>(p.conv_state) + r;
+  const _Float16* w = static_cast<const _Float16*>(p.conv_w) + r * K;
+  float in[8], wf[8];  // the window: K - 1 cached inputs, then the new one (static indices only)
+  if (cp) {
+    const uint4 c = *cp;
+    in[0] = h2f(c.x & 0xFFFFu); in[1] = h2f(c.x >> 16); in[2] = h2f(c.y); in[3] = (float)(_Float16)y;
+    wf[0] = h2f(c.z & 0xFFFFu); wf[1] = h2f(c.z >> 16); wf[2] = h2f(c.w & 0xFFFFu); wf[3] = h2f(c.w >> 16);
+#pragma unroll
+    for (int t = 4; t < 8; ++t) in[t] = wf[t] = 0.f;
+  } else {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      in[t] = t < K - 1 ? (float)st[(int64_t)t * C] : (t == K - 1 ? (float)(_Float16)y : 0.f);
+      wf[t] = t < K ? (float)w[t] : 0.f;
+    }
+  }
+  float acc = in[0] * wf[0];
+#pragma unroll
+  for (int t = 1; t < 8; ++t)
+    if (t < K) acc = acc + in[t] * wf[t];
+#pragma unroll
+  for (int t = 0; t + 1 < 8; ++t)
+    if (t < K - 1) st[(int64_t)t * C] = (_Float16)in[t + 1];
+  p.conv_out[r] = acc / (1.f + expf(-acc));
+}
+
 // PR (one fp16 activation row, K = 5120: 20 superblocks = 2.5 slices per row, one wave per
 // row): the wave's items are decoded two at a time as five full slices instead of 2 x 3 with
 // half of every third slice idle: slices 0 and 1 of items t and t + 1, then one slice whose
 // lanes 0-31 take item t's last 4 superblocks and lanes 32-63 item t + 1's. Both rows use the
 // same activations, so that slice's activations are those of groups 128 + lane % 32. Items
 // stay one row each in the ring (separate buffers).
-template <int T, int MR, bool XS, int GL, bool A4, bool PR = false>
+// PRE: the variant with the fused activation prologue and convolution epilogue (QmvPre; one
+// fp16 row), a separate instantiation so that the plain kernels carry none of its code.
+template <int T, int MR, bool XS, int GL, bool A4, bool PR = false, bool PRE = false>
 __global__ void __launch_bounds__(qmv_max_threads(qmv_weight(MR, GL, XS))) qmv_kernel(QmvArgs a) {
+  static_assert(!PRE || (MR == 1 && !XS), "the fused prologue takes one fp16 row");
   using P = Qmv<T>;
   constexpr int BB = BlockBytes<T>::v;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -909,15 +955,21 @@ __global__ void __launch_bounds__(qmv_max_threads(qmv_weight(MR, GL, XS))) qmv_k
   // stall in DMA issue (the CU's memory queue is full at kernel start) before its first item's
   // decode, and would put the first items of the waves behind it back.
   if constexpr (P::kLds > 0) dma_copy(a.tb.qmv_tbl, P::kLds, tbl, wave, nw, lane);
-  if (a.x_lds && a.pre.op != QMV_PRE_SWIGLU) dma_copy(a.x, a.x_bytes, xst, wave, nw, lane);
+  if (a.x_lds && !(PRE && a.pre.op == QMV_PRE_SWIGLU)) dma_copy(a.x, a.x_bytes, xst, wave, nw, lane);
+  // a convolution epilogue's inputs of row r0 + tid (loads before the first item, so that the
+  // prologue's wait covers them and the DMA wait counts stay exact; into LDS after it)
+  uint4 cpv;
+  const bool cpf = PRE && a.conv_lds && tid < (int)(r1 - r0) && r0 + tid < a.pre.conv_rows;
+  if (cpf) qmv_conv_prefetch(a, r0 + tid, cpv);
   int issued = 0;  // items issued so far (wave-uniform)
   if (nitems > 0) {
     dma_item(base, item_bytes, a.cdma, ring, lane);
     issued = 1;
   }
   wait_vmcnt(issued * a.cdma);  // this wave's share of the table and activations has landed
+  if (cpf) reinterpret_cast<uint4*>(dyn + a.conv_off)[tid] = cpv;
   __syncthreads();              // ... and every other wave's share
-  if constexpr (MR == 1 && !XS) {
+  if constexpr (PRE) {
     if (a.pre.op != QMV_PRE_NONE) qmv_pre(a, xst, red, tid, blockDim.x);
   }
 
@@ -1023,13 +1075,19 @@ __global__ void __launch_bounds__(qmv_max_threads(qmv_weight(MR, GL, XS))) qmv_k
       for (int w = 0; w < a.W; ++w) v += red[o * a.W + w];
       const int rl = o / MR, m = o - rl * MR;
       if (m < a.M) store_y(a.y, a.y_dtype, (int64_t)m * a.N + r0 + rl, v);
+      if constexpr (PRE) {
+        if (r0 + rl < a.pre.conv_rows)
+          qmv_post_conv(a, r0 + rl, v,  // row rl was prefetched by thread rl
+                        a.conv_lds && rl < (int)blockDim.x ? reinterpret_cast<const uint4*>(dyn + a.conv_off) + rl
+                                                           : nullptr);
+      }
     }
   }
 }
 
-template <int T, int MR, bool XS, int GL, bool A4, bool PR = false>
+template <int T, int MR, bool XS, int GL, bool A4, bool PR = false, bool PRE = false>
 static hipError_t launch_qmv_t(const QmvArgs& a, int grid, int threads, size_t lds, hipStream_t s) {
-  auto k = qmv_kernel<T, MR, XS, GL, A4, PR>;
+  auto k = qmv_kernel<T, MR, XS, GL, A4, PR, PRE>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -1057,6 +1115,11 @@ static int qmv_gl(int mr, bool xs) {
 template <int T, bool A4>
 static hipError_t launch_qmv_variant(const QmvArgs& a, int mr, bool xs, int gl, int grid, int threads, size_t lds,
                                      hipStream_t s) {
+  if (a.pre.op != QMV_PRE_NONE || a.pre.conv_rows > 0) {  // one fp16 row (checked by the plan)
+    if (gl == 1) return launch_qmv_t<T, 1, false, 1, A4, false, true>(a, grid, threads, lds, s);
+    if (a.pair) return launch_qmv_t<T, 1, false, 3, A4, true, true>(a, grid, threads, lds, s);
+    return launch_qmv_t<T, 1, false, 3, A4, false, true>(a, grid, threads, lds, s);
+  }
   if (mr == 1 && !xs && gl == 1) return launch_qmv_t<T, 1, false, 1, A4>(a, grid, threads, lds, s);
   if (mr == 1 && !xs && a.pair) return launch_qmv_t<T, 1, false, 3, A4, true>(a, grid, threads, lds, s);
   if (mr == 1) return xs ? launch_qmv_t<T, 1, true, 1, A4>(a, grid, threads, lds, s) : launch_qmv_t<T, 1, false, 3, A4>(a, grid, threads, lds, s);
@@ -1178,6 +1241,9 @@ static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, 
   a.pre = pre;
   const bool has_pre = pre.op != QMV_PRE_NONE;
   if (has_pre && (M != 1 || xdt != DT_F16 || (K & 7))) return hipErrorInvalidValue;
+  if (pre.conv_rows > 0 && (M != 1 || xdt != DT_F16 || ydt != DT_F16 || pre.conv_rows > N || pre.conv_k < 2 ||
+                            pre.conv_k > 8))
+    return hipErrorInvalidValue;
   const int bb = block_bytes_of(qt);
   a.nblk = K / 256;
   a.row_bytes = a.nblk * bb;
@@ -1219,7 +1285,10 @@ static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, 
                 ? 1 : 0;
   a.x_off = a.tbl_bytes;
   a.red_off = a.x_off + (a.x_lds ? a.x_bytes : 0);
-  a.ring_off = a.red_off + red_bytes;
+  // kernel-4 convolution epilogue: every row of a workgroup is one thread's to prefetch
+  a.conv_lds = (pre.conv_rows > 0 && pre.conv_k == 4) ? 1 : 0;
+  a.conv_off = a.red_off + red_bytes;
+  a.ring_off = a.conv_off + (a.conv_lds ? a.rows_per_wg * 16 : 0);
   int nb = (lds_cap - a.ring_off) / (nw * a.sbuf);
   // large items: fewer waves rather than a ring of one buffer
   while (nb < 2 && nw > a.W) {

@@ -156,13 +156,26 @@ class GatedDeltaNet(torch.nn.Module):
         """The projection of the layer input (its input norm can be fused into it)."""
         return self.in_proj_qkvz
 
+    def first_pre(self, x, cache: Qwen35Cache, **kw):
+        """in_proj_qkvz of the row its prologue forms from x (``forward_pre`` keywords), with the
+        convolution of the qkv rows in its epilogue: returns (qkvz, convolution outputs), the
+        ``first`` of ``forward``."""
+        work = torch.empty(1, self.args.conv_dim, dtype=torch.float32, device=x.device)
+        qkvz = self.in_proj_qkvz.forward_pre(x, "add_rms_norm", conv=(cache.conv[self.layer], self.conv_w, work),
+                                             **kw)
+        return qkvz, work
+
     def forward(self, x, cache: Qwen35Cache, first=None):
-        """``first``: ``in_proj_qkvz(x)`` when the caller has computed it already."""
+        """``first``: ``in_proj_qkvz(x)`` when the caller has computed it already, or
+        ``first_pre``'s (qkvz, convolution outputs)."""
         a_ = self.args
         B, S, _ = x.shape
         hk, hv = a_.linear_num_key_heads, a_.linear_num_value_heads
         dk, dv = a_.linear_key_head_dim, a_.linear_value_head_dim
         kw = a_.linear_conv_kernel_dim
+        conv_out = None
+        if isinstance(first, tuple):
+            first, conv_out = first
         qkvz = self.in_proj_qkvz(x) if first is None else first
         qkv, z = qkvz[..., :a_.conv_dim], qkvz[..., a_.conv_dim:]   # (B, S, conv_dim), (B, S, Hv * dv)
         if x.is_cuda:  # the a / b projections happen inside the fused step
@@ -170,7 +183,7 @@ class GatedDeltaNet(torch.nn.Module):
             outs = [model_ops.gdn_step(qkv[:, t], z[:, t], x[:, t], self.w_ab, cache.conv[self.layer], self.conv_w,
                                        self.ssm_a, self.dt_bias, cache.rec[self.layer], self.norm_w,
                                        key_heads=hk, value_heads=hv, head_k_dim=dk, head_v_dim=dv,
-                                       eps=a_.rms_norm_eps) for t in range(S)]
+                                       eps=a_.rms_norm_eps, conv_out=conv_out) for t in range(S)]
             out = outs[0][:, None] if S == 1 else torch.stack(outs, dim=1)
             return self.out_proj(out)
         z = z.view(B, S, hv, dv)
@@ -241,6 +254,10 @@ class FullAttention(torch.nn.Module):
         """The projection of the layer input (its input norm can be fused into it)."""
         return self.qk_proj
 
+    def first_pre(self, x, cache: Qwen35Cache, **kw):
+        """qk_proj of the row its prologue forms from x (``forward_pre`` keywords)."""
+        return self.qk_proj.forward_pre(x, "add_rms_norm", **kw)
+
     def forward(self, x, cache: Qwen35Cache, first=None):
         """``first``: ``qk_proj(x)`` when the caller has computed it already."""
         a_ = self.args
@@ -310,8 +327,8 @@ class Qwen35Layer(torch.nn.Module):
         if _fused_row(x, self.mixer.first_proj, self.gate_up, self.down):
             h = torch.empty_like(x)                 # the normalized layer input
             x1 = x if delta is None else torch.empty_like(x)
-            first = self.mixer.first_proj.forward_pre(x, "add_rms_norm", pre_a=delta, pre_w=self.input_norm_w,
-                                                      eps=eps, res_out=None if delta is None else x1, x_out=h)
+            first = self.mixer.first_pre(x, cache, pre_a=delta, pre_w=self.input_norm_w, eps=eps,
+                                         res_out=None if delta is None else x1, x_out=h)
             m = self.mixer(h, cache, first=first)
             x2 = torch.empty_like(x)
             gu = self.gate_up.forward_pre(x1, "add_rms_norm", pre_a=m, pre_w=self.post_norm_w, eps=eps, res_out=x2)

@@ -60,11 +60,13 @@ def swiglu(gate_up):
 
 
 def gdn_step(qkv, z, x, w_ab, conv_state, conv_w, ssm_a, dt_bias, rec_state, norm_w, *, key_heads: int,
-             value_heads: int, head_k_dim: int, head_v_dim: int, eps: float):
+             value_heads: int, head_k_dim: int, head_v_dim: int, eps: float, conv_out=None):
     """One GatedDeltaNet token for B rows: qkv (B, conv_dim), z (B, Hv*dv) and the layer input x
     (B, hidden) as rows with unit stride along the last axis; w_ab (2 Hv, hidden) the a and b
     projections; conv_state (B, K-1, conv_dim) and rec_state (B, Hv, dk, dv, float32) are
-    updated in place. Returns (B, Hv*dv)."""
+    updated in place. ``conv_out`` (B, conv_dim, float32): the convolution has run already (in
+    the input projection's epilogue, ``quantized_matvec_pre(..., conv=...)``) and these are its
+    outputs; conv_state is then left alone. Returns (B, Hv*dv)."""
     dev = _on_gpu(qkv, z, x, w_ab, conv_state, conv_w, ssm_a, dt_bias, rec_state, norm_w)
     B = qkv.shape[0]
     for t in (qkv, z, x):
@@ -86,11 +88,18 @@ def gdn_step(qkv, z, x, w_ab, conv_state, conv_w, ssm_a, dt_bias, rec_state, nor
             or ssm_a.numel() != value_heads or dt_bias.numel() != value_heads):
         raise ValueError("GatedDeltaNet tensor shapes do not match the head configuration")
     out = torch.empty(B, value_heads * head_v_dim, dtype=qkv.dtype, device=dev)
-    work = torch.empty(B, conv_dim, dtype=torch.float32, device=dev)
+    if conv_out is None:
+        work = torch.empty(B, conv_dim, dtype=torch.float32, device=dev)
+    else:
+        if (conv_out.dtype != torch.float32 or not conv_out.is_contiguous() or conv_out.numel() != B * conv_dim
+                or conv_out.device != dev):
+            raise ValueError("conv_out must be contiguous float32 (B, conv_dim) on the same device")
+        work = conv_out
     with torch.cuda.device(dev):
         _lib.check(_lib.lib().gsq_gdn_step(
             qkv.data_ptr(), qkv.stride(0), z.data_ptr(), z.stride(0), x.data_ptr(), x.stride(0), w_ab.data_ptr(),
-            hidden, conv_state.data_ptr(), conv_w.data_ptr(), ssm_a.data_ptr(), dt_bias.data_ptr(),
+            hidden, None if conv_out is not None else conv_state.data_ptr(), conv_w.data_ptr(), ssm_a.data_ptr(),
+            dt_bias.data_ptr(),
             rec_state.data_ptr(), norm_w.data_ptr(), out.data_ptr(), out.stride(0), work.data_ptr(), B, key_heads,
             value_heads, head_k_dim, head_v_dim, K, float(eps), _dt(qkv), _lib.stream_handle(dev)), "gdn_step")
     return out

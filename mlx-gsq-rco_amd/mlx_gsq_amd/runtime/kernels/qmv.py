@@ -94,7 +94,7 @@ PRE_OPS = {"add_rms_norm": 1, "swiglu": 2}  # GSQ_PRE_ADD_RMSNORM, GSQ_PRE_SWIGL
 
 
 def quantized_matvec_pre(x, packed, *, qtype: str, out_features: int, in_features: int, pre: str, pre_a=None,
-                         pre_w=None, eps: float = 0.0, res_out=None, x_out=None, out_dtype=None):
+                         pre_w=None, eps: float = 0.0, res_out=None, x_out=None, out_dtype=None, conv=None):
     """y = row @ W.T for one fp16 activation row that the QMV kernel forms itself (libgsq
     ``gsq_qmv_pre``; no counterpart in the reference, whose model runs these as separate
     operations):
@@ -107,7 +107,10 @@ def quantized_matvec_pre(x, packed, *, qtype: str, out_features: int, in_feature
 
     The row is also written to ``x_out`` when given. ``x`` and the vectors are fp16 and hold
     exactly one row (any leading shape of size 1); the result has shape ``x.shape[:-1] +
-    (out_features,)``.
+    (out_features,)``. ``conv=(state, weight, out)`` adds the GatedDeltaNet's depthwise causal
+    convolution of the first ``state.shape[-1]`` outputs (fp16 result only): ``state`` (1, k-1,
+    rows) fp16 shifted in place, ``weight`` (rows, k) fp16, ``out`` (rows,) float32 receives
+    silu(convolution), as ``model_ops.gdn_step`` computes it.
     """
     if pre not in PRE_OPS:
         raise ValueError(f"unknown pre op {pre!r}")
@@ -126,6 +129,17 @@ def quantized_matvec_pre(x, packed, *, qtype: str, out_features: int, in_feature
     if pre == "add_rms_norm" and pre_w is None:
         raise ValueError("add_rms_norm needs the norm weight pre_w")
     odt = out_dtype or x.dtype
+    conv_rows = conv_k = 0
+    if conv is not None:
+        state, weight, cout = conv
+        conv_rows, conv_k = state.shape[-1], weight.shape[-1]
+        if (odt != torch.float16 or state.dtype != torch.float16 or weight.dtype != torch.float16
+                or cout.dtype != torch.float32 or tuple(state.shape) != (1, conv_k - 1, conv_rows)
+                or weight.numel() != conv_rows * conv_k or cout.numel() != conv_rows
+                or not (state.is_contiguous() and weight.is_contiguous() and cout.is_contiguous())
+                or conv_rows > out_features or any(t.device != x.device for t in conv)):
+            raise ValueError("conv must be (state (1, k-1, rows) fp16, weight (rows, k) fp16, out (rows,) float32), "
+                             "contiguous, rows <= out_features, fp16 output")
     flat = x.contiguous()
     packed = packed.contiguous()
     y = torch.empty(x.shape[:-1] + (out_features,), dtype=odt, device=x.device)
@@ -137,6 +151,9 @@ def quantized_matvec_pre(x, packed, *, qtype: str, out_features: int, in_feature
         _lib.check(_lib.lib().gsq_qmv_pre(TYPE_IDS[qtype], packed.data_ptr(), PRE_OPS[pre], flat.data_ptr(),
                                           ptr(pre_a), ptr(pre_w), float(eps), ptr(res_out), ptr(x_out), y.data_ptr(),
                                           _lib.DTYPE_CODES[odt], out_features, in_features,
+                                          None if conv is None else conv[0].data_ptr(),
+                                          None if conv is None else conv[1].data_ptr(), conv_rows, conv_k,
+                                          None if conv is None else conv[2].data_ptr(),
                                           _lib.stream_handle(x.device)),
                    "quantized_matvec_pre")
     return y

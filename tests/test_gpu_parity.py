@@ -389,6 +389,19 @@ def test_qmv_pre_matches_separate_kernels(qtype):
             assert torch.equal(res, xs)
             with pytest.raises(ValueError):  # the residual must go to a new buffer
                 quantized_matvec_pre(x, pd, pre=pre, pre_a=d, pre_w=w, eps=1e-6, res_out=x, **kw)
+            # the GatedDeltaNet convolution of the first 1000 outputs in the epilogue (fp16 y)
+            rows, kc = 1000, 4
+            state = torch.randn(1, kc - 1, rows, generator=g).half().cuda()
+            cw = (0.5 * torch.randn(rows, kc, generator=g)).half().cuda()
+            cout = torch.empty(rows, dtype=torch.float32, device="cuda")
+            state0 = state.clone()
+            y16 = quantized_matvec_pre(x, pd, pre=pre, pre_a=d, pre_w=w, eps=1e-6, conv=(state, cw, cout),
+                                       **{**kw, "out_dtype": torch.float16})
+            assert rel_l2(y16.float().cpu().numpy(), y.cpu().numpy()) <= 1e-3
+            win = torch.cat([state0[0].float(), y16.float()[:, :rows]], dim=0)      # (k, rows)
+            acc = (win * cw.float().t()).sum(0)
+            assert torch.allclose(cout, acc * torch.sigmoid(acc), rtol=1e-5, atol=1e-5)
+            assert torch.equal(state[0], torch.cat([state0[0, 1:], y16[:, :rows]], dim=0))
             # without the add and without outputs asked for
             y0 = quantized_matvec_pre(x, pd, pre=pre, pre_w=w, eps=1e-6, **kw)
             row0 = model_ops.add_rms_norm(x.clone(), None, w, 1e-6)

@@ -50,6 +50,30 @@ def test_c_validation_errors_without_gpu():
     g = np.zeros((10, 8), np.float32)
     ks = np.zeros(128, np.uint8)
     assert lib.gsq_set_tables(16, g.ctypes.data, 10, 8, ks.ctypes.data, 128) == _lib.GSQ_E_VALUE
+    # the fused-prologue QMV: arguments are checked before anything reaches a device
+    # (qtype, packed, pre_op, x, pre_a, pre_w, eps, res_out, x_out, y, y_dtype, N, K,
+    #  conv_state, conv_w, conv_rows, conv_kernel, conv_out, stream)
+    ok = dict(qt=12, packed=2, op=1, x=16, a=32, w=48, eps=1e-6, res=64, xo=80, y=96, ydt=1, n=4, k=256,
+              cs=112, cw=128, cr=0, ck=4, co=144)
+
+    def pre(**kw):
+        v = {**ok, **kw}
+        return lib.gsq_qmv_pre(v["qt"], v["packed"], v["op"], v["x"], v["a"], v["w"], v["eps"], v["res"], v["xo"],
+                               v["y"], v["ydt"], v["n"], v["k"], v["cs"], v["cw"], v["cr"], v["ck"], v["co"], None)
+    assert pre(op=7) == _lib.GSQ_E_VALUE and b"pre_op" in lib.gsq_last_error()
+    assert pre(w=None) == _lib.GSQ_E_VALUE and b"norm weight" in lib.gsq_last_error()
+    assert pre(eps=-1.0) == _lib.GSQ_E_VALUE
+    assert pre(res=16) == _lib.GSQ_E_VALUE and b"alias" in lib.gsq_last_error()  # res_out == x
+    assert pre(x=24) == _lib.GSQ_E_VALUE and b"aligned" in lib.gsq_last_error()
+    assert pre(cr=5) == _lib.GSQ_E_VALUE  # more convolution rows than outputs
+    assert pre(cr=4, ck=9) == _lib.GSQ_E_VALUE and b"kernel" in lib.gsq_last_error()
+    assert pre(cr=4, ydt=0) == _lib.GSQ_E_VALUE and b"fp16 y" in lib.gsq_last_error()
+    assert pre(cr=4, co=None) == _lib.GSQ_E_VALUE
+    assert pre(k=300) == _lib.GSQ_E_VALUE  # K % 256
+    # the decode-step kernels
+    assert lib.gsq_add_rms_norm(16, None, 32, 48, 1, 12, 1e-6, 1, None) == _lib.GSQ_E_VALUE  # dim % 8
+    assert lib.gsq_add_rms_norm(16, None, 32, 48, 1, 16, 1e-6, 5, None) == _lib.GSQ_E_TYPE
+    assert lib.gsq_swiglu(16, 32, 1, 0, 1, None) == _lib.GSQ_E_VALUE
 
 
 def test_python_validation_mirrors_reference():

@@ -399,9 +399,12 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
     static_cast<T*>(a.vc)[base + (int64_t)p * hd + t] = E::mk(sv[t]);
   }
   __syncthreads();
-  // scores: 64 positions per pass, four threads per position (a quarter of hd each)
+  // scores: 64 positions per pass, four threads per position (a quarter of hd each); with hd a
+  // multiple of 32 and an aligned cache, a thread's quarter row is read as 8-value chunks, all
+  // issued before the first use
   const float scale = 1.f / sqrtf((float)hd);
-  const int quarter = hd / 4, pi = t >> 2, qd = t & 3;
+  const int quarter = hd / 4, pi = t >> 2, qd = t & 3, nchunk = quarter >> 3;
+  const bool vec = (hd & 31) == 0 && (reinterpret_cast<uintptr_t>(K) & 15) == 0;
   float mx = -INFINITY;
   for (int j0 = 0; j0 <= p; j0 += 64) {
     const int j = j0 + pi;
@@ -410,6 +413,17 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
       const int d0 = qd * quarter;
       if (j == p) {
         for (int d = 0; d < quarter; ++d) part += sq[d0 + d] * sk[d0 + d];
+      } else if (vec) {
+        const T* kr = K + (int64_t)j * hd + d0;
+        Vec8<DT> kv[8];  // quarter <= 64: at most 8 chunks (later ones re-read the last)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) kv[c].load(kr + 8 * min(c, nchunk - 1));
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+          if (c < nchunk) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) part += sq[d0 + 8 * c + e] * kv[c].v[e];
+          }
       } else {
         const T* kr = K + (int64_t)j * hd + d0;
         for (int d = 0; d < quarter; ++d) part += sq[d0 + d] * E::ld(kr + d);
@@ -445,7 +459,15 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
   }
   if (t < hd) {
     float o = 0.f;
-    for (int j = 0; j < p; ++j) o += sc[j] * E::ld(V + (int64_t)j * hd + t);
+    int j = 0;
+    for (; j + 8 <= p; j += 8) {  // 8 positions' loads in flight at a time, summed in order
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = E::ld(V + (int64_t)(j + u) * hd + t);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) o += sc[j + u] * v[u];
+    }
+    for (; j < p; ++j) o += sc[j] * E::ld(V + (int64_t)j * hd + t);
     o += sc[p] * sv[t];
     const float gate = E::ld(qg + hd + t);
     static_cast<T*>(a.out)[(int64_t)bb * a.out_stride + (int64_t)h * hd + t] = E::mk(o * (1.f / (1.f + expf(-gate))));

@@ -191,3 +191,21 @@ def test_gpu_attention_decode_matches_torch_formulation():
         for c in (3,):
             assert rel_l2(gcache.k[c][:, :, :t + 1].float().cpu().numpy(), ccache.k[c][:, :, :t + 1].numpy()) <= 2e-3
             assert torch.equal(gcache.v[c][:, :, :t + 1].float().cpu(), ccache.v[c][:, :, :t + 1])
+    # a longer context (three 64-position score passes, the 8-position V blocks and a tail):
+    # identical random caches up to position 141, one new token at 141
+    for c in (gcache, ccache):
+        c.k[3] = c.k[3].new_zeros(B, Hkv, 160, hd)
+        c.v[3] = c.v[3].new_zeros(B, Hkv, 160, hd)
+    kc = torch.randn(B, Hkv, 141, hd, generator=g).half()
+    vc = torch.randn(B, Hkv, 141, hd, generator=g).half()
+    gcache.k[3][:, :, :141], gcache.v[3][:, :, :141] = kc.to(dev), vc.to(dev)
+    ccache.k[3][:, :, :141], ccache.v[3][:, :, :141] = kc.float(), vc.float()
+    gcache.pos.fill_(141)
+    ccache.pos.fill_(141)
+    qk = torch.randn(B, 1, H * 2 * hd + Hkv * hd, generator=g).half()
+    v = torch.randn(B, 1, Hkv * hd, generator=g).half()
+    cpu.qk_proj.value, cpu.v_proj.value = qk.float(), v.float()
+    gpu.qk_proj.value, gpu.v_proj.value = qk.to(dev), v.to(dev)
+    want = cpu(torch.zeros(B, 1, 8), ccache)
+    got = gpu(torch.zeros(B, 1, 8, device=dev, dtype=torch.float16), gcache).float().cpu()
+    assert rel_l2(got.numpy(), want.numpy()) <= 5e-3

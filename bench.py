@@ -24,7 +24,8 @@ Printed JSON line (one, on stdout):
   decode_stack_fused  the same products with q|k and gate|up fused (320 launches)
   decode_stack_grouped  the same through GSQGroupedLinear / GSQLinear modules (fp16 outputs)
   model_decode  single-token decode of the whole 27B Qwen3.5-hybrid model (norms, GatedDeltaNet,
-                attention, MLP, lm_head) as one HIP graph per step: model tokens/s
+                attention, MLP, lm_head) as one HIP graph per step: model tokens/s; `batched`:
+                8 sequences decoded together (tokens/s over all of them)
   cpu_baseline  the numpy oracle (dequant + float32 matmul) on the configs[1] products, all host threads
 
 Algorithmic bytes per QMV launch = N*(K/256)*block_bytes + M*K*2 (x fp16) + M*N*4 (y fp32).
@@ -592,11 +593,12 @@ class SyntheticQwen35Store:
         return self.plains[name]
 
 
-def run_model_decode(device, max_len=1024, prompt=8, steps=32):
+def run_model_decode(device, max_len=1024, prompt=8, steps=32, batches=(8,)):
     """§8(f) rank 4: single-token decode steps of the 27B Qwen3.5-hybrid model (64 layers, random
     packed weights in the MODEL_TYPES mix, fp16 activations) as one HIP graph per step
     (GraphDecoder), after an eager prefill of `prompt` tokens; model tokens/s, and the packed
-    bytes read per token over the step time."""
+    bytes read per token over the step time. Then the same for `batches` sequences decoded
+    together (one step = one token of each; the projections run as small-batch products)."""
     import torch
     from mlx_gsq_amd import _lib
     from mlx_gsq_amd.models import GraphDecoder, Qwen35Args, build_qwen35
@@ -608,29 +610,37 @@ def run_model_decode(device, max_len=1024, prompt=8, steps=32):
     # bytes one token reads: every packed matrix except the embedding table (one row of it)
     emb = store.weights["token_embd.weight"]
     per_token = store.packed_bytes - emb.num_bytes + emb.num_bytes // args.vocab_size
-    cache = model.new_cache(batch=1, max_len=max_len, device=device)
-    ids = torch.randint(0, args.vocab_size, (1, prompt + steps + 1), device=device)
-    with torch.no_grad():
-        model(ids[:, :prompt], cache)
-        dec = GraphDecoder(model, cache)
-        dec.step(ids[:, prompt:prompt + 1])
-        torch.cuda.synchronize()
-        stream = torch.cuda.current_stream(device)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for i in range(steps):
-            dec.step(ids[:, prompt + 1 + i:prompt + 2 + i])
-        e1.record(stream)
-        torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
+    def step_ms(batch):
+        cache = model.new_cache(batch=batch, max_len=max_len, device=device)
+        ids = torch.randint(0, args.vocab_size, (batch, prompt + steps + 1), device=device)
+        with torch.no_grad():
+            model(ids[:, :prompt], cache)
+            dec = GraphDecoder(model, cache, batch=batch)
+            dec.step(ids[:, prompt:prompt + 1])
+            torch.cuda.synchronize()
+            stream = torch.cuda.current_stream(device)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for i in range(steps):
+                dec.step(ids[:, prompt + 1 + i:prompt + 2 + i])
+            e1.record(stream)
+            torch.cuda.synchronize()
+        del dec, cache
+        torch.cuda.empty_cache()
+        return e0.elapsed_time(e1) / steps
+
+    ms = step_ms(1)
     res = {"model": "Qwen3.5-hybrid 27B shapes (64 layers: 48 GatedDeltaNet, 16 attention), synthetic weights",
            "ms_per_token": round(ms, 4), "tokens_per_s": round(1e3 / ms, 1),
            "packed_bytes_per_token": int(per_token),
            "packed_GB/s": round(per_token / (ms * 1e-3) / 1e9, 1),
            "frac": round(per_token / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
            "context": f"prefill {prompt} tokens, then {steps} timed graph steps (KV buffer {max_len})",
-           "types": MODEL_TYPES}
-    del dec, model, store, cache
+           "types": MODEL_TYPES, "batched": {}}
+    for b in batches:
+        ms_b = step_ms(b)
+        res["batched"][f"B={b}"] = {"ms_per_step": round(ms_b, 4), "tokens_per_s": round(b * 1e3 / ms_b, 1)}
+    del model, store
     torch.cuda.empty_cache()
     return res
 

@@ -95,6 +95,36 @@ def test_gpu_decode_matches_hf_and_graph_replays(store_and_ref):
         assert cache.length == len(IDS)
 
 
+@pytest.mark.gpu
+def test_gpu_batched_decode_matches_single_sequences():
+    """Two sequences decoded together (two-row projections, the step kernels over a batch, one
+    HIP graph per step) give each sequence's own single-sequence logits (prefill of 4 tokens,
+    then 4 decode steps)."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from mlx_gsq_amd.models import GraphDecoder
+    tables.set_tables(TABLES)
+    dev = torch.device("cuda:0")
+    model = build_qwen35(TinyStore(dev, seed=1), dtype=torch.float16, args=ARGS)
+    seqs = [IDS, [3, 14, 15, 92, 65, 35, 89, 79]]
+    with torch.no_grad():
+        singles = []
+        for sq in seqs:
+            cache = model.new_cache(batch=1, max_len=16)
+            ids = torch.tensor([sq], device=dev)
+            outs = [model(ids[:, :4], cache)] + [model(ids[:, i:i + 1], cache) for i in range(4, 8)]
+            singles.append(torch.cat(outs, dim=1).float().cpu())
+        cache = model.new_cache(batch=2, max_len=16)
+        ids = torch.tensor(seqs, device=dev)
+        outs = [model(ids[:, :4], cache)]
+        dec = GraphDecoder(model, cache, batch=2)
+        outs += [dec.step(ids[:, i:i + 1]).clone() for i in range(4, 8)]
+        both = torch.cat(outs, dim=1).float().cpu()
+    assert torch.isfinite(both).all()
+    for b in range(2):
+        assert rel_l2(both[b].numpy(), singles[b][0].numpy()) <= 1e-2, b
+
+
 class _Given(torch.nn.Module):
     """Stands in for a projection: returns the tensor set for the current step."""
 

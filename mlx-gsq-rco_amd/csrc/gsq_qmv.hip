@@ -100,6 +100,12 @@ __device__ __forceinline__ uint32_t enc_codes(uint32_t codes) {
 }
 template <bool XS>
 __device__ __forceinline__ constexpr float enc_scale() { return 1.f; }
+// The same for codes already carrying 1024's exponent byte (a byte permute that puts 0x64 above
+// each code byte): only the exact subtraction of 1024 remains.
+__device__ __forceinline__ uint32_t unbias_codes(uint32_t biased) {
+  const half2_t r = __builtin_bit_cast(half2_t, biased) - (half2_t){(_Float16)1024.f, (_Float16)1024.f};
+  return __builtin_bit_cast(uint32_t, r);
+}
 
 // Both 16-bit halves shifted right by 8 (v_pk_lshrrev_b16): bytes 1 and 3 move to 0 and 2.
 typedef unsigned short ushort2_t __attribute__((ext_vector_type(2)));
@@ -237,7 +243,8 @@ template <> struct Qmv<Q6_K> {
   // 51-64). Each word of 4 weights is one funnel shift out of the ql stream (nibble to bits
   // 0-3 of every byte) and one out of the qh stream (2 bits to bits 4-5), which also absorbs
   // the superblock's 2-byte alignment; the 6-bit codes then assemble bytewise and two byte
-  // permutes spread them into the fp16 code pairs (elements 0, 2 and 1, 3).
+  // permutes spread them into the fp16 code pairs (elements 0, 2 and 1, 3), with the exponent
+  // byte of 1024 above each code.
   template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t*, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
@@ -260,8 +267,9 @@ template <> struct Qmv<Q6_K> {
       const uint32_t L = __builtin_amdgcn_alignbit(wl[k + 1], wl[k], nl);
       const uint32_t H = __builtin_amdgcn_alignbit(wh[k + 1], wh[k], nh);
       const uint32_t C = (L & 0x0F0F0F0Fu) | (H & 0x30303030u);
-      const uint32_t A = enc_codes<XS>(__builtin_amdgcn_perm(0u, C, 0x0C020C00u));
-      const uint32_t B = enc_codes<XS>(__builtin_amdgcn_perm(0u, C, 0x0C030C01u));
+      // code bytes 0, 2 (A) and 1, 3 (B) under 1024's exponent byte 0x64, then 1024 removed
+      const uint32_t A = unbias_codes(__builtin_amdgcn_perm(0x64646464u, C, 0x04020400u));
+      const uint32_t B = unbias_codes(__builtin_amdgcn_perm(0x64646464u, C, 0x04030401u));
       if (k < 4) { dacc<MR, XS>(A, x, 2 * k, a0); dacc<MR, XS>(B, x, 2 * k + 1, a0); }
       else { dacc<MR, XS>(A, x, 2 * k, a1); dacc<MR, XS>(B, x, 2 * k + 1, a1); }
     }

@@ -165,12 +165,17 @@ int gsq_gdn_step(const void* qkv, int64_t qkv_stride, const void* z, int64_t z_s
  * rotary_dim dims (rotate-half, angle pos * inv_freq[i]) and rounded; k and v written at *pos
  * into k_cache / v_cache [batch, kv_heads, max_len, head_dim]; softmax over positions 0..*pos of
  * q . K / sqrt(head_dim); out = round(sum p V * sigmoid(gate)). *pos is read on the device
- * (< max_len, at most 32768). head_dim a multiple of 4 up to 256. Strides in elements. */
+ * (< max_len). head_dim a multiple of 4 up to 256. Strides in elements. With work NULL one
+ * workgroup per (row, head) covers every position (max_len at most 32768); otherwise the
+ * positions are split into ceil(max_len / chunk) chunks (chunk a multiple of 64 up to 1024,
+ * max_len up to 2^20), one workgroup each, whose partial softmax sums meet in work (batch *
+ * heads * ceil(max_len / chunk) * (head_dim + 2) floats) and are combined by a second kernel:
+ * for long contexts. */
 int gsq_attn_decode(const void* qg, int64_t qg_stride, const void* k, int64_t k_stride, const void* v,
                     int64_t v_stride, const void* q_norm_w, const void* k_norm_w, const double* inv_freq,
                     void* k_cache, void* v_cache, const int64_t* pos, void* out, int64_t out_stride, int64_t batch,
                     int64_t heads, int64_t kv_heads, int64_t head_dim, int64_t rotary_dim, int64_t max_len,
-                    float eps, int dtype, void* stream);
+                    float eps, float* work, int64_t chunk, int dtype, void* stream);
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* gsq_last_error(void);

@@ -517,7 +517,7 @@ int gsq_attn_decode(const void* qg, int64_t qg_stride, const void* k, int64_t k_
                     int64_t v_stride, const void* q_norm_w, const void* k_norm_w, const double* inv_freq,
                     void* k_cache, void* v_cache, const int64_t* pos, void* out, int64_t out_stride, int64_t batch,
                     int64_t heads, int64_t kv_heads, int64_t head_dim, int64_t rotary_dim, int64_t max_len,
-                    float eps, int dtype, void* stream) {
+                    float eps, float* work, int64_t chunk, int dtype, void* stream) {
   if (dtype != GSQ_F32 && dtype != GSQ_F16 && dtype != GSQ_BF16) return fail(GSQ_E_TYPE, "unsupported dtype code %d", dtype);
   if (batch < 0 || batch > 65535) return fail(GSQ_E_VALUE, "batch must be 0..65535");
   if (batch == 0) return GSQ_OK;
@@ -525,7 +525,10 @@ int gsq_attn_decode(const void* qg, int64_t qg_stride, const void* k, int64_t k_
     return fail(GSQ_E_VALUE, "heads must be a positive multiple of kv heads (at most 65535)");
   if (head_dim <= 0 || head_dim > 256 || head_dim % 4) return fail(GSQ_E_VALUE, "head dim must be a multiple of 4 up to 256");
   if (rotary_dim < 0 || rotary_dim > head_dim || rotary_dim % 2) return fail(GSQ_E_VALUE, "invalid rotary dim");
-  if (max_len <= 0 || max_len > 32768) return fail(GSQ_E_VALUE, "cache length must be 1..32768");
+  if (work && (chunk < 64 || chunk > 1024 || chunk % 64))
+    return fail(GSQ_E_VALUE, "chunk must be a multiple of 64 from 64 to 1024");
+  if (max_len <= 0 || max_len > (work ? (1 << 20) : 32768))
+    return fail(GSQ_E_VALUE, "cache length must be 1..%d", work ? (1 << 20) : 32768);
   if (!qg || !k || !v || !q_norm_w || !k_norm_w || (!inv_freq && rotary_dim) || !k_cache || !v_cache || !pos || !out)
     return fail(GSQ_E_VALUE, "NULL pointer");
   if (!(eps >= 0.f)) return fail(GSQ_E_VALUE, "eps must be >= 0");
@@ -535,6 +538,11 @@ int gsq_attn_decode(const void* qg, int64_t qg_stride, const void* k, int64_t k_
   a.qg_stride = qg_stride; a.k_stride = k_stride; a.v_stride = v_stride; a.out_stride = out_stride;
   a.B = (int)batch; a.H = (int)heads; a.Hkv = (int)kv_heads; a.hd = (int)head_dim; a.rd = (int)rotary_dim;
   a.L = (int)max_len; a.eps = eps;
+  if (work) {
+    a.work = work;
+    a.chunk = (int)chunk;
+    a.nsplit = (int)((max_len + chunk - 1) / chunk);
+  }
   hipError_t e = launch_attn_decode(dtype, a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(GSQ_E_HIP, "attn_decode launch: %s", hipGetErrorString(e));
   return GSQ_OK;

@@ -148,6 +148,10 @@ struct AttnArgs {
   int64_t qg_stride, k_stride, v_stride, out_stride;
   int B, H, Hkv, hd, rd, L;
   float eps;
+  // positions split into chunks of `chunk` (nsplit = ceil(L / chunk)) when work is not null:
+  // per (row, head, chunk) the partial softmax max, sum and hd weighted V sums, then combined
+  float* work = nullptr;
+  int chunk = 0, nsplit = 0;
 };
 
 // QMM workspace: fp32 partial tiles of workgroups that share an output tile (2 slots per

@@ -474,6 +474,138 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
   }
 }
 
+// ---- gated attention over position chunks (long contexts) --------------------------------
+// Workgroup (query head h, batch row b, chunk c) covers positions [c chunk, (c + 1) chunk) up to
+// pos: q (and, in the chunk holding pos, the new k and v, which its KV head's first query head
+// also writes to the caches) as in attn_decode_kernel, the chunk's scores, their max m_c, the
+// sum l_c of exp(score - m_c) and o_c = sum exp(score - m_c) V, written to work; chunks past
+// pos write m_c = -inf. attn_combine_kernel then forms softmax-weighted V from the chunks,
+// o = sum_c exp(m_c - m) o_c / sum_c exp(m_c - m) l_c with m the largest m_c, and the gate.
+constexpr int kAttnChunkMax = 1024;
+
+template <int DT>
+__global__ void __launch_bounds__(256) attn_chunk_kernel(AttnArgs a) {
+  using E = Elem<DT>;
+  using T = typename E::T;
+  __shared__ float sq[256], sk[256], sv[256], red[16], sc[kAttnChunkMax];
+  const int h = blockIdx.x, bb = blockIdx.y, c = blockIdx.z, t = threadIdx.x;
+  const int hd = a.hd, rep = a.H / a.Hkv, kvh = h / rep;
+  const int p = (int)a.pos[0];
+  const int j0 = c * a.chunk;
+  float* part = a.work + (((int64_t)bb * a.H + h) * a.nsplit + c) * (hd + 2);
+  if (j0 > p) {  // a chunk past the new token: contributes nothing
+    if (t == 0) { part[0] = -INFINITY; part[1] = 0.f; }
+    if (t < hd) part[2 + t] = 0.f;
+    return;
+  }
+  const int j1 = min(j0 + a.chunk, p + 1);  // positions [j0, j1)
+  const bool has_new = p < j0 + a.chunk;    // the chunk holds the new token (uniform)
+  const T* qg = static_cast<const T*>(a.qg) + (int64_t)bb * a.qg_stride + (int64_t)h * 2 * hd;
+  attn_norm_rope<DT>(qg, static_cast<const T*>(a.q_norm_w), a, p, sq, red);
+  const int64_t base = ((int64_t)bb * a.Hkv + kvh) * a.L * hd;
+  const T* K = static_cast<const T*>(a.kc) + base;
+  const T* V = static_cast<const T*>(a.vc) + base;
+  if (has_new) {
+    attn_norm_rope<DT>(static_cast<const T*>(a.k) + (int64_t)bb * a.k_stride + (int64_t)kvh * hd,
+                       static_cast<const T*>(a.k_norm_w), a, p, sk, red);
+    const T* vr = static_cast<const T*>(a.v) + (int64_t)bb * a.v_stride + (int64_t)kvh * hd;
+    if (t < hd) sv[t] = E::ld(vr + t);
+    if (h % rep == 0 && t < hd) {
+      static_cast<T*>(a.kc)[base + (int64_t)p * hd + t] = E::mk(sk[t]);
+      static_cast<T*>(a.vc)[base + (int64_t)p * hd + t] = E::mk(sv[t]);
+    }
+  }
+  __syncthreads();
+  const float scale = 1.f / sqrtf((float)hd);
+  const int quarter = hd / 4, pi = t >> 2, qd = t & 3, nchunk = quarter >> 3;
+  const bool vec = (hd & 31) == 0 && (reinterpret_cast<uintptr_t>(K) & 15) == 0;
+  float mx = -INFINITY;
+  for (int jb = j0; jb < j1; jb += 64) {
+    const int j = jb + pi;
+    float part_s = 0.f;
+    if (j < j1) {
+      const int d0 = qd * quarter;
+      if (j == p) {
+        for (int d = 0; d < quarter; ++d) part_s += sq[d0 + d] * sk[d0 + d];
+      } else if (vec) {
+        const T* kr = K + (int64_t)j * hd + d0;
+        Vec8<DT> kv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) kv[u].load(kr + 8 * min(u, nchunk - 1));
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (u < nchunk) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) part_s += sq[d0 + 8 * u + e] * kv[u].v[e];
+          }
+      } else {
+        const T* kr = K + (int64_t)j * hd + d0;
+        for (int d = 0; d < quarter; ++d) part_s += sq[d0 + d] * E::ld(kr + d);
+      }
+    }
+    part_s += __shfl_xor(part_s, 1, 64);
+    part_s += __shfl_xor(part_s, 2, 64);
+    if (j < j1 && qd == 0) {
+      sc[j - j0] = part_s * scale;
+      mx = fmaxf(mx, part_s * scale);
+    }
+  }
+  float m = mx;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  __syncthreads();
+  if ((t & 63) == 0) red[t >> 6] = m;
+  __syncthreads();
+  m = -INFINITY;
+  for (int i = 0; i < (int)(blockDim.x >> 6); ++i) m = fmaxf(m, red[i]);
+  float sum = 0.f;
+  for (int j = t; j < j1 - j0; j += blockDim.x) {
+    const float e = expf(sc[j] - m);
+    sc[j] = e;
+    sum += e;
+  }
+  sum = block_sum(sum, red);
+  __syncthreads();
+  if (t < hd) {
+    float o = 0.f;
+    const int jn = has_new ? p : j1;  // cached positions; the new one comes from sv
+    int j = j0;
+    for (; j + 8 <= jn; j += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = E::ld(V + (int64_t)(j + u) * hd + t);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) o += sc[j - j0 + u] * v[u];
+    }
+    for (; j < jn; ++j) o += sc[j - j0] * E::ld(V + (int64_t)j * hd + t);
+    if (has_new) o += sc[p - j0] * sv[t];
+    part[2 + t] = o;
+  }
+  if (t == 0) { part[0] = m; part[1] = sum; }
+}
+
+template <int DT>
+__global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
+  using E = Elem<DT>;
+  using T = typename E::T;
+  const int h = blockIdx.x, bb = blockIdx.y, t = threadIdx.x, hd = a.hd;
+  if (t >= hd) return;
+  const float* part = a.work + ((int64_t)bb * a.H + h) * a.nsplit * (hd + 2);
+  float m = -INFINITY;
+  for (int c = 0; c < a.nsplit; ++c) m = fmaxf(m, part[(int64_t)c * (hd + 2)]);
+  float l = 0.f, o = 0.f;
+  for (int c = 0; c < a.nsplit; ++c) {
+    const float* pc = part + (int64_t)c * (hd + 2);
+    const float w = expf(pc[0] - m);  // 0 for chunks past the new token
+    l += w * pc[1];
+    o += w * pc[2 + t];
+  }
+  const T* qg = static_cast<const T*>(a.qg) + (int64_t)bb * a.qg_stride + (int64_t)h * 2 * hd;
+  const float gate = E::ld(qg + hd + t);
+  static_cast<T*>(a.out)[(int64_t)bb * a.out_stride + (int64_t)h * hd + t] =
+      E::mk(o / l * (1.f / (1.f + expf(-gate))));
+}
+
 constexpr int kAttnMaxPositions = 32768;  // scores of up to this many positions stay in LDS
 
 template <int DT>
@@ -490,6 +622,22 @@ static hipError_t attn_lds_attr() {
 
 hipError_t launch_attn_decode(int dt, const AttnArgs& a, hipStream_t s) {
   const dim3 grid((unsigned)a.H, (unsigned)a.B);
+  if (a.work) {
+    if (a.chunk < 64 || a.chunk > kAttnChunkMax || a.nsplit < 1 || (int64_t)a.nsplit * a.chunk < a.L)
+      return hipErrorInvalidValue;
+    const dim3 cgrid((unsigned)a.H, (unsigned)a.B, (unsigned)a.nsplit);
+    if (dt == MD_F16) {
+      hipLaunchKernelGGL(attn_chunk_kernel<MD_F16>, cgrid, dim3(256), 0, s, a);
+      hipLaunchKernelGGL(attn_combine_kernel<MD_F16>, grid, dim3(256), 0, s, a);
+    } else if (dt == MD_BF16) {
+      hipLaunchKernelGGL(attn_chunk_kernel<MD_BF16>, cgrid, dim3(256), 0, s, a);
+      hipLaunchKernelGGL(attn_combine_kernel<MD_BF16>, grid, dim3(256), 0, s, a);
+    } else {
+      hipLaunchKernelGGL(attn_chunk_kernel<MD_F32>, cgrid, dim3(256), 0, s, a);
+      hipLaunchKernelGGL(attn_combine_kernel<MD_F32>, grid, dim3(256), 0, s, a);
+    }
+    return hipGetLastError();
+  }
   const size_t lds = (size_t)a.L * sizeof(float);
   if (a.L > kAttnMaxPositions) return hipErrorInvalidValue;
   hipError_t e = dt == MD_F16 ? attn_lds_attr<MD_F16>() : (dt == MD_BF16 ? attn_lds_attr<MD_BF16>() : attn_lds_attr<MD_F32>());

@@ -37,7 +37,7 @@ EXPORTS = {
     "gsq_add_rms_norm": (_I32, [_VP, _VP, _VP, _VP, _I64, _I64, _F32, _I32, _VP]),
     "gsq_swiglu": (_I32, [_VP, _VP, _I64, _I64, _I32, _VP]),
     "gsq_attn_decode": (_I32, [_VP, _I64, _VP, _I64, _VP, _I64, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64,
-                               _I64, _I64, _I64, _I64, _F32, _I32, _VP]),
+                               _I64, _I64, _I64, _I64, _F32, _VP, _I64, _I32, _VP]),
     "gsq_gdn_step": (_I32, [_VP, _I64, _VP, _I64, _VP, _I64, _VP, _I64, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I64,
                             _VP, _I64, _I64, _I64, _I64, _I64, _I64, _F32, _I32, _VP]),
     "gsq_last_error": (ctypes.c_char_p, []),

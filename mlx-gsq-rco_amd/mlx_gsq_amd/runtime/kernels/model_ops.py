@@ -105,12 +105,19 @@ def gdn_step(qkv, z, x, w_ab, conv_state, conv_w, ssm_a, dt_bias, rec_state, nor
     return out
 
 
+# caches at least this long split the positions into chunks (one workgroup each, then a combine)
+ATTN_SPLIT_MIN_LEN = 2048
+ATTN_CHUNK = 256
+
+
 def attn_decode(qg, k, v, q_norm_w, k_norm_w, inv_freq, k_cache, v_cache, pos, *, heads: int, kv_heads: int,
-                head_dim: int, rotary_dim: int, eps: float):
+                head_dim: int, rotary_dim: int, eps: float, chunk=None):
     """One new token of gated grouped-query attention for B rows: qg (B, heads * 2 head_dim) with
     [q | gate] per head, k and v (B, kv_heads * head_dim), rows with unit inner stride; the caches
     (B, kv_heads, max_len, head_dim) get k and v at position ``pos`` (a one-element int64 device
-    tensor); inv_freq (rotary_dim / 2,) float64. Returns (B, heads * head_dim)."""
+    tensor); inv_freq (rotary_dim / 2,) float64. ``chunk``: positions per workgroup (a multiple of
+    64 up to 1024; 0 = one workgroup per head over all positions; default: ``ATTN_CHUNK`` for
+    caches of ``ATTN_SPLIT_MIN_LEN`` positions or more, else 0). Returns (B, heads * head_dim)."""
     dev = _on_gpu(qg, k, v, q_norm_w, k_norm_w, inv_freq, k_cache, v_cache, pos)
     B = qg.shape[0]
     for t in (qg, k, v):
@@ -127,10 +134,17 @@ def attn_decode(qg, k, v, q_norm_w, k_norm_w, inv_freq, k_cache, v_cache, pos, *
         if t.dtype != qg.dtype or not t.is_contiguous():
             raise ValueError("norm weights and caches must be contiguous in the activation dtype")
     out = torch.empty(B, heads * head_dim, dtype=qg.dtype, device=dev)
+    L = k_cache.shape[2]
+    if chunk is None:
+        chunk = ATTN_CHUNK if L >= ATTN_SPLIT_MIN_LEN else 0
+    work = None
+    if chunk:
+        work = torch.empty(B * heads * (-(-L // chunk)) * (head_dim + 2), dtype=torch.float32, device=dev)
     with torch.cuda.device(dev):
         _lib.check(_lib.lib().gsq_attn_decode(
             qg.data_ptr(), qg.stride(0), k.data_ptr(), k.stride(0), v.data_ptr(), v.stride(0), q_norm_w.data_ptr(),
             k_norm_w.data_ptr(), inv_freq.contiguous().data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
             pos.data_ptr(), out.data_ptr(), out.stride(0), B, heads, kv_heads, head_dim, rotary_dim,
-            k_cache.shape[2], float(eps), _dt(qg), _lib.stream_handle(dev)), "attn_decode")
+            L, float(eps), None if work is None else work.data_ptr(), int(chunk), _dt(qg),
+            _lib.stream_handle(dev)), "attn_decode")
     return out

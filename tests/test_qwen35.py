@@ -239,3 +239,16 @@ def test_gpu_attention_decode_matches_torch_formulation():
     want = cpu(torch.zeros(B, 1, 8), ccache)
     got = gpu(torch.zeros(B, 1, 8, device=dev, dtype=torch.float16), gcache).float().cpu()
     assert rel_l2(got.numpy(), want.numpy()) <= 5e-3
+    # the same token with the positions split into chunks of 64 (three chunks hold positions,
+    # the last one none) and combined: the long-context form
+    from mlx_gsq_amd.runtime.kernels import model_ops
+    orig = (model_ops.ATTN_SPLIT_MIN_LEN, model_ops.ATTN_CHUNK)
+    model_ops.ATTN_SPLIT_MIN_LEN, model_ops.ATTN_CHUNK = 1, 64
+    try:
+        kc0, vc0 = gcache.k[3].clone(), gcache.v[3].clone()
+        got_split = gpu(torch.zeros(B, 1, 8, device=dev, dtype=torch.float16), gcache).float().cpu()
+    finally:
+        model_ops.ATTN_SPLIT_MIN_LEN, model_ops.ATTN_CHUNK = orig
+    assert rel_l2(got_split.numpy(), want.numpy()) <= 5e-3
+    assert rel_l2(got_split.numpy(), got.numpy()) <= 1e-3
+    assert torch.equal(gcache.k[3], kc0) and torch.equal(gcache.v[3], vc0)  # same slot, same values

@@ -25,7 +25,8 @@ Printed JSON line (one, on stdout):
   decode_stack_grouped  the same through GSQGroupedLinear / GSQLinear modules (fp16 outputs)
   model_decode  single-token decode of the whole 27B Qwen3.5-hybrid model (norms, GatedDeltaNet,
                 attention, MLP, lm_head) as one HIP graph per step: model tokens/s; `batched`:
-                8 sequences decoded together (tokens/s over all of them)
+                8 sequences decoded together (tokens/s over all of them); `prefill`: one
+                182-token prompt (the reference's published prefill length)
   cpu_baseline  the numpy oracle (dequant + float32 matmul) on the configs[1] products, all host threads
 
 Algorithmic bytes per QMV launch = N*(K/256)*block_bytes + M*K*2 (x fp16) + M*N*4 (y fp32).
@@ -629,6 +630,22 @@ def run_model_decode(device, max_len=1024, prompt=8, steps=32, batches=(8,)):
         torch.cuda.empty_cache()
         return e0.elapsed_time(e1) / steps
 
+    def prefill_ms(tokens):
+        ids = torch.randint(0, args.vocab_size, (1, tokens), device=device)
+        with torch.no_grad():
+            model(ids, model.new_cache(batch=1, max_len=tokens, device=device))  # warm-up
+            cache = model.new_cache(batch=1, max_len=tokens, device=device)
+            torch.cuda.synchronize()
+            stream = torch.cuda.current_stream(device)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            model(ids, cache)
+            e1.record(stream)
+            torch.cuda.synchronize()
+        del cache
+        torch.cuda.empty_cache()
+        return e0.elapsed_time(e1)
+
     ms = step_ms(1)
     res = {"model": "Qwen3.5-hybrid 27B shapes (64 layers: 48 GatedDeltaNet, 16 attention), synthetic weights",
            "ms_per_token": round(ms, 4), "tokens_per_s": round(1e3 / ms, 1),
@@ -640,6 +657,10 @@ def run_model_decode(device, max_len=1024, prompt=8, steps=32, batches=(8,)):
     for b in batches:
         ms_b = step_ms(b)
         res["batched"][f"B={b}"] = {"ms_per_step": round(ms_b, 4), "tokens_per_s": round(b * 1e3 / ms_b, 1)}
+    # prefill of the reference's published prompt length (eager: tiled QMM projections, the
+    # GatedDeltaNet sequence kernels, attention on torch ops), logits of every position
+    pms = prefill_ms(182)
+    res["prefill"] = {"tokens": 182, "ms": round(pms, 2), "tokens_per_s": round(182e3 / pms, 1)}
     del model, store
     torch.cuda.empty_cache()
     return res

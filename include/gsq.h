@@ -158,6 +158,18 @@ int gsq_gdn_step(const void* qkv, int64_t qkv_stride, const void* z, int64_t z_s
                  int64_t out_stride, float* work, int64_t batch, int64_t key_heads, int64_t value_heads,
                  int64_t head_k_dim, int64_t head_v_dim, int64_t conv_kernel, float eps, int dtype, void* stream);
 
+/* gsq_gdn_step over a sequence (prefill): `seq` tokens of each of `batch` rows, rows b * seq + t
+ * of qkv, z, ab and out (row strides in elements); ab holds the a and b projections of each
+ * token (2 * value_heads values: a then b, rounded to the dtype, e.g. one GEMM of the layer input
+ * with w_ab). Same arithmetic per token as gsq_gdn_step; the recurrent state stays in registers
+ * from the first token to the last and the convolution state ends at the sequence's last
+ * conv_kernel - 1 inputs. work: batch * seq * conv_dim floats. */
+int gsq_gdn_seq(const void* qkv, int64_t qkv_stride, const void* z, int64_t z_stride, const void* ab,
+                int64_t ab_stride, void* conv_state, const void* conv_w, const float* ssm_a, const float* dt_bias,
+                float* rec_state, const void* norm_w, void* out, int64_t out_stride, float* work, int64_t batch,
+                int64_t seq, int64_t key_heads, int64_t value_heads, int64_t head_k_dim, int64_t head_v_dim,
+                int64_t conv_kernel, float eps, int dtype, void* stream);
+
 /* One new token of gated grouped-query attention for `batch` rows (replaces the attention of a
  * full-attention layer at decode, qwen35.py's mlx-lm attention): per query head h (kv head
  * h / (heads / kv_heads)), q = round(rms_norm(q) * q_norm_w) from the q half of qg's head

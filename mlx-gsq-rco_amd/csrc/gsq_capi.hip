@@ -27,6 +27,7 @@ hipError_t launch_add_rms_norm(int dt, void* x, const void* delta, const void* w
                                float eps, hipStream_t s);
 hipError_t launch_swiglu(int dt, const void* gu, void* out, int64_t rows, int n, hipStream_t s);
 hipError_t launch_gdn_step(int dt, const GdnArgs& a, hipStream_t s);
+hipError_t launch_gdn_seq(int dt, const GdnArgs& a, hipStream_t s);
 hipError_t launch_attn_decode(int dt, const AttnArgs& a, hipStream_t s);
 int qmv_table_bytes(int qt);
 bool build_qmv_table(int qt, const uint16_t* grid16, const uint8_t* ksigns, std::vector<uint8_t>& out);
@@ -510,6 +511,34 @@ int gsq_gdn_step(const void* qkv, int64_t qkv_stride, const void* z, int64_t z_s
   a.K = (int)conv_kernel; a.hidden = (int)hidden; a.eps = eps;
   hipError_t e = launch_gdn_step(dtype, a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(GSQ_E_HIP, "gdn_step launch: %s", hipGetErrorString(e));
+  return GSQ_OK;
+}
+
+int gsq_gdn_seq(const void* qkv, int64_t qkv_stride, const void* z, int64_t z_stride, const void* ab,
+                int64_t ab_stride, void* conv_state, const void* conv_w, const float* ssm_a, const float* dt_bias,
+                float* rec_state, const void* norm_w, void* out, int64_t out_stride, float* work, int64_t batch,
+                int64_t seq, int64_t key_heads, int64_t value_heads, int64_t head_k_dim, int64_t head_v_dim,
+                int64_t conv_kernel, float eps, int dtype, void* stream) {
+  if (dtype != GSQ_F32 && dtype != GSQ_F16 && dtype != GSQ_BF16) return fail(GSQ_E_TYPE, "unsupported dtype code %d", dtype);
+  if (batch < 0 || batch > 65535 || seq < 0 || seq > 65535) return fail(GSQ_E_VALUE, "batch and seq must be 0..65535");
+  if (batch == 0 || seq == 0) return GSQ_OK;
+  if (key_heads <= 0 || value_heads <= 0 || value_heads % key_heads || value_heads > 65535)
+    return fail(GSQ_E_VALUE, "value heads must be a positive multiple of key heads (at most 65535)");
+  if (head_k_dim <= 0 || head_k_dim > 128 || head_k_dim % 4) return fail(GSQ_E_VALUE, "key head dim must be a multiple of 4 up to 128");
+  if (head_v_dim <= 0 || head_v_dim % 64 || head_v_dim > 256) return fail(GSQ_E_VALUE, "value head dim must be 64, 128, 192 or 256");
+  if (conv_kernel < 2 || conv_kernel > 8) return fail(GSQ_E_VALUE, "convolution kernel must be 2..8");
+  if (!qkv || !z || !ab || !conv_state || !conv_w || !ssm_a || !dt_bias || !rec_state || !norm_w || !out || !work)
+    return fail(GSQ_E_VALUE, "NULL pointer");
+  if (!(eps >= 0.f)) return fail(GSQ_E_VALUE, "eps must be >= 0");
+  GdnArgs a;
+  a.qkv = qkv; a.z = z; a.x = nullptr; a.w_ab = nullptr; a.conv = conv_state; a.conv_w = conv_w; a.ssm_a = ssm_a;
+  a.dt_bias = dt_bias; a.rec = rec_state; a.norm_w = norm_w; a.out = out; a.work = work;
+  a.qkv_stride = qkv_stride; a.z_stride = z_stride; a.x_stride = 0; a.out_stride = out_stride;
+  a.B = (int)batch; a.Hk = (int)key_heads; a.Hv = (int)value_heads; a.dk = (int)head_k_dim; a.dv = (int)head_v_dim;
+  a.K = (int)conv_kernel; a.hidden = 0; a.eps = eps;
+  a.S = (int)seq; a.ab = ab; a.ab_stride = ab_stride;
+  hipError_t e = launch_gdn_seq(dtype, a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(GSQ_E_HIP, "gdn_seq launch: %s", hipGetErrorString(e));
   return GSQ_OK;
 }
 

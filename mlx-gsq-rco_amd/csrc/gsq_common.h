@@ -127,9 +127,15 @@ struct GdnArgs {
   float* rec;          // [B, Hv, dk, dv] recurrent state
   const void* norm_w;  // [dv]
   void* out;           // [B] rows of Hv*dv (row stride out_stride)
-  float* work;         // [B, conv_dim] convolution outputs (after SiLU)
+  float* work;         // [B, conv_dim] convolution outputs (after SiLU); [B * S, conv_dim] for a sequence
   int64_t qkv_stride, z_stride, x_stride, out_stride;
   int B, Hk, Hv, dk, dv, K, hidden;
+  // a sequence of S tokens per batch row (the prefill kernels): rows b * S + t of qkv, z, out
+  // and of ab, the a and b projections (2 Hv values per row, activation dtype, row stride
+  // ab_stride), computed beforehand
+  int S = 1;
+  const void* ab = nullptr;
+  int64_t ab_stride = 0;
   float eps;
 };
 

@@ -339,6 +339,138 @@ __global__ void __launch_bounds__(1024) gdn_rec_kernel(GdnArgs a) {
   }
 }
 
+// ---- GatedDeltaNet over a sequence (prefill) ----------------------------------------------
+// The convolution of every (token, channel) at once (thread per channel, grid over tokens and
+// batch rows): the window of token t is the inputs t-K+1 .. t, from the state for those before
+// the sequence. The state is left alone here and advanced by gdn_rec_seq_kernel afterwards.
+template <int DT>
+__global__ void __launch_bounds__(256) gdn_conv_seq_kernel(GdnArgs a) {
+  using E = Elem<DT>;
+  using T = typename E::T;
+  const int conv_dim = 2 * a.Hk * a.dk + a.Hv * a.dv, K = a.K, S = a.S;
+  const int c = blockIdx.x * 256 + threadIdx.x, t = blockIdx.y, bb = blockIdx.z;
+  if (c >= conv_dim) return;
+  const T* cst = static_cast<const T*>(a.conv) + (int64_t)bb * (K - 1) * conv_dim + c;
+  const T* q = static_cast<const T*>(a.qkv) + (int64_t)bb * S * a.qkv_stride + c;
+  const T* cw = static_cast<const T*>(a.conv_w) + (int64_t)c * K;
+  float in[kGdnMaxK];
+#pragma unroll
+  for (int i = 0; i < kGdnMaxK; ++i) {
+    const int u = t - (K - 1) + i;  // input position (negative: from the state)
+    in[i] = i < K ? (u < 0 ? E::ld(cst + (int64_t)(K - 1 + u) * conv_dim) : E::ld(q + (int64_t)u * a.qkv_stride)) : 0.f;
+  }
+  float acc = in[0] * E::ld(cw);
+#pragma unroll
+  for (int i = 1; i < kGdnMaxK; ++i)
+    if (i < K) acc = acc + in[i] * E::ld(cw + i);
+  a.work[((int64_t)bb * S + t) * conv_dim + c] = silu_f(acc);
+}
+
+// The recurrence of value head h over the S tokens of batch row b, the state column held in
+// registers from the first token to the last; per token as gdn_rec_kernel (a and b read from
+// `ab` instead of being projected here). Also advances the convolution state of the head's
+// channels (v channels, and the q/k channels of key head h when h < Hk) to the last K-1 inputs.
+template <int DT>
+__global__ void __launch_bounds__(1024) gdn_rec_seq_kernel(GdnArgs a) {
+  using E = Elem<DT>;
+  using T = typename E::T;
+  constexpr int R = kGdnRowGroups, MAXR = kGdnMaxDk / R;
+  __shared__ float sq[kGdnMaxDk], sk[kGdnMaxDk], part[R][256], red[16];
+  __shared__ float4 red4[16];
+  const int h = blockIdx.x, bb = blockIdx.y, tid = threadIdx.x, nt = blockDim.x;
+  const int dk = a.dk, dv = a.dv, Hk = a.Hk, Hv = a.Hv, kh = h % Hk, S = a.S, K = a.K;
+  const int key_dim = Hk * dk, conv_dim = 2 * key_dim + Hv * dv;
+  const int g = tid / dv, j = tid - g * dv, rows = dk / R;
+  float* Sp = a.rec + ((int64_t)bb * Hv + h) * dk * dv + (int64_t)g * rows * dv + j;
+  float col[MAXR];
+#pragma unroll
+  for (int i = 0; i < MAXR; ++i) col[i] = Sp[(int64_t)min(i, rows - 1) * dv];
+  const float nw = E::ld(static_cast<const T*>(a.norm_w) + j);
+  const float dtb = a.dt_bias[h], sa = a.ssm_a[h];
+  const int qi = min(tid, dk - 1);
+  const float* kg = sk + g * rows;
+  const float* qg = sq + g * rows;
+  for (int t = 0; t < S; ++t) {
+    const int64_t row = (int64_t)bb * S + t;
+    const float* co = a.work + row * conv_dim;
+    const float v = co[2 * key_dim + h * dv + j];
+    const float qr = co[kh * dk + qi], kr = co[key_dim + kh * dk + qi];
+    const float zv = E::ld(static_cast<const T*>(a.z) + row * a.z_stride + h * dv + j);
+    const T* abr = static_cast<const T*>(a.ab) + row * a.ab_stride;
+    const float av = E::ld(abr + h) + dtb, bv = E::ld(abr + Hv + h);
+    const float4 r = block_sum4(make_float4(0.f, 0.f, tid < dk ? qr * qr : 0.f, tid < dk ? kr * kr : 0.f), red4);
+    if (tid < dk) {
+      sq[tid] = qr * (1.f / sqrtf(r.z / (float)dk + 1e-6f)) * (1.f / (float)dk);
+      sk[tid] = kr * (1.f / sqrtf(r.w / (float)dk + 1e-6f)) * (1.f / sqrtf((float)dk));
+    }
+    const float sp = av > 20.f ? av : log1pf(expf(av));
+    const float beta = 1.f / (1.f + expf(-bv));
+    const float decay = expf(sa * sp);
+    lds_sync();
+    float kv = 0.f;
+#pragma unroll
+    for (int i = 0; i < MAXR; ++i) {
+      const float s = col[i] * decay;
+      col[i] = s;
+      kv += (i < rows ? s : 0.f) * kg[min(i, rows - 1)];
+    }
+    part[g][j] = kv;
+    lds_sync();
+    kv = 0.f;
+    for (int q = 0; q < R; ++q) kv += part[q][j];
+    const float delta = (v - kv) * beta;
+    float o = 0.f;
+#pragma unroll
+    for (int i = 0; i < MAXR; ++i) {
+      const float s = col[i] + kg[min(i, rows - 1)] * delta;
+      col[i] = s;
+      o += (i < rows ? s : 0.f) * qg[min(i, rows - 1)];
+    }
+    lds_sync();  // every thread has read part[][j] for kv, and sq / sk for this token
+    part[g][j] = o;
+    lds_sync();
+    o = 0.f;
+    for (int q = 0; q < R; ++q) o += part[q][j];
+    const float ss = block_sum(g == 0 ? o * o : 0.f, red);
+    if (g == 0) {
+      const float rn = 1.f / sqrtf(ss / (float)dv + a.eps);
+      static_cast<T*>(a.out)[row * a.out_stride + h * dv + j] = E::mk(o * rn * nw * silu_f(zv));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < MAXR; ++i)
+    if (i < rows) Sp[(int64_t)i * dv] = col[i];
+  // the convolution state: the last K-1 inputs (from the sequence, or shifted from the state
+  // when the sequence is shorter), in ascending slots so an in-place shift reads before it writes
+  const int nch = dv + (h < Hk ? 2 * dk : 0);
+  T* cst = static_cast<T*>(a.conv) + (int64_t)bb * (K - 1) * conv_dim;
+  const T* qs = static_cast<const T*>(a.qkv) + (int64_t)bb * S * a.qkv_stride;
+  for (int idx = tid; idx < nch; idx += nt) {
+    const int c = idx < dv ? 2 * key_dim + h * dv + idx : (idx < dv + dk ? h * dk + idx - dv : key_dim + h * dk + idx - dv - dk);
+    for (int i = 0; i < K - 1; ++i) {
+      const int u = S - (K - 1) + i;
+      cst[(int64_t)i * conv_dim + c] = u < 0 ? cst[(int64_t)(K - 1 + u) * conv_dim + c] : qs[(int64_t)u * a.qkv_stride + c];
+    }
+  }
+}
+
+hipError_t launch_gdn_seq(int dt, const GdnArgs& a, hipStream_t s) {
+  const int conv_dim = 2 * a.Hk * a.dk + a.Hv * a.dv;
+  const dim3 cgrid((unsigned)((conv_dim + 255) / 256), (unsigned)a.S, (unsigned)a.B), rgrid((unsigned)a.Hv, (unsigned)a.B);
+  const dim3 rblock((unsigned)(kGdnRowGroups * a.dv));
+  if (dt == MD_F16) {
+    hipLaunchKernelGGL(gdn_conv_seq_kernel<MD_F16>, cgrid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL(gdn_rec_seq_kernel<MD_F16>, rgrid, rblock, 0, s, a);
+  } else if (dt == MD_BF16) {
+    hipLaunchKernelGGL(gdn_conv_seq_kernel<MD_BF16>, cgrid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL(gdn_rec_seq_kernel<MD_BF16>, rgrid, rblock, 0, s, a);
+  } else {
+    hipLaunchKernelGGL(gdn_conv_seq_kernel<MD_F32>, cgrid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL(gdn_rec_seq_kernel<MD_F32>, rgrid, rblock, 0, s, a);
+  }
+  return hipGetLastError();
+}
+
 // ---- gated attention, one new token -------------------------------------------------------
 // Workgroup (query head h, batch row b), 256 threads, kv head h / rep. In order, as the torch
 // formulation rounds: q = round(rms_norm(q) * w_q), k likewise with w_k, both rotated on their

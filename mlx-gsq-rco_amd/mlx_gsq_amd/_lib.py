@@ -40,6 +40,8 @@ EXPORTS = {
                                _I64, _I64, _I64, _I64, _F32, _VP, _I64, _I32, _VP]),
     "gsq_gdn_step": (_I32, [_VP, _I64, _VP, _I64, _VP, _I64, _VP, _I64, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I64,
                             _VP, _I64, _I64, _I64, _I64, _I64, _I64, _F32, _I32, _VP]),
+    "gsq_gdn_seq": (_I32, [_VP, _I64, _VP, _I64, _VP, _I64, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I64, _VP, _I64,
+                           _I64, _I64, _I64, _I64, _I64, _I64, _F32, _I32, _VP]),
     "gsq_last_error": (ctypes.c_char_p, []),
 }
 

@@ -178,13 +178,18 @@ class GatedDeltaNet(torch.nn.Module):
             first, conv_out = first
         qkvz = self.in_proj_qkvz(x) if first is None else first
         qkv, z = qkvz[..., :a_.conv_dim], qkvz[..., a_.conv_dim:]   # (B, S, conv_dim), (B, S, Hv * dv)
-        if x.is_cuda:  # the a / b projections happen inside the fused step
+        if x.is_cuda:
             from ..runtime.kernels import model_ops
-            outs = [model_ops.gdn_step(qkv[:, t], z[:, t], x[:, t], self.w_ab, cache.conv[self.layer], self.conv_w,
-                                       self.ssm_a, self.dt_bias, cache.rec[self.layer], self.norm_w,
-                                       key_heads=hk, value_heads=hv, head_k_dim=dk, head_v_dim=dv,
-                                       eps=a_.rms_norm_eps, conv_out=conv_out) for t in range(S)]
-            out = outs[0][:, None] if S == 1 else torch.stack(outs, dim=1)
+            if S == 1:  # the a / b projections happen inside the fused step
+                out = model_ops.gdn_step(qkv[:, 0], z[:, 0], x[:, 0], self.w_ab, cache.conv[self.layer], self.conv_w,
+                                         self.ssm_a, self.dt_bias, cache.rec[self.layer], self.norm_w,
+                                         key_heads=hk, value_heads=hv, head_k_dim=dk, head_v_dim=dv,
+                                         eps=a_.rms_norm_eps, conv_out=conv_out)[:, None]
+            else:  # a sequence: a / b of all tokens in one product, then one recurrence launch
+                out = model_ops.gdn_seq(qkv, z, F.linear(x, self.w_ab), cache.conv[self.layer], self.conv_w,
+                                        self.ssm_a, self.dt_bias, cache.rec[self.layer], self.norm_w,
+                                        key_heads=hk, value_heads=hv, head_k_dim=dk, head_v_dim=dv,
+                                        eps=a_.rms_norm_eps)
             return self.out_proj(out)
         z = z.view(B, S, hv, dv)
         a, b = F.linear(x, self.w_ab).float().split(hv, dim=-1)  # (B, S, Hv) each

@@ -105,6 +105,43 @@ def gdn_step(qkv, z, x, w_ab, conv_state, conv_w, ssm_a, dt_bias, rec_state, nor
     return out
 
 
+def gdn_seq(qkv, z, ab, conv_state, conv_w, ssm_a, dt_bias, rec_state, norm_w, *, key_heads: int, value_heads: int,
+            head_k_dim: int, head_v_dim: int, eps: float):
+    """``gdn_step`` over S tokens of B rows (prefill): qkv (B, S, conv_dim), z (B, S, Hv*dv) and ab
+    (B, S, 2 Hv: the a and b projections, a then b) with unit stride along the last axis and the
+    (B, S) rows at one stride each. The states advance over all S tokens. Returns (B, S, Hv*dv)."""
+    dev = _on_gpu(qkv, z, ab, conv_state, conv_w, ssm_a, dt_bias, rec_state, norm_w)
+    B, S = qkv.shape[0], qkv.shape[1]
+    rows = []
+    for t in (qkv, z, ab):
+        if (t.dim() != 3 or tuple(t.shape[:2]) != (B, S) or t.stride(2) != 1 or t.dtype != qkv.dtype
+                or (S > 1 and t.stride(0) != S * t.stride(1))):
+            raise ValueError("qkv, z and ab must be (B, S, n) of one dtype, unit inner stride, rows at one stride")
+        rows.append(t.stride(1))
+    for t in (conv_state, conv_w, norm_w):
+        if t.dtype != qkv.dtype or not t.is_contiguous():
+            raise ValueError("conv_state, conv_w and norm_w must be contiguous in the activation dtype")
+    for t in (ssm_a, dt_bias, rec_state):
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError("ssm_a, dt_bias and rec_state must be contiguous float32")
+    conv_dim = 2 * key_heads * head_k_dim + value_heads * head_v_dim
+    K = conv_w.shape[-1]
+    if (qkv.shape[2] != conv_dim or z.shape[2] != value_heads * head_v_dim or ab.shape[2] != 2 * value_heads
+            or tuple(conv_state.shape) != (B, K - 1, conv_dim) or conv_w.numel() != conv_dim * K
+            or tuple(rec_state.shape) != (B, value_heads, head_k_dim, head_v_dim) or norm_w.numel() != head_v_dim
+            or ssm_a.numel() != value_heads or dt_bias.numel() != value_heads):
+        raise ValueError("GatedDeltaNet tensor shapes do not match the head configuration")
+    out = torch.empty(B, S, value_heads * head_v_dim, dtype=qkv.dtype, device=dev)
+    work = torch.empty(B * S, conv_dim, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _lib.check(_lib.lib().gsq_gdn_seq(
+            qkv.data_ptr(), rows[0], z.data_ptr(), rows[1], ab.data_ptr(), rows[2], conv_state.data_ptr(),
+            conv_w.data_ptr(), ssm_a.data_ptr(), dt_bias.data_ptr(), rec_state.data_ptr(), norm_w.data_ptr(),
+            out.data_ptr(), out.stride(1), work.data_ptr(), B, S, key_heads, value_heads, head_k_dim, head_v_dim, K,
+            float(eps), _dt(qkv), _lib.stream_handle(dev)), "gdn_seq")
+    return out
+
+
 # caches at least this long split the positions into chunks (one workgroup each, then a combine)
 ATTN_SPLIT_MIN_LEN = 2048
 ATTN_CHUNK = 256

@@ -138,9 +138,10 @@ class _Given(torch.nn.Module):
 
 @pytest.mark.gpu
 def test_gpu_fused_ops_match_torch_formulation():
-    """The fused kernels (add + RMSNorm, SwiGLU, GatedDeltaNet token) against the model's torch
-    formulation run on the CPU in float32, at the 27B head shapes (16 key / 48 value heads of
-    128, conv 4) for 3 tokens of 2 batch rows."""
+    """The fused kernels (add + RMSNorm, SwiGLU, GatedDeltaNet token and sequence) against the
+    model's torch formulation run on the CPU in float32, at the 27B head shapes (16 key / 48
+    value heads of 128, conv 4): 3 single tokens, then sequences of 5 and 2 tokens, for 2 batch
+    rows."""
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     from mlx_gsq_amd.models.qwen35 import GatedDeltaNet, Qwen35Args, Qwen35Cache, rms_norm
@@ -186,6 +187,20 @@ def test_gpu_fused_ops_match_torch_formulation():
         assert rel_l2(got.numpy(), want.numpy()) <= 5e-3, t
         assert rel_l2(gcache.rec[0].cpu().numpy(), ccache.rec[0].numpy()) <= 1e-3, t
         assert torch.equal(gcache.conv[0].cpu().float(), ccache.conv[0])
+    # then a 5-token sequence at once (the prefill kernels: a / b by one product, the recurrence
+    # over all tokens in one launch), and a 2-token one (shorter than the convolution window)
+    for S in (5, 2):
+        qkv = torch.randn(B, S, C, generator=g).half()
+        z = torch.randn(B, S, a.value_dim, generator=g).half()
+        h = torch.randn(B, S, 64, generator=g).half()
+        cpu.in_proj_qkvz.value = torch.cat([qkv, z], dim=-1).float()
+        gpu.in_proj_qkvz.value = torch.cat([qkv, z], dim=-1).to(dev)
+        want = cpu(h.float(), ccache)
+        got = gpu(h.to(dev), gcache).float().cpu()
+        assert torch.isfinite(got).all()
+        assert rel_l2(got.numpy(), want.numpy()) <= 5e-3, S
+        assert rel_l2(gcache.rec[0].cpu().numpy(), ccache.rec[0].numpy()) <= 1e-3, S
+        assert torch.equal(gcache.conv[0].cpu().float(), ccache.conv[0]), S
 
 
 @pytest.mark.gpu

@@ -249,17 +249,28 @@ QMM_ROWS = (182, 512, 2048)
 
 def run_qmm(device, reps=10):
     """QMM for IQ3_S and Q6_K at both 27B shapes, M in {182, 512, 2048} rows of fp16
-    activations, fp32 output; time per launch from HIP events on the launch stream."""
+    activations, fp32 output; time per launch from HIP events on the launch stream.
+
+    Beside each product, ``dense_fp16_library`` times the vendor library's dense fp16 GEMM
+    (torch.mm with fp32 output, hipBLASLt on ROCm) on the same weights already dequantized to
+    fp16, the operand the QMM rounds to: what a plain GEMM reaches on these shapes with no
+    dequantization in it at all, for scale."""
     import torch
     from mlx_gsq_amd import _lib
     from mlx_gsq_amd.formats import TYPE_IDS
     lib = _lib.lib()
     out = {}
+    dense = {}
     stream = torch.cuda.current_stream(device)
     for q in QMM_TYPES:
         _lib.ensure_tables(q, device)
         for (n, k) in QMM_SHAPES:
             packed = make_device_packed(q, n, k, seed=77, device=device)
+            w32 = torch.empty(n * k, device=device, dtype=torch.float32)
+            assert lib.gsq_dequant(TYPE_IDS[q], packed.data_ptr(), n * k // 256, w32.data_ptr(),
+                                   stream.cuda_stream) == 0, lib.gsq_last_error()
+            w16 = w32.view(n, k).half()
+            del w32
             for m in QMM_ROWS:
                 x = torch.randn(m, k, device=device).half()
                 y = torch.empty(m, n, device=device, dtype=torch.float32)
@@ -276,10 +287,24 @@ def run_qmm(device, reps=10):
                 tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
                 out[f"{q} {n}x{k} M={m}"] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1),
                                               "frac": round(tf / FP16_PEAK_TFLOPS, 4)}
+                def library_gemm():
+                    torch.mm(x, w16.t(), out_dtype=torch.float32)
+                    return 0
+
+                lib_us = _time_launches(library_gemm, stream, reps)
+                ltf = 2.0 * m * n * k / (lib_us * 1e-6) / 1e12
+                dense[f"{q} {n}x{k} M={m}"] = {"us": round(lib_us, 1), "TFLOP/s": round(ltf, 1),
+                                                "frac": round(ltf / FP16_PEAK_TFLOPS, 4),
+                                                "qmm_time_over_library": round(ms * 1e3 / lib_us, 3)}
                 del x, y
-            del packed
+            del packed, w16
     m512 = [v["frac"] for kk, v in out.items() if kk.endswith("M=512")]
     out["mean_frac_M512"] = round(sum(m512) / len(m512), 4)
+    d512 = [v["frac"] for kk, v in dense.items() if kk.endswith("M=512")]
+    dense["mean_frac_M512"] = round(sum(d512) / len(d512), 4)
+    dense["what"] = ("torch.mm(x fp16, W fp16 dequantized beforehand, out_dtype=float32): the vendor "
+                     "GEMM (hipBLASLt) with no dequantization, same shapes, HIP events")
+    out["dense_fp16_library"] = dense
     return out
 
 

@@ -112,6 +112,7 @@ struct QmmTuning {
   int small_waves;
   int small_nb;
   int small_min_cols;
+  int order;  // tiled kernel's tile order: 2 = activation tile fastest, else weight tile fastest
 };
 
 // Arguments of one GatedDeltaNet token step (gsq_gdn_step; kernels in gsq_model.hip).

@@ -7,15 +7,15 @@
 
 namespace gsq {
 
-// GSQ_QMM_TUNING="mf,min_cols,waves,small_max_m,small_waves,small_nb,small_min_cols" (a
+// GSQ_QMM_TUNING="mf,min_cols,waves,small_max_m,small_waves,small_nb,small_min_cols,order" (a
 // prefix may be given; 0 keeps a field's default) overrides the launch plans, read once at
 // library load, for measuring plans without a rebuild.
 static QmmTuning qmm_tuning_from_env() {
-  QmmTuning t = {0, 0, 0, 0, 0, 0, 0};
+  QmmTuning t = {0, 0, 0, 0, 0, 0, 0, 0};
   if (const char* s = std::getenv("GSQ_QMM_TUNING")) {
-    int v[7] = {0, 0, 0, 0, 0, 0, 0};
-    std::sscanf(s, "%d,%d,%d,%d,%d,%d,%d", &v[0], &v[1], &v[2], &v[3], &v[4], &v[5], &v[6]);
-    t = {v[0], v[1], v[2], v[3], v[4], v[5], v[6]};
+    int v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    std::sscanf(s, "%d,%d,%d,%d,%d,%d,%d,%d", &v[0], &v[1], &v[2], &v[3], &v[4], &v[5], &v[6], &v[7]);
+    t = {v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]};
   }
   return t;
 }

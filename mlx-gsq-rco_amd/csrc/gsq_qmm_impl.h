@@ -25,8 +25,9 @@
 //    (17408 = 17 * 1024 rows) still fill the chip. A tile split between workgroups is
 //    finished by the last one to arrive (per-tile arrival counter), which sums the fp32
 //    partials in a fixed order (deterministic) and writes y.
-//  * workgroups are renumbered so that consecutive work (same weight rows, neighbouring
-//    activation tiles and K ranges) lands on one XCD and shares its L2.
+//  * tiles are numbered weight tile fastest and workgroups renumbered so that consecutive work
+//    (one activation tile, neighbouring weight tiles and K ranges) lands on one XCD and shares
+//    its L2.
 // fp32 / bf16 activations use the generic kernel below.
 #pragma once
 #include <type_traits>
@@ -183,6 +184,8 @@ struct QmmMfmaArgs {
   int nblk;              // superblocks per row (K / 256)
   long long row_bytes;
   int mt;                // activation tiles
+  int nt;                // weight tiles (kQBN rows)
+  int nfast;             // tile t = (activation tile t / nt, weight tile t % nt), else (t % mt, t / mt)
   int units;             // tiles * nblk
   int G;                 // workgroups
   int xcd_remap;         // G is a multiple of 8
@@ -240,11 +243,11 @@ __device__ __forceinline__ void qmm_store_tile(void* y, int ydt, int M, int N, c
 template <int NX, int BM, int LX>
 struct QmmXIter {
   const _Float16* x;
-  int M, K, mt, nblk;
+  int M, K, mt, nt, nfast, nblk;
   int q, t, c, b;
   const _Float16* row[NX];
   __device__ __forceinline__ void rows(int wave, int lane) {
-    const int m0 = (t % mt) * BM;
+    const int m0 = (nfast ? t / nt : t % mt) * BM;
 #pragma unroll
     for (int i = 0; i < NX; ++i) {
       const int s = (wave * NX + i) * 64 + lane;
@@ -253,11 +256,14 @@ struct QmmXIter {
       row[i] = x + (long long)min(m0 + m, M - 1) * K + 8 * o;
     }
   }
-  __device__ __forceinline__ void init(const _Float16* x_, int M_, int K_, int mt_, int nblk_, int ub, int wave, int lane) {
+  __device__ __forceinline__ void init(const _Float16* x_, int M_, int K_, int mt_, int nt_, int nfast_, int nblk_, int ub,
+                                       int wave, int lane) {
     x = x_;
     M = M_;
     K = K_;
     mt = mt_;
+    nt = nt_;
+    nfast = nfast_;
     nblk = nblk_;
     q = 0;
     b = 0;
@@ -302,6 +308,9 @@ __global__ void __launch_bounds__(64 * WV, 1) qmm_mfma_kernel(QmmMfmaArgs args) 
   const _Float16* const xg = args.x;
   void* const yg = args.y;
   const int M = args.M, N = args.N, K = args.K, ydt = args.y_dtype, nblk = args.nblk, mt = args.mt;
+  const int nt = args.nt, nfast = args.nfast;
+  auto tile_m = [&](int t) { return nfast ? t / nt : t % mt; };
+  auto tile_n = [&](int t) { return nfast ? t % nt : t / mt; };
   const int units = args.units, G = args.G, xcd = args.xcd_remap, tbl_bytes = args.tbl_bytes;
   const long long row_bytes = args.row_bytes;
   const uint8_t* const tblg = args.tbl;
@@ -337,7 +346,7 @@ __global__ void __launch_bounds__(64 * WV, 1) qmm_mfma_kernel(QmmMfmaArgs args) 
 
   // activation stages are issued in order by an iterator
   QmmXIter<NX, BM, LX> xi;
-  xi.init(xg, M, K, mt, nblk, ub, wave, lane);
+  xi.init(xg, M, K, mt, nt, nfast, nblk, ub, wave, lane);
   // weight column cl (local index): the wave's RW superblocks, granule e of the column at
   // byte 16e (row e / GR, granule e % GR of that row); granules past a row's last one reload
   // its last granule, and lanes past the last row (whole instructions) reload the last row's,
@@ -345,7 +354,7 @@ __global__ void __launch_bounds__(64 * WV, 1) qmm_mfma_kernel(QmmMfmaArgs args) 
   auto issue_w = [&](int cl) {
     const int u = ub + cl;
     const int tile = u / nblk, c = u - tile * nblk;
-    const int n0 = (tile / mt) * kQBN + wave * RW;
+    const int n0 = tile_n(tile) * kQBN + wave * RW;
     uint8_t* buf = wring + (cl & 1) * Geo::kCol;
 #pragma unroll
     for (int i = 0; i < GW; ++i) {
@@ -391,7 +400,7 @@ __global__ void __launch_bounds__(64 * WV, 1) qmm_mfma_kernel(QmmMfmaArgs args) 
   auto col_delta = [&](int q, uint32_t (&dl)[NB]) {
     const int u = ub + (q >> 3);
     const int tl = u / nblk, c = u - tl * nblk;
-    const int n0 = (tl / mt) * kQBN + wave * RW;
+    const int n0 = tile_n(tl) * kQBN + wave * RW;
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       const int n = min(n0 + 16 * j + (lane & 15), N - 1);
@@ -431,7 +440,7 @@ __global__ void __launch_bounds__(64 * WV, 1) qmm_mfma_kernel(QmmMfmaArgs args) 
     const int u0 = ub + (q0 >> 3);
     const int tile = u0 / nblk;
     const int q1 = q0 + 8 * (min(ue, (tile + 1) * nblk) - u0);
-    const int m0 = (tile % mt) * BM, n0 = (tile / mt) * kQBN + wave * RW;
+    const int m0 = tile_m(tile) * BM, n0 = tile_n(tile) * kQBN + wave * RW;
     float4_t acc[MF][NB];
 #pragma unroll
     for (int i = 0; i < MF; ++i)
@@ -725,7 +734,11 @@ static hipError_t launch_mfma(QmmMfmaArgs& a, int num_cus, const QmmWorkspace& w
   for (;;) {
     const int bm = 16 * mf;
     a.mt = (a.M + bm - 1) / bm;
-    const long long units = (long long)a.mt * (((long long)a.N + kQBN - 1) / kQBN) * a.nblk;
+    a.nt = (int)((a.N + kQBN - 1) / kQBN);
+    // weight tile fastest: the workgroups of one XCD (consecutive units) share an activation
+    // tile in its L2 (3-6% faster at M = 2048 than activation tile fastest)
+    a.nfast = g_qmm_tuning.order == 2 ? 0 : 1;
+    const long long units = (long long)a.mt * a.nt * a.nblk;
     if (units >= (1ll << 31)) return hipErrorInvalidValue;
     a.units = (int)units;
     const int gmax = (a.units + min_cols - 1) / min_cols;

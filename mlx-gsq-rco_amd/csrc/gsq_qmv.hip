@@ -87,31 +87,18 @@ __device__ __forceinline__ void dacc(uint32_t w, const XReg<MR, XS, NS>& x, int 
   }
 }
 
-// K-quant codes (small unsigned integers q < 1024, masked into the low bits of each fp16 lane)
-// become exact normal fp16 integers for v_dot2_f32_f16: (1024 + q) by OR-ing in the exponent,
-// then the 1024 removed by one v_pk_add_f16 (exact). The bare bits would be the fp16
-// subnormals q * 2^-24, but v_dot2_f32_f16 does not form products of subnormal operands
-// exactly on gfx950 (measured: relative errors up to ~5e-5 per product, far more once
-// accumulated), while every product of normal fp16 values is exact in fp32.
-template <bool XS>
-__device__ __forceinline__ uint32_t enc_codes(uint32_t codes) {
-  const half2_t r = __builtin_bit_cast(half2_t, codes | 0x64006400u) - (half2_t){(_Float16)1024.f, (_Float16)1024.f};
-  return __builtin_bit_cast(uint32_t, r);
-}
-template <bool XS>
-__device__ __forceinline__ constexpr float enc_scale() { return 1.f; }
-// The same for codes already carrying 1024's exponent byte (a byte permute that puts 0x64 above
-// each code byte): only the exact subtraction of 1024 remains.
+// Q6_K's 6-bit codes, each under 1024's exponent byte (a byte permute puts 0x64 above each code
+// byte), become exact normal fp16 integers for v_dot2_f32_f16 by one exact v_pk_add_f16 that
+// removes the 1024. The bare code bits would be the fp16 subnormals q * 2^-24, but
+// v_dot2_f32_f16 does not form products of subnormal operands exactly on gfx950 (measured:
+// relative errors up to ~5e-5 per product, far more once accumulated), while every product of
+// normal fp16 values is exact in fp32.
 __device__ __forceinline__ uint32_t unbias_codes(uint32_t biased) {
   const half2_t r = __builtin_bit_cast(half2_t, biased) - (half2_t){(_Float16)1024.f, (_Float16)1024.f};
   return __builtin_bit_cast(uint32_t, r);
 }
 
-// Both 16-bit halves shifted right by 8 (v_pk_lshrrev_b16): bytes 1 and 3 move to 0 and 2.
 typedef unsigned short ushort2_t __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint32_t pk_shr8(uint32_t v) {
-  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(ushort2_t, v) >> (ushort2_t){8, 8});
-}
 
 // Views of an LDS table of 8- or 16-byte entries read as scalar words (the compiler merges
 // them into ds_read_b64/b128). Vector-typed LDS loads would make the compiler drain every
@@ -158,6 +145,13 @@ struct SignBits {
 // codebook values.
 template <int T> struct Qmv;
 
+// K-quant codes of at most 4 bits go into the top mantissa bits of fp16 1.0: a 4-bit code q at
+// mantissa bits 6-9 is 1 + q/16, a 2-bit code at bits 8-9 is 1 + q/4. Each is a normal fp16
+// number, so every product with an fp16 activation is exact in v_dot2_f32_f16 (which does not
+// form products of subnormal operands exactly on gfx950), and placing a code pair costs one
+// shift and one and-or, with no subtraction. The 1 is removed per group through the activation
+// sums: sum x (1 + q/16) = S + sum x q / 16, where S and sum x q / 16 are of the same size
+// (about one bit cancels, against ten for codes below an exponent of 1024).
 template <> struct Qmv<Q4_K> {
   static constexpr int kPair = PAIR_K;
   static constexpr int kSums = 1;
@@ -176,24 +170,23 @@ template <> struct Qmv<Q4_K> {
     const uint32_t mn = lo ? (B & 63u) : ((C >> 4) | ((B >> 6) << 4));
     uint32_t q[8];
     lds_words<8, A4>(buf, off + 16 + 32 * (g >> 1), q);
-    // odd groups use the high nibbles: mask them in place (value x 16, folded into the scale)
+    // the group's nibble of bytes 0, 2 (pair 2k) and bytes 1, 3 (pair 2k + 1) of word k moved to
+    // bits 6-9 of each half: even groups use the low nibbles, odd groups the high ones
     const bool odd = g & 1;
-    const uint32_t M = odd ? 0x00F000F0u : 0x000F000Fu;
+    const uint32_t sa = odd ? 2u : 6u, sb = odd ? 6u : 2u;
     float acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = 0.f;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      dacc<MR, XS>(enc_codes<XS>(q[k] & M), x, 2 * k, acc);
-      dacc<MR, XS>(enc_codes<XS>(pk_shr8(q[k]) & M), x, 2 * k + 1, acc);
+      dacc<MR, XS>(((q[k] << sa) & 0x03C003C0u) | 0x3C003C00u, x, 2 * k, acc);
+      dacc<MR, XS>(((q[k] >> sb) & 0x03C003C0u) | 0x3C003C00u, x, 2 * k + 1, acc);
     }
-    const float s = d * (float)sc * (odd ? enc_scale<XS>() * 0.0625f : enc_scale<XS>());
-    const float o = -(dmin * (float)mn);
+    // d sc sum x q - dmin mn S = 16 d sc acc - (16 d sc + dmin mn) S
+    const float s = 16.f * d * (float)sc;
+    const float o = -(s + dmin * (float)mn);
 #pragma unroll
-    for (int m = 0; m < MR; ++m) {
-      const float xs = x.s8[m][0];
-      out[m] += s * acc[m] + o * xs;
-    }
+    for (int m = 0; m < MR; ++m) out[m] += s * acc[m] + o * x.s8[m][0];
   }
 };
 
@@ -210,23 +203,22 @@ template <> struct Qmv<Q2_K> {
     const float d = h2f(dd & 0xFFFFu), dmin = h2f(dd >> 16);
     uint32_t q[8];
     lds_words<8, A4>(buf, off + 16 + 32 * (g >> 2), q);
-    const uint32_t sh = 2u * (g & 3);
+    // the group's 2-bit field of bytes 0, 2 and of bytes 1, 3 moved to bits 8-9 of each half
+    const uint32_t sh = 2u * (g & 3), sa = 8u - sh;
     float a0[MR], a1[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) { a0[m] = 0.f; a1[m] = 0.f; }
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      // 2-bit values are small next to the 1024 magic offset: remove it exactly in fp16
-      // before the dot so the fp32 sums carry no cancellation.
-      const uint32_t v = q[k] >> sh;
-      const uint32_t A = enc_codes<XS>(v & 0x00030003u);
-      const uint32_t B = enc_codes<XS>((v >> 8) & 0x00030003u);
+      const uint32_t A = ((q[k] << sa) & 0x03000300u) | 0x3C003C00u;
+      const uint32_t B = ((q[k] >> sh) & 0x03000300u) | 0x3C003C00u;
       if (k < 4) { dacc<MR, XS>(A, x, 2 * k, a0); dacc<MR, XS>(B, x, 2 * k + 1, a0); }
       else { dacc<MR, XS>(A, x, 2 * k, a1); dacc<MR, XS>(B, x, 2 * k + 1, a1); }
     }
-    const float s0 = d * (float)(sm & 15u) * enc_scale<XS>(), s1 = d * (float)((sm >> 8) & 15u) * enc_scale<XS>();
-    const float o0 = -(dmin * (float)((sm >> 4) & 15u));
-    const float o1 = -(dmin * (float)((sm >> 12) & 15u));
+    // per half h: d sc_h sum x q - dmin mn_h S_h = 4 d sc_h acc_h - (4 d sc_h + dmin mn_h) S_h
+    const float s0 = 4.f * d * (float)(sm & 15u), s1 = 4.f * d * (float)((sm >> 8) & 15u);
+    const float o0 = -(s0 + dmin * (float)((sm >> 4) & 15u));
+    const float o1 = -(s1 + dmin * (float)((sm >> 12) & 15u));
 #pragma unroll
     for (int m = 0; m < MR; ++m)
       out[m] += s0 * a0[m] + s1 * a1[m] + o0 * x.s8[m][0] + o1 * x.s8[m][1];
@@ -276,8 +268,7 @@ template <> struct Qmv<Q6_K> {
     const float s0 = d * (float)(int)(int8_t)(sc2 & 0xFFu), s1 = d * (float)(int)(int8_t)(sc2 >> 8);
 #pragma unroll
     for (int m = 0; m < MR; ++m)
-      out[m] += s0 * (enc_scale<XS>() * a0[m] - 32.f * x.s8[m][0]) +
-                s1 * (enc_scale<XS>() * a1[m] - 32.f * x.s8[m][1]);
+      out[m] += s0 * (a0[m] - 32.f * x.s8[m][0]) + s1 * (a1[m] - 32.f * x.s8[m][1]);
   }
 };
 

@@ -794,6 +794,7 @@ def main():
     ap.add_argument("--copy-bytes", type=int, default=0, help="run only a plain copy of this many bytes")
     ap.add_argument("--qmm-profile-case", default=None, help="TYPE:MxNxK, launch only that QMM product")
     ap.add_argument("--model-decode", action="store_true", help="run only the Qwen3.5-hybrid decode-step leg")
+    ap.add_argument("--embedding-case", type=int, default=0, help="run only the embedding gather of this many ids")
     ap.add_argument("--reps", type=int, default=20)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -802,7 +803,7 @@ def main():
         sys.exit(2)
     # the CPU baseline runs first, in fresh worker processes, before anything touches the GPU
     cpu = None if (args.no_cpu or args.copy_bytes or args.profile_case or args.qmm_profile_case
-                   or args.model_decode) else cpu_baseline()
+                   or args.model_decode or args.embedding_case) else cpu_baseline()
     import torch
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
@@ -814,6 +815,10 @@ def main():
         return
     if args.qmm_profile_case:
         qmm_profile_case(args.qmm_profile_case, args.reps, device)
+        return
+    if args.embedding_case:
+        print(json.dumps({"embedding": run_embedding(device, tokens=(args.embedding_case,), reps=args.reps)}),
+              flush=True)
         return
     if args.model_decode:
         from mlx_gsq_amd import tables

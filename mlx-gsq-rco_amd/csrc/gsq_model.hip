@@ -508,48 +508,108 @@ __device__ __forceinline__ void attn_norm_rope(const typename Elem<DT>::T* src, 
   __syncthreads();
 }
 
+// Two block sums at once (one pair of LDS barriers); red holds at least 16 floats.
+__device__ __forceinline__ float2 block_sum2(float a, float b, float* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  a = wave_sum(a);
+  b = wave_sum(b);
+  lds_sync();
+  if (lane == 0) { red[wave] = a; red[8 + wave] = b; }
+  lds_sync();
+  float sa = 0.f, sb = 0.f;
+  for (int i = 0; i < nw; ++i) { sa += red[i]; sb += red[8 + i]; }
+  return make_float2(sa, sb);
+}
+
+// Single-token gated attention, one workgroup per (query head, batch row). Every global load
+// of the step is issued at the start: q, its gate, the new k and v, both norm weights, the
+// rotary frequency, the first pass of cached K rows (a quarter row per thread, positions
+// 0..63) and the first 8 cached V rows; the barriers wait on LDS only, so a short context costs
+// one memory round trip. The arithmetic (norms, rotary, scores, softmax, V sums) is the same
+// as, and in the same order as, the separate steps it replaces.
 template <int DT>
 __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
   using E = Elem<DT>;
   using T = typename E::T;
   extern __shared__ float sc[];  // scores of positions 0..pos
-  __shared__ float sq[256], sk[256], sv[256], red[16];
+  __shared__ float sq[256], sk[256], red[16];
   const int h = blockIdx.x, bb = blockIdx.y, t = threadIdx.x;
-  const int hd = a.hd, rep = a.H / a.Hkv, kvh = h / rep;
+  const int hd = a.hd, rd = a.rd, rep = a.H / a.Hkv, kvh = h / rep;
   const int p = (int)a.pos[0];
   const T* qg = static_cast<const T*>(a.qg) + (int64_t)bb * a.qg_stride + (int64_t)h * 2 * hd;
-  attn_norm_rope<DT>(qg, static_cast<const T*>(a.q_norm_w), a, p, sq, red);
-  attn_norm_rope<DT>(static_cast<const T*>(a.k) + (int64_t)bb * a.k_stride + (int64_t)kvh * hd,
-                     static_cast<const T*>(a.k_norm_w), a, p, sk, red);
-  const T* vr = static_cast<const T*>(a.v) + (int64_t)bb * a.v_stride + (int64_t)kvh * hd;
-  if (t < hd) sv[t] = E::ld(vr + t);
+  const T* kn = static_cast<const T*>(a.k) + (int64_t)bb * a.k_stride + (int64_t)kvh * hd;
+  const T* vn = static_cast<const T*>(a.v) + (int64_t)bb * a.v_stride + (int64_t)kvh * hd;
   const int64_t base = ((int64_t)bb * a.Hkv + kvh) * a.L * hd;
   const T* K = static_cast<const T*>(a.kc) + base;
   const T* V = static_cast<const T*>(a.vc) + base;
-  if (h % rep == 0 && t < hd) {
-    static_cast<T*>(a.kc)[base + (int64_t)p * hd + t] = E::mk(sk[t]);
-    static_cast<T*>(a.vc)[base + (int64_t)p * hd + t] = E::mk(sv[t]);
-  }
-  __syncthreads();
+  const bool th = t < hd;
+  const float xq = th ? E::ld(qg + t) : 0.f, gate = th ? E::ld(qg + hd + t) : 0.f;
+  const float xk = th ? E::ld(kn + t) : 0.f, xv = th ? E::ld(vn + t) : 0.f;
+  const float wq = th ? E::ld(static_cast<const T*>(a.q_norm_w) + t) : 0.f;
+  const float wk = th ? E::ld(static_cast<const T*>(a.k_norm_w) + t) : 0.f;
+  const int hr = rd / 2;
+  const double fr = t < rd ? a.inv_freq[t < hr ? t : t - hr] : 0.0;
   // scores: 64 positions per pass, four threads per position (a quarter of hd each); with hd a
   // multiple of 32 and an aligned cache, a thread's quarter row is read as 8-value chunks, all
-  // issued before the first use
-  const float scale = 1.f / sqrtf((float)hd);
-  const int quarter = hd / 4, pi = t >> 2, qd = t & 3, nchunk = quarter >> 3;
+  // issued before the first use (the first pass's here)
+  const int quarter = hd / 4, pi = t >> 2, qd = t & 3, nchunk = quarter >> 3, d0 = qd * quarter;
   const bool vec = (hd & 31) == 0 && (reinterpret_cast<uintptr_t>(K) & 15) == 0;
+  Vec8<DT> kv[8];  // quarter <= 64: at most 8 chunks (later ones re-read the last)
+  const bool k_early = vec && pi < p;  // position pi of the first pass, a cached one
+  if (k_early) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) kv[c].load(K + (int64_t)pi * hd + d0 + 8 * min(c, nchunk - 1));
+  }
+  float v8[8];  // V rows 0..7 of this thread's column, when the first block of 8 is whole
+  const bool v_early = th && p >= 8;
+  if (v_early) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v8[u] = E::ld(V + (int64_t)u * hd + t);
+  }
+  // q and k: RMS norm (one pair of barriers for both sums), then the partial rotary
+  const float2 ss = block_sum2(xq * xq, xk * xk, red);
+  const float rq = 1.f / sqrtf(ss.x / (float)hd + a.eps), rk = 1.f / sqrtf(ss.y / (float)hd + a.eps);
+  float nq = 0.f, nk = 0.f;
+  if (th) {
+    const T q1 = E::mk(xq * rq * wq), k1 = E::mk(xk * rk * wk);
+    nq = E::ld(&q1);
+    nk = E::ld(&k1);
+    sq[t] = nq;
+    sk[t] = nk;
+  }
+  lds_sync();
+  if (t < rd) {
+    const double ang = (double)p * fr;
+    const float c = (float)cos(ang), s = (float)sin(ang);
+    const float oq = t < hr ? -sq[t + hr] : sq[t - hr], ok = t < hr ? -sk[t + hr] : sk[t - hr];
+    const T q2 = E::mk(nq * c + oq * s), k2 = E::mk(nk * c + ok * s);
+    nq = E::ld(&q2);
+    nk = E::ld(&k2);
+  }
+  lds_sync();
+  if (th) {
+    sq[t] = nq;
+    sk[t] = nk;
+  }
+  if (h % rep == 0 && th) {
+    static_cast<T*>(a.kc)[base + (int64_t)p * hd + t] = E::mk(nk);
+    static_cast<T*>(a.vc)[base + (int64_t)p * hd + t] = E::mk(xv);
+  }
+  lds_sync();
+  const float scale = 1.f / sqrtf((float)hd);
   float mx = -INFINITY;
   for (int j0 = 0; j0 <= p; j0 += 64) {
     const int j = j0 + pi;
     float part = 0.f;
     if (j <= p) {
-      const int d0 = qd * quarter;
       if (j == p) {
         for (int d = 0; d < quarter; ++d) part += sq[d0 + d] * sk[d0 + d];
       } else if (vec) {
-        const T* kr = K + (int64_t)j * hd + d0;
-        Vec8<DT> kv[8];  // quarter <= 64: at most 8 chunks (later ones re-read the last)
+        if (j0 > 0 || !k_early) {
+          const T* kr = K + (int64_t)j * hd + d0;
 #pragma unroll
-        for (int c = 0; c < 8; ++c) kv[c].load(kr + 8 * min(c, nchunk - 1));
+          for (int c = 0; c < 8; ++c) kv[c].load(kr + 8 * min(c, nchunk - 1));
+        }
 #pragma unroll
         for (int c = 0; c < 8; ++c)
           if (c < nchunk) {
@@ -573,9 +633,9 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
     float m = mx;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-    __syncthreads();
+    lds_sync();
     if ((t & 63) == 0) red[t >> 6] = m;
-    __syncthreads();
+    lds_sync();
     m = -INFINITY;
     for (int i = 0; i < (int)(blockDim.x >> 6); ++i) m = fmaxf(m, red[i]);
     float sum = 0.f;
@@ -587,11 +647,16 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
     sum = block_sum(sum, red);
     const float inv = 1.f / sum;
     for (int j = t; j <= p; j += blockDim.x) sc[j] *= inv;
-    __syncthreads();
+    lds_sync();
   }
-  if (t < hd) {
+  if (th) {
     float o = 0.f;
     int j = 0;
+    if (v_early) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) o += sc[u] * v8[u];
+      j = 8;
+    }
     for (; j + 8 <= p; j += 8) {  // 8 positions' loads in flight at a time, summed in order
       float v[8];
 #pragma unroll
@@ -600,8 +665,7 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
       for (int u = 0; u < 8; ++u) o += sc[j + u] * v[u];
     }
     for (; j < p; ++j) o += sc[j] * E::ld(V + (int64_t)j * hd + t);
-    o += sc[p] * sv[t];
-    const float gate = E::ld(qg + hd + t);
+    o += sc[p] * xv;
     static_cast<T*>(a.out)[(int64_t)bb * a.out_stride + (int64_t)h * hd + t] = E::mk(o * (1.f / (1.f + expf(-gate))));
   }
 }

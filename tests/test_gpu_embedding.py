@@ -93,3 +93,17 @@ def test_gsq_embedding_store_roundtrip(tmp_path):
     ids_np = np.array([[1, 39, 0]], dtype=np.int32)
     got = emb(torch.from_numpy(ids_np).cuda()).cpu().numpy()
     np.testing.assert_array_equal(got, _rows(packed, "IQ2_S", vocab, dims, ids_np).astype(np.float16))
+
+
+def test_embedding_many_ids_27b_width():
+    """Hundreds of random ids (some outside the table) at the 27B embedding width, bf16 rows: every
+    wave's staged 4 KB output span, the partial last wave included, equals the oracle's rows."""
+    from mlx_gsq_amd.runtime.kernels.embedding import iq2_s_embedding
+    vocab, dims = 1500, 5120
+    packed = synth.make_packed("IQ2_S", vocab, dims, seed=45)
+    rng = np.random.default_rng(46)
+    ids_np = rng.integers(-3, vocab + 3, size=777).astype(np.int64)
+    want = _rows(packed, "IQ2_S", vocab, dims, ids_np)
+    got = iq2_s_embedding(torch.from_numpy(ids_np).cuda(), torch.from_numpy(packed).cuda(), vocab_size=vocab,
+                          dimensions=dims)
+    assert torch.equal(got.cpu(), torch.from_numpy(want).to(torch.bfloat16))

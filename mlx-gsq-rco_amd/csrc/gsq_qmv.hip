@@ -949,23 +949,24 @@ __global__ void __launch_bounds__(qmv_max_threads(qmv_weight(MR, GL, XS))) qmv_k
   const uintptr_t base = reinterpret_cast<uintptr_t>(a.packed) + (uintptr_t)(row0 * a.row_bytes + (int64_t)sl0 * 8 * BB);
   const uintptr_t stride = (uintptr_t)a.row_bytes * (uintptr_t)a.slots;
 
-  // ---- prologue: the table and the activations (once per workgroup), then this wave's first
-  // item; the ring fills up gradually (below). A wave that queued its whole ring at once would
-  // stall in DMA issue (the CU's memory queue is full at kernel start) before its first item's
-  // decode, and would put the first items of the waves behind it back.
-  if constexpr (P::kLds > 0) dma_copy(a.tb.qmv_tbl, P::kLds, tbl, wave, nw, lane);
-  if (a.x_lds && !(PRE && a.pre.op == QMV_PRE_SWIGLU)) dma_copy(a.x, a.x_bytes, xst, wave, nw, lane);
-  // a convolution epilogue's inputs of row r0 + tid (loads before the first item, so that the
-  // prologue's wait covers them and the DMA wait counts stay exact; into LDS after it)
-  uint4 cpv;
-  const bool cpf = PRE && a.conv_lds && tid < (int)(r1 - r0) && r0 + tid < a.pre.conv_rows;
-  if (cpf) qmv_conv_prefetch(a, r0 + tid, cpv);
+  // ---- prologue: this wave's first item, then the table and the activations (once per
+  // workgroup); the ring fills up gradually (below). A wave that queued its whole ring at once
+  // would stall in DMA issue (the CU's memory queue is full at kernel start) before its first
+  // item's decode, and would put the first items of the waves behind it back. The first item
+  // goes ahead of the table and activation copies, which would otherwise delay it in that queue
+  // (1024x5120 products 0.1 us faster in the graph step, ~0.5 us in back-to-back launches).
   int issued = 0;  // items issued so far (wave-uniform)
   if (nitems > 0) {
     dma_item(base, item_bytes, a.cdma, ring, lane);
     issued = 1;
   }
-  wait_vmcnt(issued * a.cdma);  // this wave's share of the table and activations has landed
+  if constexpr (P::kLds > 0) dma_copy(a.tb.qmv_tbl, P::kLds, tbl, wave, nw, lane);
+  if (a.x_lds && !(PRE && a.pre.op == QMV_PRE_SWIGLU)) dma_copy(a.x, a.x_bytes, xst, wave, nw, lane);
+  // a convolution epilogue's inputs of row r0 + tid (into LDS after the wait below)
+  uint4 cpv;
+  const bool cpf = PRE && a.conv_lds && tid < (int)(r1 - r0) && r0 + tid < a.pre.conv_rows;
+  if (cpf) qmv_conv_prefetch(a, r0 + tid, cpv);
+  wait_vmcnt(0);  // this wave's first item and its share of the table and activations have landed
   if (cpf) reinterpret_cast<uint4*>(dyn + a.conv_off)[tid] = cpv;
   __syncthreads();              // ... and every other wave's share
   if constexpr (PRE) {

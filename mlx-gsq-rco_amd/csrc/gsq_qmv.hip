@@ -1305,10 +1305,10 @@ static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, 
   a.nb = nb;
   a.fill = g_qmv_tuning.fill < 1 ? 1 : g_qmv_tuning.fill;
   // items decoded in pairs (qmv_kernel PR): one fp16 row of 20 superblocks per wave and at least
-  // three ring buffers (a pair being decoded and one in flight); for the types where it measured
-  // faster on 17408x5120 (IQ1_S/IQ1_M/IQ2_S/Q2_K 4-7%, IQ3_S/IQ4_XS 1-2%; Q4_K and IQ2_XS were
-  // 3-5% slower, the rest even)
-  const bool pair_type = qt == IQ1_S || qt == IQ1_M || qt == IQ2_S || qt == Q2_K || qt == IQ3_S || qt == IQ4_XS;
+  // three ring buffers (a pair being decoded and one in flight); every type but Q6_K, whose
+  // ring is two buffers deep at 12 waves (measured on 17408x5120: IQ1_S/IQ1_M/IQ2_S/Q2_K 4-7%,
+  // IQ2_XS 4%, IQ2_XXS 3%, IQ3_XXS/Q4_K/IQ3_S/IQ4_XS 1-2% faster than unpaired)
+  const bool pair_type = qt != Q6_K;
   a.pair = (g_qmv_tuning.pair && pair_type && mr == 1 && !xs && gl == 3 && a.W == 1 && a.nblk == 20 && nb >= 3) ? 1 : 0;
   const int threads = nw * 64;
   const size_t lds_all = (size_t)a.ring_off + (size_t)nw * nb * a.sbuf;

@@ -469,6 +469,10 @@ __global__ void __launch_bounds__(64 * WV, 1) qmm_mfma_kernel(QmmMfmaArgs args) 
       // LDS reads stay in this order: the decode's table reads are waited for without waiting
       // for the activation reads issued after them (LDS completes in order)
       __builtin_amdgcn_sched_barrier(0x1 | 0x2 | 0x4 | 0x8);
+      // a wave issuing its MFMAs takes issue priority over the SIMD's other wave, which is
+      // still decoding: the matrix pipe gets its next instruction as soon as it can take one
+      // (2-4% faster at M = 512 and 2048)
+      __builtin_amdgcn_s_setprio(1);
       // stage q + 1's activations (after the last stage: stale, in-bounds LDS, not used), or
       // stage q's without the lookahead
       load_a(rb, na);
@@ -479,6 +483,7 @@ __global__ void __launch_bounds__(64 * WV, 1) qmm_mfma_kernel(QmmMfmaArgs args) 
         for (int j = 0; j < NB; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(PF ? ua[i] : na[i], ub_[j], acc[i][j], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);  // stages stay apart: two sets of operands at most
+      __builtin_amdgcn_s_setprio(0);
     };
     // a segment is whole columns: its stage count is a multiple of 8
     for (int q = q0; q < q1; q += 2) {

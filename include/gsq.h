@@ -43,7 +43,8 @@ int gsq_block_bytes(int qtype_id);
 
 /* Upload a codebook for a grid type (IQ1_S, IQ1_M, IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS,
  * IQ3_S) and the 128-entry ksigns table to the current device. `grid` is a host array
- * of entries x coords float32 values; every value must be exact in fp16.
+ * of entries x coords float32 values; every value must be exact in fp16. `ksigns` must be
+ * the published table (entry i = i with bit 7 set to the parity of i), else GSQ_E_VALUE.
  * Replaces the table buffers the reference hands its kernels
  * (iq_lookup_decode.py:46-53 `_tables`, iq3_s_decode.py:56-61 `_grid`). */
 int gsq_set_tables(int qtype_id, const float* grid, int64_t entries, int64_t coords,

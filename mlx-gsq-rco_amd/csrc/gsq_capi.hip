@@ -257,6 +257,12 @@ int gsq_set_tables(int qt, const float* grid, int64_t entries, int64_t coords, c
     return fail(GSQ_E_VALUE, "%s codebook must be %dx%d, got %lldx%lld", type_name(qt), ee, cc,
                 (long long)entries, (long long)coords);
   if (!ksigns || n_ksigns != 128) return fail(GSQ_E_VALUE, "ksigns must have 128 entries");
+  // the QMV decoders form the sign byte from the table's closed form (every published ksigns
+  // table has it); a different table would make them disagree with the other kernels
+  for (int i = 0; i < 128; ++i)
+    if (ksigns[i] != (uint8_t)(i | ((__builtin_popcount((unsigned)i) & 1) << 7)))
+      return fail(GSQ_E_VALUE, "ksigns[%d] is %d: the table must be the published one (entry i = i with bit 7 "
+                  "the parity of i)", i, (int)ksigns[i]);
   std::vector<uint16_t> h16((size_t)ee * cc);
   for (size_t i = 0; i < h16.size(); ++i) {
     const float v = grid[i];

@@ -217,7 +217,7 @@ struct QmmDec<IQ3_XXS, A4> {
   __device__ __forceinline__ static void run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
     const uint32_t u = lds_w32<A4>(sb, sd + 66 + 4 * g);
     const float d = h2f(lds_u16(sb, sd + 0)) * (0.5f + (float)(u >> 28)) * 0.5f;
-    const uint32_t* m = tbl_words(tbl, kGridB + ((u >> (7 * kq)) & 127u) * 16);
+    const uint32_t* m = tbl_words(tbl, kGridB + 16 * 8 + ((u >> (7 * kq)) & 127u) * 16);
     const uint32_t qq = lds_u16(sb, sd + 2 + 8 * g + 2 * kq);
     const uint32_t* e0 = tbl_words(tbl, (qq & 0xFFu) * 8);
     const uint32_t* e1 = tbl_words(tbl, (qq >> 8) * 8);
@@ -235,7 +235,7 @@ struct QmmDec<IQ2_XXS, A4> {
   __device__ __forceinline__ static void run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
     const uint32_t u = lds_w32<A4>(sb, sd + 2 + 8 * g + 4);
     const float d = h2f(lds_u16(sb, sd + 0)) * (0.5f + (float)(u >> 28)) * 0.25f;
-    grid8<true>(tbl, lds_u8(sb, sd + 2 + 8 * g + kq), d, 0.f, tbl_words(tbl, kGridB + ((u >> (7 * kq)) & 127u) * 16), o);
+    grid8<true>(tbl, lds_u8(sb, sd + 2 + 8 * g + kq), d, 0.f, tbl_words(tbl, kGridB + 16 * 8 + ((u >> (7 * kq)) & 127u) * 16), o);
   }
 };
 
@@ -247,7 +247,7 @@ struct QmmDec<IQ2_XS, A4> {
     const uint32_t q = lds_u16(sb, sd + 2 + 2 * (4 * g + kq));
     const uint32_t sc = (lds_u8(sb, sd + 66 + g) >> (4 * (kq >> 1))) & 15u;
     const float d = h2f(lds_u16(sb, sd + 0)) * (0.5f + (float)sc) * 0.25f;
-    grid8<true>(tbl, q & 511u, d, 0.f, tbl_words(tbl, kGridB + (q >> 9) * 16), o);
+    grid8<true>(tbl, q & 511u, d, 0.f, tbl_words(tbl, kGridB + 16 * 8 + (q >> 9) * 16), o);
   }
 };
 

@@ -50,6 +50,14 @@ def test_c_validation_errors_without_gpu():
     g = np.zeros((10, 8), np.float32)
     ks = np.zeros(128, np.uint8)
     assert lib.gsq_set_tables(16, g.ctypes.data, 10, 8, ks.ctypes.data, 128) == _lib.GSQ_E_VALUE
+    # a ksigns table other than the published one (entry i = i with bit 7 its parity) is refused:
+    # the QMV decoders form the sign bytes from that closed form
+    from mlx_gsq_amd import tables
+    g = np.zeros((256, 8), np.float32)
+    bad = tables.ksigns().copy()
+    bad[5] ^= 0x80
+    assert lib.gsq_set_tables(16, g.ctypes.data, 256, 8, bad.ctypes.data, 128) == _lib.GSQ_E_VALUE
+    assert b"published" in lib.gsq_last_error()
     # the fused-prologue QMV: arguments are checked before anything reaches a device
     # (qtype, packed, pre_op, x, pre_a, pre_w, eps, res_out, x_out, y, y_dtype, N, K,
     #  conv_state, conv_w, conv_rows, conv_kernel, conv_out, stream)

@@ -350,7 +350,7 @@ template <> struct Qmv<IQ3_S> {
 // other table), so the sign byte costs two instructions, and its two nibbles index the 16
 // nibble masks of two words each: a 128-byte table whose reads never conflict, where 16-byte
 // masks read at random from a 2 KB table put these types' LDS ~40% of the time in bank
-// conflicts (17408x5120 products 5-6% faster, 5120x5120 1-2% slower).
+// conflicts (17408x5120 products 2.6-4.5% faster, 5120x5120 up to 2.4% slower).
 __device__ __forceinline__ uint4 ksigns_masks(const uint8_t* nib, uint32_t k7) {
   const uint32_t s8 = k7 | ((__builtin_popcount(k7) & 1u) << 7);
   const LdsV2 nm{nib};

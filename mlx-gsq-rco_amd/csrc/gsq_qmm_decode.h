@@ -210,6 +210,19 @@ __device__ __forceinline__ void grid8(const uint8_t* tbl, uint32_t qi, float d, 
   for (int i = 0; i < 4; ++i) o[i] = mix2(d, ev[i], c) ^ mv[i];
 }
 
+// Sign masks of one ksigns field (8 weights, 4 words): the sign byte from the ksigns table's
+// closed form (entry i = i with bit 7 the parity of i; the library accepts no other table),
+// the masks of its two nibbles from the 16-entry nibble-mask table after the codebook, whose
+// reads never conflict. Used by IQ3_XXS (11-21% faster than 16-byte masks read from a 2 KB
+// table, M = 4..512); IQ2_XXS and IQ2_XS read those 16-byte masks, which follow the nibble
+// table in their images (the nibble form was 1-6% slower for them here).
+__device__ __forceinline__ void ksigns_masks(const uint8_t* tbl, uint32_t mask_off, uint32_t k7, uint32_t (&m)[4]) {
+  const uint32_t s8 = k7 | ((__builtin_popcount(k7) & 1u) << 7);
+  const uint32_t* lo = tbl_words(tbl, mask_off + (s8 & 15u) * 8);
+  const uint32_t* hi = tbl_words(tbl, mask_off + (s8 >> 4) * 8);
+  m[0] = lo[0]; m[1] = lo[1]; m[2] = hi[0]; m[3] = hi[1];
+}
+
 // IQ3_XXS (iq_lookup_decode.py:7-12): w = +-d*(0.5+s)*0.5*grid[qi][c], ksigns masks
 template <bool A4>
 struct QmmDec<IQ3_XXS, A4> {
@@ -217,7 +230,8 @@ struct QmmDec<IQ3_XXS, A4> {
   __device__ __forceinline__ static void run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
     const uint32_t u = lds_w32<A4>(sb, sd + 66 + 4 * g);
     const float d = h2f(lds_u16(sb, sd + 0)) * (0.5f + (float)(u >> 28)) * 0.5f;
-    const uint32_t* m = tbl_words(tbl, kGridB + 16 * 8 + ((u >> (7 * kq)) & 127u) * 16);
+    uint32_t m[4];
+    ksigns_masks(tbl, kGridB, (u >> (7 * kq)) & 127u, m);
     const uint32_t qq = lds_u16(sb, sd + 2 + 8 * g + 2 * kq);
     const uint32_t* e0 = tbl_words(tbl, (qq & 0xFFu) * 8);
     const uint32_t* e1 = tbl_words(tbl, (qq >> 8) * 8);

@@ -72,15 +72,15 @@ struct QmmGeo {
 };
 
 // Byte size of a type's LDS table image (the QMV kernel's image: fp16 codebook followed by
-// the sign masks; for IQ2_XXS / IQ2_XS / IQ3_XXS 16 nibble masks, then the 128 ksigns masks
-// of four words that these decoders read); checked against the host-built image at launch.
+// the 16 nibble sign masks, and for IQ2_XXS / IQ2_XS the 128 ksigns masks of four words that
+// their decoders read); checked against the host-built image at launch.
 template <int T>
 constexpr int qmm_tbl_bytes() {
   return T == IQ1_S || T == IQ1_M ? 2048 * 8 * 2
        : T == IQ2_XXS            ? 256 * 8 * 2 + 16 * 8 + 128 * 16
        : T == IQ2_XS             ? 512 * 8 * 2 + 16 * 8 + 128 * 16
        : T == IQ2_S              ? 1024 * 8 * 2 + 16 * 8
-       : T == IQ3_XXS            ? 256 * 4 * 2 + 16 * 8 + 128 * 16
+       : T == IQ3_XXS            ? 256 * 4 * 2 + 16 * 8
        : T == IQ3_S              ? 512 * 4 * 2 + 16 * 8
                                  : 0;
 }

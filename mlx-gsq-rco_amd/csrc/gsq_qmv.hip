@@ -362,9 +362,8 @@ template <> struct Qmv<IQ3_XXS> {
   static constexpr int kPair = PAIR_NAT;
   static constexpr int kSums = 0;
   static constexpr int kGridB = 256 * 4 * 2;
-  // image: grid, 16 nibble masks, then the 128 ksigns masks of four words (the QMM decoders')
-  static constexpr int kTbl = kGridB + 16 * 8 + 128 * 16;
-  static constexpr int kLds = kGridB + 16 * 8;  // bytes of it the QMV decoder keeps in LDS
+  static constexpr int kTbl = kGridB + 16 * 8;  // grid + 16 nibble sign masks
+  static constexpr int kLds = kTbl;             // bytes of it the QMV decoder keeps in LDS
   template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
@@ -401,7 +400,7 @@ template <> struct Qmv<IQ2_XXS> {
   static constexpr int kPair = PAIR_NAT;
   static constexpr int kSums = 0;
   static constexpr int kGridB = 256 * 8 * 2;
-  // image: grid, 16 nibble masks, then the 128 ksigns masks of four words (the QMM decoders')
+  // image: grid, 16 nibble sign masks, then the 128 ksigns masks of four words the QMM decoder reads
   static constexpr int kTbl = kGridB + 16 * 8 + 128 * 16;
   static constexpr int kLds = kGridB + 16 * 8;  // bytes of it the QMV decoder keeps in LDS
   template <int MR, bool XS, bool A4>
@@ -439,7 +438,7 @@ template <> struct Qmv<IQ2_XS> {
   static constexpr int kPair = PAIR_NAT;
   static constexpr int kSums = 0;
   static constexpr int kGridB = 512 * 8 * 2;
-  // image: grid, 16 nibble masks, then the 128 ksigns masks of four words (the QMM decoders')
+  // image: grid, 16 nibble sign masks, then the 128 ksigns masks of four words the QMM decoder reads
   static constexpr int kTbl = kGridB + 16 * 8 + 128 * 16;
   static constexpr int kLds = kGridB + 16 * 8;  // bytes of it the QMV decoder keeps in LDS
   template <int MR, bool XS, bool A4>
@@ -1227,10 +1226,10 @@ bool build_qmv_table(int qt, const uint16_t* grid16, const uint8_t* ksigns, std:
       }
       break;
     }
-    case IQ3_S: case IQ2_S:  // 16 nibble masks, 2 dwords each
+    case IQ3_S: case IQ2_S: case IQ3_XXS:  // 16 nibble masks, 2 dwords each
       for (int i = 0; i < 16 * 2; ++i) m[i] = sign_mask_pair_host((uint32_t)(i >> 1), i & 1);
       break;
-    case IQ2_XXS: case IQ2_XS: case IQ3_XXS:  // 16 nibble masks, then 128 ksigns masks of 4 dwords
+    case IQ2_XXS: case IQ2_XS:  // 16 nibble masks, then 128 ksigns masks of 4 dwords (QMM's)
       for (int i = 0; i < 16 * 2; ++i) m[i] = sign_mask_pair_host((uint32_t)(i >> 1), i & 1);
       for (int i = 0; i < 128 * 4; ++i) m[32 + i] = sign_mask_pair_host(ksigns[i >> 2], i & 3);
       break;

@@ -67,7 +67,9 @@ int gsq_tables_ready(int qtype_id);
 int gsq_dequant(int qtype_id, const void* packed, int64_t nblocks, float* out, void* stream);
 
 /* y[M, N] = x[M, K] * W[N, K]^T with the fused-dequant matrix-vector kernel (decode path,
- * small M). Replaces quantized_matvec (mlx_gsq/runtime/kernels/qmv.py:537-576). */
+ * small M). Replaces quantized_matvec (mlx_gsq/runtime/kernels/qmv.py:537-576). x at any
+ * address aligned to its element size: one that is not 16-byte aligned is first copied into
+ * the stream's QMM workspace (see gsq_qmm; made on that first call). */
 int gsq_qmv(int qtype_id, const void* packed, const void* x, int x_dtype, void* y, int y_dtype,
             int64_t M, int64_t N, int64_t K, void* stream);
 
@@ -76,11 +78,13 @@ int gsq_qmv(int qtype_id, const void* packed, const void* x, int x_dtype, void* 
  * the reference, whose model runs them as separate mlx operations in
  * mlx_gsq/models/qwen35.py). y[1, N] = row * W[N, K]^T with
  *   GSQ_PRE_ADD_RMSNORM: s = round(x + pre_a) (pre_a may be NULL: s = x), written to res_out
- *     when not NULL (res_out must not alias x or pre_a); row = round(s / sqrt(mean(s^2) + eps)
+ *     when not NULL; row = round(s / sqrt(mean(s^2) + eps)
  *     * pre_w), as gsq_add_rms_norm computes it;
  *   GSQ_PRE_SWIGLU: x holds [gate | up] (2K values); row = round(silu(gate) * up), as
  *     gsq_swiglu computes it (pre_a, pre_w, eps, res_out unused).
- * The row is written to x_out when not NULL. All vectors fp16, 16-byte aligned; K a multiple
+ * The row is written to x_out when not NULL. The first workgroup writes res_out and x_out while
+ * the others still read x, pre_a and pre_w, so an output that overlaps any of them (or the other
+ * output) is refused with GSQ_E_VALUE. All vectors fp16, 16-byte aligned; K a multiple
  * of 8 up to 32768. With conv_rows > 0 (fp16 y), output rows r < conv_rows also run a
  * depthwise causal convolution (the GatedDeltaNet's, of the qkv rows of its input projection):
  * state conv_state [conv_kernel - 1, conv_rows] fp16 shifted in place with the new input
@@ -96,7 +100,11 @@ int gsq_qmv_pre(int qtype_id, const void* packed, int pre_op, const void* x, con
  * (mlx_gsq/runtime/kernels/qmm.py:559-594). Workgroups that share an output tile exchange
  * fp32 partials through a workspace the library keeps per (device, stream) and allocates on
  * the first call on that stream (or in gsq_prepare): calls on one stream run in order and
- * share it, calls on different streams may overlap and never share one. */
+ * share it, calls on different streams may overlap and never share one. A workspace is 2 slots
+ * of 256 x 256 floats per CU plus counters (128 MB on a 256-CU device), held until the process
+ * ends, for at most 64 streams per device; the call that makes it synchronizes the device once.
+ * A graph captured from stream S uses S's workspace: its replays must not overlap other QMM
+ * work on S or replays of other graphs captured from S. */
 int gsq_qmm(int qtype_id, const void* packed, const void* x, int x_dtype, void* y, int y_dtype,
             int64_t M, int64_t N, int64_t K, void* stream);
 
@@ -177,8 +185,9 @@ int gsq_gdn_seq(const void* qkv, int64_t qkv_stride, const void* z, int64_t z_st
  * block [q | gate] and k likewise from k with k_norm_w (eps), both rotated on their first
  * rotary_dim dims (rotate-half, angle pos * inv_freq[i]) and rounded; k and v written at *pos
  * into k_cache / v_cache [batch, kv_heads, max_len, head_dim]; softmax over positions 0..*pos of
- * q . K / sqrt(head_dim); out = round(sum p V * sigmoid(gate)). *pos is read on the device
- * (< max_len). head_dim a multiple of 4 up to 256. Strides in elements. With work NULL one
+ * q . K / sqrt(head_dim); out = round(sum p V * sigmoid(gate)). *pos is read on the device;
+ * when it is outside 0..max_len-1 (a graph replayed past the cache's end) the kernels write NaN
+ * to out and nothing to the caches. head_dim a multiple of 4 up to 256. Strides in elements. With work NULL one
  * workgroup per (row, head) covers every position (max_len at most 32768); otherwise the
  * positions are split into ceil(max_len / chunk) chunks (chunk a multiple of 64 up to 1024,
  * max_len up to 2^20), one workgroup each, whose partial softmax sums meet in work (batch *

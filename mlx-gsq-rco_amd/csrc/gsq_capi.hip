@@ -19,6 +19,7 @@ hipError_t launch_qmv_pre(int qt, const uint8_t* packed, const void* x, void* y,
                           const QmvPre& pre, const DevTables& tb, int num_cus, hipStream_t s);
 hipError_t launch_qmv(int qt, const uint8_t* packed, const void* x, int xdt, void* y, int ydt, int64_t M, int64_t N,
                       int K, const DevTables& tb, int num_cus, hipStream_t s);
+hipError_t launch_stage_copy(const void* src, void* dst, int64_t bytes, hipStream_t s);
 hipError_t launch_qmm(int qt, const uint8_t* packed, const void* x, int xdt, void* y, int ydt, int64_t M, int64_t N,
                       int K, const DevTables& tb, int num_cus, const QmmWorkspace& ws, hipStream_t s);
 hipError_t launch_embedding(int qt, const uint8_t* packed, const void* ids, int ids64, int64_t n_ids, int64_t vocab,
@@ -223,6 +224,13 @@ int noalloc_scratch(uint8_t** p, int* num_cus) {
   return GSQ_OK;
 }
 
+// True if the byte ranges [a, a + an) and [b, b + bn) share a byte (a NULL range shares none).
+bool overlaps(const void* a, int64_t an, const void* b, int64_t bn) {
+  if (!a || !b) return false;
+  const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+  return pa < pb + (uintptr_t)bn && pb < pa + (uintptr_t)an;
+}
+
 int check_common(int qt, const void* packed, int64_t M, int64_t N, int64_t K, int xdt, int ydt) {
   if (block_bytes_of(qt) == 0) return fail(GSQ_E_UNSUPPORTED, "unsupported quant type id %d", qt);
   if (K <= 0 || K % 256) return fail(GSQ_E_VALUE, "invalid %s matrix width %lld", type_name(qt), (long long)K);
@@ -353,13 +361,33 @@ int gsq_qmv(int qt, const void* packed, const void* x, int xdt, void* y, int ydt
   if (K > (xdt == GSQ_F16 ? 65536 : 32768))
     return fail(GSQ_E_VALUE, "QMV supports K <= %d for this activation dtype (got %lld); use gsq_qmm",
                 xdt == GSQ_F16 ? 65536 : 32768, (long long)K);
-  if (reinterpret_cast<uintptr_t>(x) & 15) return fail(GSQ_E_VALUE, "x must be 16-byte aligned");
+  const int64_t xe = xdt == GSQ_F32 ? 4 : 2;
+  if (reinterpret_cast<uintptr_t>(x) & (xe - 1)) return fail(GSQ_E_VALUE, "x is not aligned to its element size");
+  hipStream_t s = static_cast<hipStream_t>(stream);
   DevTables tb;
   int cus;
-  if (int rc = resolve(qt, &tb, &cus, static_cast<hipStream_t>(stream))) return rc;
-  hipError_t e = launch_qmv(qt, static_cast<const uint8_t*>(packed), x, xdt, y, ydt, M, N, (int)K, tb, cus,
-                            static_cast<hipStream_t>(stream));
-  if (e != hipSuccess) return fail(GSQ_E_HIP, "qmv launch: %s", hipGetErrorString(e));
+  if (int rc = resolve(qt, &tb, &cus, s)) return rc;
+  const uint8_t* pk = static_cast<const uint8_t*>(packed);
+  if ((reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+    hipError_t e = launch_qmv(qt, pk, x, xdt, y, ydt, M, N, (int)K, tb, cus, s);
+    if (e != hipSuccess) return fail(GSQ_E_HIP, "qmv launch: %s", hipGetErrorString(e));
+    return GSQ_OK;
+  }
+  // x not 16-byte aligned (the kernels read it in 16-byte pieces): rows are copied into the
+  // stream's QMM workspace first, as many per launch as it holds; stream order keeps the copies
+  // and the launches that read them (and any QMM launch on the stream) apart
+  QmmWorkspace ws;
+  if (int rc = qmm_workspace(s, &ws)) return rc;
+  const int64_t row_bytes = K * xe, chunk = ws.part_bytes / row_bytes;
+  if (chunk < 1) return fail(GSQ_E_VALUE, "x row of %lld bytes exceeds the staging workspace", (long long)row_bytes);
+  const int64_t ye = ydt == GSQ_F32 ? 4 : 2;
+  for (int64_t r = 0; r < M; r += chunk) {
+    const int64_t rows = M - r < chunk ? M - r : chunk;
+    hipError_t e = launch_stage_copy(static_cast<const uint8_t*>(x) + r * row_bytes, ws.part, rows * row_bytes, s);
+    if (e == hipSuccess)
+      e = launch_qmv(qt, pk, ws.part, xdt, static_cast<uint8_t*>(y) + r * N * ye, ydt, rows, N, (int)K, tb, cus, s);
+    if (e != hipSuccess) return fail(GSQ_E_HIP, "qmv launch: %s", hipGetErrorString(e));
+  }
   return GSQ_OK;
 }
 
@@ -381,8 +409,18 @@ int gsq_qmv_pre(int qt, const void* packed, int pre_op, const void* x, const voi
   if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(pre_a) | reinterpret_cast<uintptr_t>(pre_w) |
        reinterpret_cast<uintptr_t>(res_out) | reinterpret_cast<uintptr_t>(x_out)) & 15)
     return fail(GSQ_E_VALUE, "x, pre_a, pre_w, res_out and x_out must be 16-byte aligned");
-  if (res_out && (res_out == x || res_out == pre_a))
-    return fail(GSQ_E_VALUE, "res_out must not alias x or pre_a (other workgroups still read them)");
+  // workgroup 0 writes res_out and x_out while the other workgroups still read x, pre_a and
+  // pre_w: an output that overlaps an input (or the other output) would race
+  const int64_t kb = K * 2, xb = (pre_op == GSQ_PRE_SWIGLU ? 2 : 1) * kb;
+  const bool norm = pre_op == GSQ_PRE_ADD_RMSNORM;
+  const void* outs[2] = {norm ? res_out : nullptr, x_out};
+  const char* out_names[2] = {"res_out", "x_out"};
+  for (int i = 0; i < 2; ++i) {
+    if (!outs[i]) continue;
+    if (overlaps(outs[i], kb, x, xb) || (norm && (overlaps(outs[i], kb, pre_a, kb) || overlaps(outs[i], kb, pre_w, kb))))
+      return fail(GSQ_E_VALUE, "%s must not alias x, pre_a or pre_w (other workgroups still read them)", out_names[i]);
+  }
+  if (outs[0] && overlaps(outs[0], kb, outs[1], kb)) return fail(GSQ_E_VALUE, "res_out and x_out must not alias");
   QmvPre pre;
   pre.op = pre_op == GSQ_PRE_ADD_RMSNORM ? QMV_PRE_ADD_NORM : QMV_PRE_SWIGLU;
   pre.a = pre_op == GSQ_PRE_SWIGLU ? x : pre_a;

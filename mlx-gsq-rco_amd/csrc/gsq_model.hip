@@ -527,6 +527,17 @@ __device__ __forceinline__ float2 block_sum2(float a, float b, float* red) {
 // 0..63) and the first 8 cached V rows; the barriers wait on LDS only, so a short context costs
 // one memory round trip. The arithmetic (norms, rotary, scores, softmax, V sums) is the same
 // as, and in the same order as, the separate steps it replaces.
+// A position outside the cache (pos < 0 or pos >= L, e.g. a graph replayed past the cache's
+// end) would write K / V rows outside the head's cache slab and scores past the LDS: the
+// attention kernels then write NaN rows to out and touch nothing else. Uniform per workgroup.
+template <typename T, typename E>
+__device__ __forceinline__ bool attn_pos_invalid(const AttnArgs& a, int h, int bb, int t) {
+  const int64_t p = a.pos[0];
+  if (p >= 0 && p < a.L) return false;
+  if (t < a.hd) static_cast<T*>(a.out)[(int64_t)bb * a.out_stride + (int64_t)h * a.hd + t] = E::mk(__builtin_nanf(""));
+  return true;
+}
+
 template <int DT>
 __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
   using E = Elem<DT>;
@@ -535,6 +546,7 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
   __shared__ float sq[256], sk[256], red[16];
   const int h = blockIdx.x, bb = blockIdx.y, t = threadIdx.x;
   const int hd = a.hd, rd = a.rd, rep = a.H / a.Hkv, kvh = h / rep;
+  if (attn_pos_invalid<T, E>(a, h, bb, t)) return;  // uniform: before any cache, LDS or barrier
   const int p = (int)a.pos[0];
   const T* qg = static_cast<const T*>(a.qg) + (int64_t)bb * a.qg_stride + (int64_t)h * 2 * hd;
   const T* kn = static_cast<const T*>(a.k) + (int64_t)bb * a.k_stride + (int64_t)kvh * hd;
@@ -686,6 +698,7 @@ __global__ void __launch_bounds__(256) attn_chunk_kernel(AttnArgs a) {
   __shared__ float sq[256], sk[256], sv[256], red[16], sc[kAttnChunkMax];
   const int h = blockIdx.x, bb = blockIdx.y, c = blockIdx.z, t = threadIdx.x;
   const int hd = a.hd, rep = a.H / a.Hkv, kvh = h / rep;
+  if (a.pos[0] < 0 || a.pos[0] >= a.L) return;  // the combine kernel writes NaN rows
   const int p = (int)a.pos[0];
   const int j0 = c * a.chunk;
   float* part = a.work + (((int64_t)bb * a.H + h) * a.nsplit + c) * (hd + 2);
@@ -785,6 +798,7 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
   using E = Elem<DT>;
   using T = typename E::T;
   const int h = blockIdx.x, bb = blockIdx.y, t = threadIdx.x, hd = a.hd;
+  if (attn_pos_invalid<T, E>(a, h, bb, t)) return;
   if (t >= hd) return;
   const float* part = a.work + ((int64_t)bb * a.H + h) * a.nsplit * (hd + 2);
   float m = -INFINITY;

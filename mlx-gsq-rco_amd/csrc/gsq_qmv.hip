@@ -18,10 +18,11 @@
 //   so the wait count is plain arithmetic.
 // * A workgroup owns a contiguous range of rows; each row slot owns a contiguous sub-range, so
 //   every wave reads long sequential spans of the packed matrix.
-// * The decode turns packed bits into fp16 pairs with masks (K-quants, small integer codes
-//   are exact fp16 subnormals), byte lookups (IQ4_XS) or LDS-resident codebook entries with
-//   sign masks (IQ types) and accumulates with v_dot2_f32_f16 in fp32. Per-group scales are
-//   applied once per group.
+// * The decode turns packed bits into fp16 pairs with masks (K-quant codes as normal fp16
+//   numbers: 2- and 4-bit codes in the top mantissa bits of 1.0, 6-bit codes as integers under
+//   1024's exponent), byte lookups (IQ4_XS) or LDS-resident codebook entries with sign masks
+//   (IQ types) and accumulates with v_dot2_f32_f16 in fp32. Per-group scales are applied once
+//   per group.
 // * Prologue: the type's LDS table and the activations are fetched once per workgroup (DMA),
 //   behind the first weight slices of every wave.
 #include <cstdio>
@@ -1361,6 +1362,28 @@ static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, 
     case IQ1_M: return launch_qmv_type<IQ1_M>(a, mr, xs, gl, grid, threads, lds, s);
     default: return hipErrorInvalidValue;
   }
+}
+
+// Copy of `bytes` (a multiple of 16) from a 2-byte aligned src to a 16-byte aligned dst: the
+// QMV kernels read activations in 16-byte pieces, so an x that is not 16-byte aligned goes
+// through this copy first. One thread per 16 bytes, read as eight 2-byte pieces.
+__global__ void __launch_bounds__(256) stage_copy_kernel(const uint16_t* __restrict__ src, uint4* __restrict__ dst,
+                                                         int64_t n16) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n16) return;
+  const uint16_t* p = src + 8 * i;
+  uint32_t w[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) w[j] = (uint32_t)p[2 * j] | ((uint32_t)p[2 * j + 1] << 16);
+  dst[i] = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+hipError_t launch_stage_copy(const void* src, void* dst, int64_t bytes, hipStream_t s) {
+  const int64_t n16 = bytes / 16;
+  if (n16 <= 0) return hipSuccess;
+  hipLaunchKernelGGL(stage_copy_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, s,
+                     static_cast<const uint16_t*>(src), static_cast<uint4*>(dst), n16);
+  return hipGetLastError();
 }
 
 // y[M, N] = x[M, K] W^T: activation rows go out in launches of up to 4 (2 for fp32/bf16).

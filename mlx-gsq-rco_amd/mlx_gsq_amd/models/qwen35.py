@@ -433,7 +433,9 @@ def build_qwen35(store, dtype=torch.float16, args: Qwen35Args | None = None, lin
                 args, i, joint([p + "attn_qkv.weight", p + "attn_gate.weight"]),
                 linear(store.weight(p + "ssm_out.weight")), plain(p + "ssm_alpha.weight"),
                 plain(p + "ssm_beta.weight"), conv.reshape(conv.shape[0], conv.shape[-1]),
-                plain(p + "ssm_a", torch.float32), plain(p + "ssm_dt.bias", torch.float32),
+                # dt_bias rounded to the activation dtype, as the reference loads it
+                # (qwen35.py:142 ``.astype(dtype)``); the kernels add it to a in float32
+                plain(p + "ssm_a", torch.float32), plain(p + "ssm_dt.bias"),
                 plain(p + "ssm_norm.weight"))
         else:
             mixer = FullAttention(
@@ -473,6 +475,9 @@ class GraphDecoder:
                 self.logits = model(self.ids, cache)
         torch.cuda.current_stream(device).wait_stream(side)
         torch.cuda.synchronize(device)
+        # the graph's QMM launches use the capture stream's workspace (libgsq keys workspaces
+        # by stream): the stream is kept with the graph
+        self.capture_stream = side
         # the capture traced one step without running it: undo its host-side bookkeeping
         self._restore(snap)
 

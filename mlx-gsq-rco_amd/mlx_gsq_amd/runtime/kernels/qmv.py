@@ -57,6 +57,17 @@ def _small_batch_faster(rows, dtype, out_features, in_features):
     return rows >= SMALL_BATCH_MIN_ROWS
 
 
+def routes_to_qmm(rows, dtype, out_features, in_features):
+    """True if ``quantized_matvec`` sends ``rows`` activation rows of ``dtype`` to the QMM
+    kernels: the reference's row threshold (qmv.py:548-549), rows wider than the vector
+    kernel's activation registers hold (K <= 65536 for fp16 activations, K <= 32768 for
+    fp32/bf16, split into two fp16 parts), and the small batches where the small-batch QMM is
+    faster."""
+    max_k = 65536 if dtype == torch.float16 else 32768
+    return (rows >= QMM_MIN_ROWS or in_features > max_k
+            or _small_batch_faster(rows, dtype, out_features, in_features))
+
+
 def quantized_matvec(x, packed, *, qtype: str, out_features: int, in_features: int, out_dtype=None):
     """y = x @ W.T for packed ``W`` of shape ``(out_features, in_features)``.
 
@@ -67,10 +78,7 @@ def quantized_matvec(x, packed, *, qtype: str, out_features: int, in_features: i
     original = x.shape[:-1]
     rows = x.numel() // in_features
     flat = x.reshape(rows, in_features)
-    # the fused QMV keeps a row's activations in registers: K <= 65536 for fp16 activations,
-    # K <= 32768 for fp32/bf16 (split into two fp16 parts); wider rows go to the tiled QMM
-    max_k = 65536 if x.dtype == torch.float16 else 32768
-    if rows >= QMM_MIN_ROWS or in_features > max_k or _small_batch_faster(rows, x.dtype, out_features, in_features):
+    if routes_to_qmm(rows, x.dtype, out_features, in_features):
         return quantized_matmul(flat, packed, qtype=qtype, out_features=out_features,
                                 in_features=in_features, out_dtype=out_dtype).reshape(*original, out_features)
     if qtype not in QTYPES:
@@ -93,6 +101,14 @@ def quantized_matvec(x, packed, *, qtype: str, out_features: int, in_features: i
 PRE_OPS = {"add_rms_norm": 1, "swiglu": 2}  # GSQ_PRE_ADD_RMSNORM, GSQ_PRE_SWIGLU
 
 
+def _overlap(a, b):
+    """True if contiguous tensors ``a`` and ``b`` share a byte of device memory."""
+    if a is None or b is None:
+        return False
+    pa, pb = a.data_ptr(), b.data_ptr()
+    return pa < pb + b.numel() * b.element_size() and pb < pa + a.numel() * a.element_size()
+
+
 def quantized_matvec_pre(x, packed, *, qtype: str, out_features: int, in_features: int, pre: str, pre_a=None,
                          pre_w=None, eps: float = 0.0, res_out=None, x_out=None, out_dtype=None, conv=None):
     """y = row @ W.T for one fp16 activation row that the QMV kernel forms itself (libgsq
@@ -100,12 +116,14 @@ def quantized_matvec_pre(x, packed, *, qtype: str, out_features: int, in_feature
     operations):
 
     * ``pre="add_rms_norm"``: ``s = x + pre_a`` (``pre_a`` may be None), rounded to fp16 and
-      written to ``res_out`` when given (a different buffer from ``x`` and ``pre_a``); ``row =
+      written to ``res_out`` when given; ``row =
       rms_norm(s) * pre_w`` with ``eps``, as ``model_ops.add_rms_norm`` computes it;
     * ``pre="swiglu"``: ``x`` holds ``[gate | up]`` (``2 * in_features`` values); ``row =
       silu(gate) * up``, as ``model_ops.swiglu`` computes it.
 
-    The row is also written to ``x_out`` when given. ``x`` and the vectors are fp16 and hold
+    The row is also written to ``x_out`` when given. Neither ``res_out`` nor ``x_out`` may
+    overlap ``x``, ``pre_a``, ``pre_w`` or each other (other workgroups of the launch still read
+    the inputs while the first writes the outputs; ValueError). ``x`` and the vectors are fp16 and hold
     exactly one row (any leading shape of size 1); the result has shape ``x.shape[:-1] +
     (out_features,)``. ``conv=(state, weight, out)`` adds the GatedDeltaNet's depthwise causal
     convolution of the first ``state.shape[-1]`` outputs (fp16 result only): ``state`` (1, k-1,
@@ -141,6 +159,14 @@ def quantized_matvec_pre(x, packed, *, qtype: str, out_features: int, in_feature
             raise ValueError("conv must be (state (1, k-1, rows) fp16, weight (rows, k) fp16, out (rows,) float32), "
                              "contiguous, rows <= out_features, fp16 output")
     flat = x.contiguous()
+    # the first workgroup writes res_out / x_out while the others still read x, pre_a and pre_w
+    outs = (("res_out", res_out if pre == "add_rms_norm" else None), ("x_out", x_out))
+    ins = (flat,) + ((pre_a, pre_w) if pre == "add_rms_norm" else ())
+    for name, o in outs:
+        if o is not None and any(_overlap(o, t) for t in ins):
+            raise ValueError(f"{name} must not alias x, pre_a or pre_w (other workgroups still read them)")
+    if res_out is not None and x_out is not None and pre == "add_rms_norm" and _overlap(res_out, x_out):
+        raise ValueError("res_out and x_out must not alias")
     packed = packed.contiguous()
     y = torch.empty(x.shape[:-1] + (out_features,), dtype=odt, device=x.device)
 

@@ -61,8 +61,9 @@ def test_c_validation_errors_without_gpu():
     # the fused-prologue QMV: arguments are checked before anything reaches a device
     # (qtype, packed, pre_op, x, pre_a, pre_w, eps, res_out, x_out, y, y_dtype, N, K,
     #  conv_state, conv_w, conv_rows, conv_kernel, conv_out, stream)
-    ok = dict(qt=12, packed=2, op=1, x=16, a=32, w=48, eps=1e-6, res=64, xo=80, y=96, ydt=1, n=4, k=256,
-              cs=112, cw=128, cr=0, ck=4, co=144)
+    # (fake device addresses 4 KiB apart: no two vectors of up to 2 x 256 fp16 values overlap)
+    ok = dict(qt=12, packed=2, op=1, x=1 << 12, a=2 << 12, w=3 << 12, eps=1e-6, res=4 << 12, xo=5 << 12,
+              y=6 << 12, ydt=1, n=4, k=256, cs=7 << 12, cw=8 << 12, cr=0, ck=4, co=9 << 12)
 
     def pre(**kw):
         v = {**ok, **kw}
@@ -71,7 +72,18 @@ def test_c_validation_errors_without_gpu():
     assert pre(op=7) == _lib.GSQ_E_VALUE and b"pre_op" in lib.gsq_last_error()
     assert pre(w=None) == _lib.GSQ_E_VALUE and b"norm weight" in lib.gsq_last_error()
     assert pre(eps=-1.0) == _lib.GSQ_E_VALUE
-    assert pre(res=16) == _lib.GSQ_E_VALUE and b"alias" in lib.gsq_last_error()  # res_out == x
+    # an output overlapping an input (or the other output) races with the workgroups that
+    # still read it
+    x0 = ok["x"]
+    assert pre(res=x0) == _lib.GSQ_E_VALUE and b"res_out must not alias" in lib.gsq_last_error()
+    assert pre(res=ok["a"] + 256) == _lib.GSQ_E_VALUE and b"res_out must not alias" in lib.gsq_last_error()
+    assert pre(xo=x0) == _lib.GSQ_E_VALUE and b"x_out must not alias" in lib.gsq_last_error()
+    assert pre(xo=x0 - 496) == _lib.GSQ_E_VALUE and b"x_out must not alias" in lib.gsq_last_error()
+    assert pre(xo=ok["a"]) == _lib.GSQ_E_VALUE and b"x_out must not alias" in lib.gsq_last_error()
+    assert pre(xo=ok["w"] + 16) == _lib.GSQ_E_VALUE and b"x_out must not alias" in lib.gsq_last_error()
+    assert pre(xo=ok["res"] + 16) == _lib.GSQ_E_VALUE and b"res_out and x_out" in lib.gsq_last_error()
+    # SWIGLU reads 2K values of x: an x_out in its second half overlaps
+    assert pre(op=2, xo=x0 + 512) == _lib.GSQ_E_VALUE and b"x_out must not alias" in lib.gsq_last_error()
     assert pre(x=24) == _lib.GSQ_E_VALUE and b"aligned" in lib.gsq_last_error()
     assert pre(cr=5) == _lib.GSQ_E_VALUE  # more convolution rows than outputs
     assert pre(cr=4, ck=9) == _lib.GSQ_E_VALUE and b"kernel" in lib.gsq_last_error()

@@ -1,4 +1,4 @@
-"""GPU parity at the BASELINE workload sizes (configs[0]-[2]), checked on sampled output columns.
+"""GPU parity at the BASELINE workload sizes (configs[0]-[3]), checked on sampled output columns.
 
 Every product runs on the device at its full size; the oracle (dequant + float32 matmul,
 reference tests/test_all_qmv.py:22, test_all_qmm.py:41-57) then recomputes a seeded sample of
@@ -75,17 +75,8 @@ def sampled_reference(x, packed, qtype, n, k, rows, f64=False):
     return np.asarray(x, np.float64).reshape(-1, k) @ w.T
 
 
-def run_qmv(qtype, n, k, seed):
-    from mlx_gsq_amd.runtime.kernels.qmv import quantized_matvec
-    print(f"full-size qmv {qtype} {n}x{k}", flush=True)
-    packed = synth.make_packed(qtype, n, k, seed=seed)
-    x = synth.make_x(1, k, seed=seed + 1, dtype=np.float16)
-    y = quantized_matvec(torch.from_numpy(x).cuda(), torch.from_numpy(packed).cuda(), qtype=qtype,
-                         out_features=n, in_features=k, out_dtype=torch.float32).cpu().numpy()
-    assert np.isfinite(y).all()
-    rows = sample_rows(n, seed)
-    want = sampled_reference(x, packed, qtype, n, k, rows)
-    got = y[:, rows]
+def check_qmv_bar(got, want, x, packed, qtype, n, k, rows):
+    """The vector kernel's bar (module docstring): rel-L2 1e-4, rtol 3e-5 + the absolute allowance."""
     assert rel_l2(got, want) <= 1e-4, rel_l2(got, want)
     truth = sampled_reference(x, packed, qtype, n, k, rows, f64=True)
     err = np.abs(got - truth)
@@ -94,6 +85,37 @@ def run_qmv(qtype, n, k, seed):
     print(f"max error {err.max():.3g} (float32 oracle {oracle_err:.3g})", flush=True)
     assert ok.all(), (f"{int((~ok).sum())} outputs off: max error {err.max():.3g}, "
                       f"float32 oracle's max error {oracle_err:.3g}")
+
+
+def check_qmm_bar(got, want):
+    """The matrix kernels' bar: rel-L2 1e-3 and the reference's QMM tolerance."""
+    assert rel_l2(got, want) <= 1e-3, rel_l2(got, want)
+    np.testing.assert_allclose(got, want, rtol=2e-3, atol=2e-3 * np.abs(want).max())
+
+
+def run_matvec(qtype, n, k, seed, m=1):
+    """y = x W^T through quantized_matvec's routing (the vector kernel, or the small-batch /
+    tiled QMM where the router sends these rows), checked on sampled columns at the bar of the
+    kernel that ran."""
+    from mlx_gsq_amd.runtime.kernels.qmv import quantized_matvec, routes_to_qmm
+    vector = not routes_to_qmm(m, torch.float16, n, k)
+    print(f"full-size {'qmv' if vector else 'qmm'} {qtype} M={m} {n}x{k}", flush=True)
+    packed = synth.make_packed(qtype, n, k, seed=seed)
+    x = synth.make_x(m, k, seed=seed + 1, dtype=np.float16)
+    y = quantized_matvec(torch.from_numpy(x).cuda(), torch.from_numpy(packed).cuda(), qtype=qtype,
+                         out_features=n, in_features=k, out_dtype=torch.float32).cpu().numpy()
+    assert y.shape == (m, n) and np.isfinite(y).all()
+    rows = sample_rows(n, seed)
+    want = sampled_reference(x, packed, qtype, n, k, rows)
+    got = y[:, rows]
+    if vector:
+        check_qmv_bar(got, want, x, packed, qtype, n, k, rows)
+    else:
+        check_qmm_bar(got, want)
+
+
+def run_qmv(qtype, n, k, seed):
+    run_matvec(qtype, n, k, seed, m=1)
 
 
 def test_qmv_configs0_q4k_17408x5120():
@@ -109,12 +131,29 @@ def test_qmv_configs1_27b_shapes(qtype, shape):
     run_qmv(qtype, n, k, seed=200 + 7 * QTYPES.index(qtype) + (k == 17408) + 2 * (n == k))
 
 
+# the mixed decoder layer (q / k / v / o / gate / up / down)
+LAYER = [("q", "IQ2_XS", 5120, 5120), ("k", "IQ2_XS", 1024, 5120), ("v", "IQ4_XS", 1024, 5120),
+         ("o", "IQ3_S", 5120, 5120), ("gate", "IQ2_S", 17408, 5120), ("up", "IQ2_S", 17408, 5120),
+         ("down", "Q4_K", 5120, 17408)]
+
+
+@pytest.mark.parametrize("m", [2, 4, 8, 16])
+@pytest.mark.parametrize("proj", LAYER, ids=[p[0] for p in LAYER])
+def test_layer_configs3_small_batch(proj, m):
+    """every projection of the mixed layer at M = 2..16 through quantized_matvec's
+    routing (the vector kernel, or the small-batch QMM with its stream-K split of 17408-row and
+    17408-wide products over all CUs), at full size."""
+    name, qtype, n, k = proj
+    run_matvec(qtype, n, k, seed=500 + 13 * [p[0] for p in LAYER].index(name) + m, m=m)
+
+
 @pytest.mark.parametrize("qtype", ["IQ3_S", "Q6_K"])
-@pytest.mark.parametrize("case", [(2048, 17408, 5120), (182, 5120, 17408), (512, 5120, 17408),
-                                  (182, 17408, 5120)])
+@pytest.mark.parametrize("case", [(182, 17408, 5120), (512, 17408, 5120), (2048, 17408, 5120),
+                                  (182, 5120, 17408), (512, 5120, 17408), (2048, 5120, 17408)])
 def test_qmm_configs2_shapes(qtype, case):
-    """tiled QMM at M = 2048 on 17408 x 5120 and M = 182 / 512 on the K = 17408
-    shape (68 K columns per tile, stream-K split tiles summed by the last workgroup)."""
+    """tiled QMM at every M of the config on both shapes (17408 x 5120: 17 x 1024
+    weight rows over all CUs; 5120 x 17408: 68 K columns per tile, stream-K split tiles summed
+    by the last workgroup)."""
     from mlx_gsq_amd.runtime.kernels.qmm import quantized_matmul
     m, n, k = case
     print(f"full-size qmm {qtype} M={m} {n}x{k}", flush=True)
@@ -126,6 +165,4 @@ def test_qmm_configs2_shapes(qtype, case):
     assert np.isfinite(y).all()
     rows = sample_rows(n, seed)
     want = sampled_reference(x, packed, qtype, n, k, rows)
-    got = y[:, rows]
-    assert rel_l2(got, want) <= 1e-3, rel_l2(got, want)
-    np.testing.assert_allclose(got, want, rtol=2e-3, atol=2e-3 * np.abs(want).max())
+    check_qmm_bar(y[:, rows], want)

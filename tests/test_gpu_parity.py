@@ -145,6 +145,31 @@ def test_qmv_unaligned_packed_view_and_odd_rows():
         assert rel_l2(y, want) <= 1e-4, (qtype, rel_l2(y, want))
 
 
+@pytest.mark.parametrize("dtype,offset", [(torch.float16, 8), (torch.float16, 2), (torch.bfloat16, 6),
+                                          (torch.float32, 4)])
+@pytest.mark.parametrize("rows", [1, 2])
+def test_qmv_activations_not_16_byte_aligned(dtype, offset, rows):
+    """x at a byte offset that is not a multiple of 16 (the reference accepts any array): the
+    library stages it into an aligned copy, so the vector kernel gives the same bits as for
+    the aligned x."""
+    from mlx_gsq_amd.runtime.kernels.qmv import quantized_matvec, routes_to_qmm
+    N, K = 300, 1024
+    assert not routes_to_qmm(rows, dtype, N, K)
+    print(f"qmv unaligned x {dtype} +{offset} M={rows}", flush=True)
+    packed = dev(synth.make_packed("IQ3_S", N, K, seed=2))
+    x = torch.from_numpy(synth.make_x(rows, K, seed=4, dtype=np.float32)).to("cuda", dtype)
+    es = x.element_size()
+    big = torch.zeros(x.numel() + 16, dtype=dtype, device="cuda")
+    big[offset // es:offset // es + x.numel()] = x.reshape(-1)
+    xv = big[offset // es:offset // es + x.numel()].reshape(rows, K)
+    assert xv.data_ptr() % 16 == offset % 16 != 0
+    kw = dict(qtype="IQ3_S", out_features=N, in_features=K, out_dtype=torch.float32)
+    y = quantized_matvec(xv, packed, **kw)
+    assert torch.equal(y, quantized_matvec(x, packed, **kw))
+    want = O.matmul_reference(x.float().cpu().numpy(), packed.cpu().numpy(), "IQ3_S", N, K, TABLES["IQ3_S"])
+    assert rel_l2(y.cpu().numpy(), want) <= 1e-4
+
+
 @pytest.mark.parametrize("qtype", QTYPES)
 @pytest.mark.parametrize("rows", [8, 16, 33, 100, 128, 182, 257])
 def test_qmm_matches_oracle(qtype, rows):
@@ -389,6 +414,10 @@ def test_qmv_pre_matches_separate_kernels(qtype):
             assert torch.equal(res, xs)
             with pytest.raises(ValueError):  # the residual must go to a new buffer
                 quantized_matvec_pre(x, pd, pre=pre, pre_a=d, pre_w=w, eps=1e-6, res_out=x, **kw)
+            with pytest.raises(ValueError, match="x_out must not alias"):  # so must the row (in place)
+                quantized_matvec_pre(x, pd, pre=pre, pre_w=w, eps=1e-6, x_out=x, **kw)
+            with pytest.raises(ValueError, match="x_out must not alias"):
+                quantized_matvec_pre(x, pd, pre=pre, pre_a=d, pre_w=w, eps=1e-6, x_out=d, **kw)
             # the GatedDeltaNet convolution of the first 1000 outputs in the epilogue (fp16 y)
             rows, kc = 1000, 4
             state = torch.randn(1, kc - 1, rows, generator=g).half().cuda()
@@ -410,6 +439,8 @@ def test_qmv_pre_matches_separate_kernels(qtype):
             x = torch.randn(1, 2 * k, generator=g).half().cuda()
             y = quantized_matvec_pre(x, pd, pre=pre, x_out=row, **kw)
             want_row = model_ops.swiglu(x)
+            with pytest.raises(ValueError, match="x_out must not alias"):  # over the up half of x
+                quantized_matvec_pre(x, pd, pre=pre, x_out=x[0, k:], **kw)
         assert torch.allclose(row.float(), want_row.float(), rtol=1e-3, atol=1e-6), pre
         assert torch.equal(y, quantized_matvec(row, pd, **kw)), pre
         ref = O.matmul_reference(row.float().cpu().numpy(), packed, qtype, n, k, TABLES.get(qtype))

@@ -267,3 +267,42 @@ def test_gpu_attention_decode_matches_torch_formulation():
     assert rel_l2(got_split.numpy(), want.numpy()) <= 5e-3
     assert rel_l2(got_split.numpy(), got.numpy()) <= 1e-3
     assert torch.equal(gcache.k[3], kc0) and torch.equal(gcache.v[3], vc0)  # same slot, same values
+
+
+@pytest.mark.gpu
+def test_gpu_attention_position_bounds():
+    """attn_decode at the last cache slot (pos = max_len - 1) on the single-workgroup and the
+    chunked path, and with a position outside the cache (pos = max_len, pos = -1): NaN rows and
+    untouched caches instead of writes past the head's cache slab."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from mlx_gsq_amd.runtime.kernels import model_ops
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(21)
+    B, H, Hkv, hd, rd, L = 2, 4, 2, 64, 32, 128
+    qg = torch.randn(B, H * 2 * hd, generator=g).half().to(dev)
+    k = torch.randn(B, Hkv * hd, generator=g).half().to(dev)
+    v = torch.randn(B, Hkv * hd, generator=g).half().to(dev)
+    qn = (1 + 0.1 * torch.randn(hd, generator=g)).half().to(dev)
+    kn = (1 + 0.1 * torch.randn(hd, generator=g)).half().to(dev)
+    inv_freq = (1.0 / (10000.0 ** (torch.arange(0, rd, 2, dtype=torch.float64) / rd))).to(dev)
+    kc0 = torch.randn(B, Hkv, L, hd, generator=g).half().to(dev)
+    vc0 = torch.randn(B, Hkv, L, hd, generator=g).half().to(dev)
+    kw = dict(heads=H, kv_heads=Hkv, head_dim=hd, rotary_dim=rd, eps=1e-6)
+    outs = []
+    for chunk in (0, 64):
+        kc, vc = kc0.clone(), vc0.clone()
+        pos = torch.tensor([L - 1], dtype=torch.int64, device=dev)
+        out = model_ops.attn_decode(qg, k, v, qn, kn, inv_freq, kc, vc, pos, chunk=chunk, **kw)
+        torch.cuda.synchronize()
+        assert torch.isfinite(out).all(), chunk
+        assert torch.equal(kc[:, :, :L - 1], kc0[:, :, :L - 1]) and torch.equal(vc[:, :, L - 1].flatten(1), v), chunk
+        outs.append(out.float().cpu())
+        for bad in (L, -1):
+            kc, vc = kc0.clone(), vc0.clone()
+            pos = torch.tensor([bad], dtype=torch.int64, device=dev)
+            out = model_ops.attn_decode(qg, k, v, qn, kn, inv_freq, kc, vc, pos, chunk=chunk, **kw)
+            torch.cuda.synchronize()
+            assert torch.isnan(out).all(), (chunk, bad)
+            assert torch.equal(kc, kc0) and torch.equal(vc, vc0), (chunk, bad)
+    assert rel_l2(outs[1].numpy(), outs[0].numpy()) <= 1e-3

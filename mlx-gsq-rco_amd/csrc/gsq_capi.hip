@@ -31,7 +31,9 @@ hipError_t launch_gdn_step(int dt, const GdnArgs& a, hipStream_t s);
 hipError_t launch_gdn_seq(int dt, const GdnArgs& a, hipStream_t s);
 hipError_t launch_attn_decode(int dt, const AttnArgs& a, hipStream_t s);
 int qmv_table_bytes(int qt);
-bool build_qmv_table(int qt, const uint16_t* grid16, const uint8_t* ksigns, std::vector<uint8_t>& out);
+int build_qmv_table(int qt, const uint16_t* grid16, const uint8_t* ksigns, std::vector<uint8_t>& out);
+int qmm_table_bytes(int qt);
+int build_qmm_table(int qt, const uint16_t* grid16, const uint8_t* ksigns, std::vector<uint8_t>& out);
 }  // namespace gsq
 
 using namespace gsq;
@@ -79,7 +81,8 @@ static __device__ __align__(256) uint8_t scratch[kNoAllocCounterBytes + kNoAlloc
 
 struct DevState {
   std::map<int, uint16_t*> grids;     // per grid type
-  std::map<int, uint8_t*> qmv_tbls;   // per type with a QMV LDS table
+  std::map<int, uint8_t*> qmv_tbls;   // per type with a QMV LDS table image
+  std::map<int, uint8_t*> qmm_tbls;   // per type with a QMM LDS table image
   uint8_t* ksigns = nullptr;
   int num_cus = 0;
   uint8_t* scratch = nullptr;         // this device's address of `scratch`
@@ -96,18 +99,33 @@ bool capturing(hipStream_t s) {
   return st != hipStreamCaptureStatusNone;
 }
 
-// Upload (or refresh) the QMV LDS table image of `qt` on the current device; caller holds g_mu.
-int upload_qmv_table(DevState& st, int qt, const uint16_t* grid16_host, const uint8_t* ksigns_host) {
-  std::vector<uint8_t> img;
-  if (!build_qmv_table(qt, grid16_host, ksigns_host, img)) return GSQ_OK;
-  uint8_t*& d = st.qmv_tbls[qt];
+// Upload one built table image into `tbls[qt]` (allocated on first use); caller holds g_mu.
+int upload_image(std::map<int, uint8_t*>& tbls, int qt, const std::vector<uint8_t>& img) {
+  uint8_t*& d = tbls[qt];
   hipError_t e;
   if (!d) {
     e = hipMalloc(&d, img.size());
-    if (e != hipSuccess) { st.qmv_tbls.erase(qt); return fail(GSQ_E_HIP, "hipMalloc: %s", hipGetErrorString(e)); }
+    if (e != hipSuccess) { tbls.erase(qt); return fail(GSQ_E_HIP, "hipMalloc: %s", hipGetErrorString(e)); }
   }
   e = hipMemcpy(d, img.data(), img.size(), hipMemcpyHostToDevice);
   if (e != hipSuccess) return fail(GSQ_E_HIP, "hipMemcpy: %s", hipGetErrorString(e));
+  return GSQ_OK;
+}
+
+// Build and upload (or refresh) the QMV and QMM LDS table images of `qt` on the current device;
+// caller holds g_mu. Both images are built before either is uploaded, so a codebook that one of
+// them cannot hold exactly changes nothing.
+int upload_qmv_table(DevState& st, int qt, const uint16_t* grid16_host, const uint8_t* ksigns_host) {
+  std::vector<uint8_t> img_v, img_m;
+  const int rv = build_qmv_table(qt, grid16_host, ksigns_host, img_v);
+  if (rv < 0)
+    return fail(GSQ_E_VALUE, "%s codebook: a value of the QMV table (codebook entry +- 0.125) is not exact in fp16",
+                type_name(qt));
+  const int rm = build_qmm_table(qt, grid16_host, ksigns_host, img_m);
+  if (rv > 0)
+    if (int rc = upload_image(st.qmv_tbls, qt, img_v)) return rc;
+  if (rm > 0)
+    if (int rc = upload_image(st.qmm_tbls, qt, img_m)) return rc;
   return GSQ_OK;
 }
 
@@ -136,6 +154,7 @@ int resolve(int qt, DevTables* tb, int* num_cus, hipStream_t s = nullptr, bool m
   tb->grid16 = nullptr;
   tb->ksigns = st.ksigns;
   tb->qmv_tbl = nullptr;
+  tb->qmm_tbl = nullptr;
   if (is_grid_type(qt)) {
     auto it = st.grids.find(qt);
     if (it == st.grids.end())
@@ -155,6 +174,8 @@ int resolve(int qt, DevTables* tb, int* num_cus, hipStream_t s = nullptr, bool m
   }
   auto tt = st.qmv_tbls.find(qt);
   if (tt != st.qmv_tbls.end()) tb->qmv_tbl = tt->second;
+  auto mt = st.qmm_tbls.find(qt);
+  if (mt != st.qmm_tbls.end()) tb->qmm_tbl = mt->second;
   return GSQ_OK;
 }
 
@@ -279,6 +300,11 @@ int gsq_set_tables(int qt, const float* grid, int64_t entries, int64_t coords, c
       return fail(GSQ_E_VALUE, "%s codebook value %g at %zu is not exact in fp16", type_name(qt), (double)v, i);
     h16[i] = __builtin_bit_cast(uint16_t, h);
   }
+  {  // the QMV image must hold the codebook exactly (IQ1_M's holds entry +- 0.125): check first
+    std::vector<uint8_t> img;
+    if (build_qmv_table(qt, h16.data(), ksigns, img) < 0)
+      return fail(GSQ_E_VALUE, "%s codebook: entry +- 0.125 is not exact in fp16 for some value", type_name(qt));
+  }
   int dev;
   if (int rc = current_device(&dev)) return rc;
   std::lock_guard<std::mutex> lk(g_mu);
@@ -297,7 +323,7 @@ int gsq_set_tables(int qt, const float* grid, int64_t entries, int64_t coords, c
   }
   e = hipMemcpy(g, h16.data(), h16.size() * 2, hipMemcpyHostToDevice);
   if (e != hipSuccess) return fail(GSQ_E_HIP, "hipMemcpy: %s", hipGetErrorString(e));
-  // the QMV kernels of every type that reads this codebook or the ksigns table
+  // the QMV and QMM table images of every type that reads this codebook or the ksigns table
   for (int t : {IQ1_S, IQ1_M, IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S}) {
     if (t != qt && !(uses_ksigns(t) && st.qmv_tbls.count(t))) continue;
     auto git = st.grids.find(t);

@@ -56,6 +56,7 @@ struct DevTables {
   const uint16_t* grid16;   // fp16 codebook, entries x coords (grid types)
   const uint8_t* ksigns;    // [128]
   const uint8_t* qmv_tbl;   // the QMV kernel's LDS table image of this type (see gsq_qmv.hip)
+  const uint8_t* qmm_tbl;   // the QMM kernels' LDS table image of this type
 };
 
 // Launch-plan parameters of the QMV kernel: waves per workgroup, target in-flight weight

@@ -71,9 +71,9 @@ struct QmmGeo {
   static constexpr int kRing = 2 * kCol;                 // per wave: two columns
 };
 
-// Byte size of a type's LDS table image (the QMV kernel's image: fp16 codebook followed by
-// the 16 nibble sign masks, and for IQ2_XXS / IQ2_XS the 128 ksigns masks of four words that
-// their decoders read); checked against the host-built image at launch.
+// Byte size of a type's LDS table image (fp16 codebook followed by the 16 nibble sign masks,
+// and for IQ2_XXS / IQ2_XS the 128 ksigns masks of four words that their decoders read; built
+// by build_qmm_table in gsq_qmv.hip); checked against the host-built image at launch.
 template <int T>
 constexpr int qmm_tbl_bytes() {
   return T == IQ1_S || T == IQ1_M ? 2048 * 8 * 2
@@ -661,7 +661,7 @@ namespace gsq {
 // ---- host side --------------------------------------------------------------------------
 extern QmmTuning g_qmm_tuning;
 
-int qmv_table_bytes(int qt);  // the LDS table image of a type (gsq_qmv.hip)
+int qmm_table_bytes(int qt);  // the QMM kernels' LDS table image of a type (gsq_qmv.hip)
 static bool qmm_grid_type(int qt) {
   return qt == IQ1_S || qt == IQ1_M || qt == IQ2_XXS || qt == IQ2_XS || qt == IQ2_S || qt == IQ3_XXS || qt == IQ3_S;
 }
@@ -826,9 +826,9 @@ static hipError_t launch_qmm_type(const uint8_t* packed, const void* x, int xdt,
     a.nblk = K / 256;
     a.row_bytes = (long long)a.nblk * BlockBytes<T>::v;
     if (qmm_grid_type(T)) {
-      if (!tb.qmv_tbl) return hipErrorInvalidValue;
-      a.tbl = tb.qmv_tbl;
-      a.tbl_bytes = qmv_table_bytes(T);
+      if (!tb.qmm_tbl) return hipErrorInvalidValue;
+      a.tbl = tb.qmm_tbl;
+      a.tbl_bytes = qmm_table_bytes(T);
     }
     return launch_qms<T>(a, num_cus, ws, s);
   }
@@ -844,9 +844,9 @@ static hipError_t launch_qmm_type(const uint8_t* packed, const void* x, int xdt,
     a.nblk = K / 256;
     a.row_bytes = (long long)a.nblk * BlockBytes<T>::v;
     if (qmm_grid_type(T)) {
-      if (!tb.qmv_tbl) return hipErrorInvalidValue;
-      a.tbl = tb.qmv_tbl;
-      a.tbl_bytes = qmv_table_bytes(T);
+      if (!tb.qmm_tbl) return hipErrorInvalidValue;
+      a.tbl = tb.qmm_tbl;
+      a.tbl_bytes = qmm_table_bytes(T);
     }
     return launch_mfma<T>(a, num_cus, ws, s);
   }

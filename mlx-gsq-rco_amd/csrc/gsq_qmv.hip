@@ -305,15 +305,32 @@ template <> struct Qmv<IQ4_XS> {
   }
 };
 
+// Signed half-entry tables (IQ3_S, IQ3_XXS, IQ2_XXS): four codebook values with the signs of
+// one sign nibble applied, for every (entry, nibble) pair, 8 bytes each: a lookup by (entry,
+// nibble) yields the signed fp16 pairs directly, with no sign-mask reads and no XORs (each 8
+// weights cost two 8-byte reads, the bytes of the unsigned entry). Entry-major: byte offset
+// (entry << 7 | nibble << 3) for 4-value entries, (entry << 8 | half << 7 | nibble << 3) for
+// 8-value entries, half 0 holding values 0-3.
+struct LdsV2Off {
+  const uint8_t* p;
+  __device__ __forceinline__ uint2 at(uint32_t byte_off) const {
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p + byte_off);
+    return make_uint2(q[0], q[1]);
+  }
+};
+
+// Sign byte of a ksigns field from the table's closed form (entry i = i with bit 7 the parity
+// of i; the library rejects any other table): k7 | popcount(k7) << 7. Bits 8-9 of the result
+// hold the rest of the popcount, which the callers mask off.
+__device__ __forceinline__ uint32_t ksign_byte(uint32_t k7) {
+  return k7 | (__builtin_amdgcn_ubfe(__builtin_popcount(k7), 0, 3) << 7);
+}
+
 template <> struct Qmv<IQ3_S> {
   static constexpr int kPair = PAIR_NAT;
   static constexpr int kSums = 0;
-  static constexpr int kGridB = 512 * 4 * 2;
-  // grid + 16 nibble sign masks (two words each: a 128-byte table whose reads never conflict;
-  // 256 byte masks of four words were 2-4% slower on the 17408-row shapes, and signs from bit
-  // operations as in IQ2_S, 8 more VALU instructions per 32 weights here, 4% slower at
-  // 5120x17408 and even elsewhere)
-  static constexpr int kTbl = kGridB + 16 * 8;
+  // signed table: 512 entries x 16 sign nibbles x 4 fp16 values
+  static constexpr int kTbl = 512 * 16 * 8;
   static constexpr int kLds = kTbl;  // bytes of it the QMV decoder keeps in LDS
   template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
@@ -325,46 +342,34 @@ template <> struct Qmv<IQ3_S> {
     lds_words<2, A4>(buf, off + 2 + 8 * g, q);
     const uint32_t qh = lds_u8(buf, off + 66 + g);
     const uint32_t sg = lds_w32<A4>(buf, off + 74 + 4 * g);
-    const LdsV2 grid{tbl};
+    const LdsV2Off t{tbl};
     float acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = 0.f;
-    const LdsV2 nm{tbl + kGridB};
-    uint2 Ns[8], Gs[8];
+    uint2 Gs[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {  // all table reads of the group in flight before the first use
-      Gs[e] = grid[bfe(q[e >> 2], 8 * (e & 3), 8) | (bfe(qh, e, 1) << 8)];
-      Ns[e] = nm[bfe(sg, 4 * e, 4)];  // sign nibble of entry e
+      // entry (qs byte | qh bit e << 8) << 7 | sign nibble e << 3 (iq3_s_decode.py:25-33)
+      const uint32_t hi = ((qh << (15 - e)) & 0x8000u) | (bfe(q[e >> 2], 8 * (e & 3), 8) << 7);
+      const uint32_t nb = e == 0 ? (sg << 3) & 0x78u : (sg >> (4 * e - 3)) & 0x78u;
+      Gs[e] = t.at(hi | nb);
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      dacc<MR, XS>(Gs[e].x ^ Ns[e].x, x, 2 * e, acc);
-      dacc<MR, XS>(Gs[e].y ^ Ns[e].y, x, 2 * e + 1, acc);
+      dacc<MR, XS>(Gs[e].x, x, 2 * e, acc);
+      dacc<MR, XS>(Gs[e].y, x, 2 * e + 1, acc);
     }
 #pragma unroll
     for (int m = 0; m < MR; ++m) out[m] += db * acc[m];
   }
 };
 
-// Sign masks of one ksigns field (8 weights, 4 words) for the three ksigns types. The ksigns
-// table has a closed form (entry i = i with bit 7 the parity of i; the library rejects any
-// other table), so the sign byte costs two instructions, and its two nibbles index the 16
-// nibble masks of two words each: a 128-byte table whose reads never conflict, where 16-byte
-// masks read at random from a 2 KB table put these types' LDS ~40% of the time in bank
-// conflicts (17408x5120 products 2.6-4.5% faster, 5120x5120 up to 2.4% slower).
-__device__ __forceinline__ uint4 ksigns_masks(const uint8_t* nib, uint32_t k7) {
-  const uint32_t s8 = k7 | ((__builtin_popcount(k7) & 1u) << 7);
-  const LdsV2 nm{nib};
-  const uint2 lo = nm[s8 & 15u], hi = nm[s8 >> 4];
-  return make_uint4(lo.x, lo.y, hi.x, hi.y);
-}
-
 template <> struct Qmv<IQ3_XXS> {
   static constexpr int kPair = PAIR_NAT;
   static constexpr int kSums = 0;
-  static constexpr int kGridB = 256 * 4 * 2;
-  static constexpr int kTbl = kGridB + 16 * 8;  // grid + 16 nibble sign masks
-  static constexpr int kLds = kTbl;             // bytes of it the QMV decoder keeps in LDS
+  // signed table: 256 entries x 16 sign nibbles x 4 fp16 values
+  static constexpr int kTbl = 256 * 16 * 8;
+  static constexpr int kLds = kTbl;  // bytes of it the QMV decoder keeps in LDS
   template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
@@ -373,24 +378,23 @@ template <> struct Qmv<IQ3_XXS> {
     lds_words<2, A4>(buf, off + 2 + 8 * g, q);
     const uint32_t u = lds_w32<A4>(buf, off + 66 + 4 * g);
     const float d = dh * (0.5f + (float)(u >> 28)) * 0.5f;
-    const LdsV2 grid{tbl};
+    const LdsV2Off t{tbl};
     float acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = 0.f;
-    uint4 M[4];
     uint2 G0[4], G1[4];
 #pragma unroll
     for (int l = 0; l < 4; ++l) {  // all table reads of the group in flight before the first use
-      M[l] = ksigns_masks(tbl + kGridB, bfe(u, 7 * l, 7));
-      G0[l] = grid[bfe(q[l >> 1], 16 * (l & 1), 8)];
-      G1[l] = grid[bfe(q[l >> 1], 16 * (l & 1) + 8, 8)];
+      const uint32_t s8 = ksign_byte(bfe(u, 7 * l, 7));
+      G0[l] = t.at((bfe(q[l >> 1], 16 * (l & 1), 8) << 7) | ((s8 << 3) & 0x78u));
+      G1[l] = t.at((bfe(q[l >> 1], 16 * (l & 1) + 8, 8) << 7) | ((s8 >> 1) & 0x78u));
     }
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
-      dacc<MR, XS>(G0[l].x ^ M[l].x, x, 4 * l, acc);
-      dacc<MR, XS>(G0[l].y ^ M[l].y, x, 4 * l + 1, acc);
-      dacc<MR, XS>(G1[l].x ^ M[l].z, x, 4 * l + 2, acc);
-      dacc<MR, XS>(G1[l].y ^ M[l].w, x, 4 * l + 3, acc);
+      dacc<MR, XS>(G0[l].x, x, 4 * l, acc);
+      dacc<MR, XS>(G0[l].y, x, 4 * l + 1, acc);
+      dacc<MR, XS>(G1[l].x, x, 4 * l + 2, acc);
+      dacc<MR, XS>(G1[l].y, x, 4 * l + 3, acc);
     }
 #pragma unroll
     for (int m = 0; m < MR; ++m) out[m] += d * acc[m];
@@ -400,10 +404,9 @@ template <> struct Qmv<IQ3_XXS> {
 template <> struct Qmv<IQ2_XXS> {
   static constexpr int kPair = PAIR_NAT;
   static constexpr int kSums = 0;
-  static constexpr int kGridB = 256 * 8 * 2;
-  // image: grid, 16 nibble sign masks, then the 128 ksigns masks of four words the QMM decoder reads
-  static constexpr int kTbl = kGridB + 16 * 8 + 128 * 16;
-  static constexpr int kLds = kGridB + 16 * 8;  // bytes of it the QMV decoder keeps in LDS
+  // signed table: 256 entries x 2 halves x 16 sign nibbles x 4 fp16 values
+  static constexpr int kTbl = 256 * 2 * 16 * 8;
+  static constexpr int kLds = kTbl;  // bytes of it the QMV decoder keeps in LDS
   template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
@@ -412,36 +415,48 @@ template <> struct Qmv<IQ2_XXS> {
     lds_words<2, A4>(buf, off + 2 + 8 * g, q);
     const uint32_t u = q[1];
     const float d = dh * (0.5f + (float)(u >> 28)) * 0.25f;
-    const LdsV4 grid{tbl};
+    const LdsV2Off t{tbl};
     float acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = 0.f;
-    // all eight table reads of the group in flight before the first use
-    uint4 M[4], G[4];
+    uint2 G0[4], G1[4];
 #pragma unroll
-    for (int l = 0; l < 4; ++l) {
-      M[l] = ksigns_masks(tbl + kGridB, bfe(u, 7 * l, 7));
-      G[l] = grid[bfe(q[0], 8 * l, 8)];
+    for (int l = 0; l < 4; ++l) {  // all table reads of the group in flight before the first use
+      const uint32_t s8 = ksign_byte(bfe(u, 7 * l, 7));
+      const uint32_t eb = bfe(q[0], 8 * l, 8) << 8;
+      G0[l] = t.at(eb | ((s8 << 3) & 0x78u));
+      G1[l] = t.at((eb | 128u) | ((s8 >> 1) & 0x78u));
     }
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
-      dacc<MR, XS>(G[l].x ^ M[l].x, x, 4 * l, acc);
-      dacc<MR, XS>(G[l].y ^ M[l].y, x, 4 * l + 1, acc);
-      dacc<MR, XS>(G[l].z ^ M[l].z, x, 4 * l + 2, acc);
-      dacc<MR, XS>(G[l].w ^ M[l].w, x, 4 * l + 3, acc);
+      dacc<MR, XS>(G0[l].x, x, 4 * l, acc);
+      dacc<MR, XS>(G0[l].y, x, 4 * l + 1, acc);
+      dacc<MR, XS>(G1[l].x, x, 4 * l + 2, acc);
+      dacc<MR, XS>(G1[l].y, x, 4 * l + 3, acc);
     }
 #pragma unroll
     for (int m = 0; m < MR; ++m) out[m] += d * acc[m];
   }
 };
 
+// Sign masks of one ksigns field (8 weights, 4 words) for IQ2_XS: the sign byte from the
+// table's closed form (two instructions), and its two nibbles index the 16 nibble masks of two
+// words each, a 128-byte table whose reads never conflict (16-byte masks read at random from a
+// 2 KB table put the LDS ~40% of the time in bank conflicts). IQ2_XS's 512-entry codebook is too
+// large for a signed half-entry table (128 KB).
+__device__ __forceinline__ uint4 ksigns_masks(const uint8_t* nib, uint32_t k7) {
+  const uint32_t s8 = k7 | ((__builtin_popcount(k7) & 1u) << 7);
+  const LdsV2 nm{nib};
+  const uint2 lo = nm[s8 & 15u], hi = nm[s8 >> 4];
+  return make_uint4(lo.x, lo.y, hi.x, hi.y);
+}
+
 template <> struct Qmv<IQ2_XS> {
   static constexpr int kPair = PAIR_NAT;
   static constexpr int kSums = 0;
   static constexpr int kGridB = 512 * 8 * 2;
-  // image: grid, 16 nibble sign masks, then the 128 ksigns masks of four words the QMM decoder reads
-  static constexpr int kTbl = kGridB + 16 * 8 + 128 * 16;
-  static constexpr int kLds = kGridB + 16 * 8;  // bytes of it the QMV decoder keeps in LDS
+  static constexpr int kTbl = kGridB + 16 * 8;  // grid, then 16 nibble sign masks
+  static constexpr int kLds = kTbl;             // bytes of it the QMV decoder keeps in LDS
   template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
                              float (&out)[MR]) {
@@ -480,10 +495,9 @@ template <> struct Qmv<IQ2_S> {
   static constexpr int kPair = PAIR_NAT;
   static constexpr int kSums = 0;
   static constexpr int kGridB = 1024 * 8 * 2;
-  // table image: grid + 16 nibble sign masks (the QMM decoder's); QMV applies the signs with
-  // bit operations (SignBits: a third fewer LDS reads per group, 0-2% faster than the nibble
-  // masks) and copies only the grid
-  static constexpr int kTbl = kGridB + 16 * 8;
+  // image: the grid; QMV applies the signs with bit operations (SignBits: a third fewer LDS
+  // reads per group, 0-2% faster than nibble masks)
+  static constexpr int kTbl = kGridB;
   static constexpr int kLds = kGridB;
   template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
@@ -550,10 +564,16 @@ template <> struct Qmv<IQ1_S> {
   }
 };
 
+// IQ1_M's image holds every codebook entry twice, with its delta added (iq_lookup_decode.py:
+// 31-37: w = d (2 s + 1) (grid + delta), delta = -0.125 when bit 3 of the entry's qh nibble is
+// set, else +0.125): entry (nibble << 8 | qs byte) is grid[qs | (nibble & 7) << 8] + delta, so
+// the whole 4-bit nibble indexes it and the group needs no per-entry delta term (values
+// +-0.125 / 0.875 / 1.125 for the published codebook, exact in fp16; the library refuses a
+// codebook for which grid +- 0.125 is not exact).
 template <> struct Qmv<IQ1_M> {
   static constexpr int kPair = PAIR_NAT;
-  static constexpr int kSums = 4;
-  static constexpr int kTbl = 2048 * 8 * 2;
+  static constexpr int kSums = 0;
+  static constexpr int kTbl = 2 * 2048 * 8 * 2;
   static constexpr int kLds = kTbl;  // bytes of it the QMV decoder keeps in LDS
   template <int MR, bool XS, bool A4>
   __device__ static void dot(const uint8_t* buf, uint32_t off, int g, const uint8_t* tbl, const XReg<MR, XS, kSums>& x,
@@ -562,34 +582,34 @@ template <> struct Qmv<IQ1_M> {
     const uint32_t qh = lds_u16(buf, off + 32 + 2 * g);
     uint32_t w[2];
     lds_words<2, A4>(buf, off + 48, w);
-    const uint32_t w0 = w[0] & 0xFFFFu, w1 = w[0] >> 16, w2 = w[1] & 0xFFFFu, w3 = w[1] >> 16;
-    const uint32_t dbits = ((w0 & 61440u) >> 12) | ((w1 & 61440u) >> 8) | ((w2 & 61440u) >> 4) | (w3 & 61440u);
+    // d: the top nibbles of the four scale words (iq_lookup_decode.py:34-35)
+    const uint32_t dbits = ((w[0] >> 12) & 0xFu) | ((w[0] >> 24) & 0xF0u) | ((w[1] >> 4) & 0xF00u) |
+                           ((w[1] >> 16) & 0xF000u);
     const float d = h2f(dbits);
-    const uint32_t ww = (g >> 1) == 0 ? w0 : ((g >> 1) == 1 ? w1 : ((g >> 1) == 2 ? w2 : w3));
-    const uint32_t sh0 = 3u * ((2 * g) & 3);
+    const uint32_t ww = lds_u16(buf, off + 48 + 2 * (g >> 1));  // this group's scale word
+    const uint32_t sh0 = 6u * (g & 1);
     const float d0 = d * (float)(2u * ((ww >> sh0) & 7u) + 1u);
     const float d1 = d * (float)(2u * ((ww >> (sh0 + 3)) & 7u) + 1u);
     const LdsV4 grid{tbl};
-    float a[4][MR];
+    float a0[MR], a1[MR];
 #pragma unroll
-    for (int l = 0; l < 4; ++l)
-#pragma unroll
-      for (int m = 0; m < MR; ++m) a[l][m] = 0.f;
+    for (int m = 0; m < MR; ++m) { a0[m] = 0.f; a1[m] = 0.f; }
     uint4 Gs[4];
 #pragma unroll
-    for (int l = 0; l < 4; ++l) Gs[l] = grid[bfe(qs, 8 * l, 8) | (bfe(qh, 4 * l, 3) << 8)];
+    for (int l = 0; l < 4; ++l) Gs[l] = grid[bfe(qs, 8 * l, 8) | (bfe(qh, 4 * l, 4) << 8)];
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
-      const uint32_t hn = bfe(qh, 4 * l, 4);
       const uint4 G = Gs[l];
-      dacc<MR, XS>(G.x, x, 4 * l, a[l]); dacc<MR, XS>(G.y, x, 4 * l + 1, a[l]);
-      dacc<MR, XS>(G.z, x, 4 * l + 2, a[l]); dacc<MR, XS>(G.w, x, 4 * l + 3, a[l]);
-      const float delta = (hn & 8u) ? -0.125f : 0.125f;
-#pragma unroll
-      for (int m = 0; m < MR; ++m) a[l][m] += delta * x.s8[m][l];
+      if (l < 2) {
+        dacc<MR, XS>(G.x, x, 4 * l, a0); dacc<MR, XS>(G.y, x, 4 * l + 1, a0);
+        dacc<MR, XS>(G.z, x, 4 * l + 2, a0); dacc<MR, XS>(G.w, x, 4 * l + 3, a0);
+      } else {
+        dacc<MR, XS>(G.x, x, 4 * l, a1); dacc<MR, XS>(G.y, x, 4 * l + 1, a1);
+        dacc<MR, XS>(G.z, x, 4 * l + 2, a1); dacc<MR, XS>(G.w, x, 4 * l + 3, a1);
+      }
     }
 #pragma unroll
-    for (int m = 0; m < MR; ++m) out[m] += d0 * (a[0][m] + a[1][m]) + d1 * (a[2][m] + a[3][m]);
+    for (int m = 0; m < MR; ++m) out[m] += d0 * a0[m] + d1 * a1[m];
   }
 };
 
@@ -719,12 +739,17 @@ __device__ __forceinline__ void qmv_load_x1(XReg<MR, XS, Qmv<T>::kSums>& xr, boo
   if constexpr (!XS) {
     // fp16 activations (the only input of the !XS variants): the pairs are byte permutes of
     // the loaded words and the partial sums v_dot2 against (1, 1), with no conversions
+    // Lanes without a group here (act false) and rows past M load group 0 / row M - 1: their
+    // decodes are discarded (the callers select 0 for them, and rows past M are not stored), so
+    // no zero fill is needed.
     (void)dt;
+    (void)act;
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
       uint32_t w[16];
-      if (act && m < M) {
-        const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(x) + (int64_t)m * K + 32 * u);
+      {
+        const int mm = m < M ? m : M - 1;
+        const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(x) + (int64_t)mm * K + 32 * u);
         uint4 v[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) v[k] = p[k];
@@ -732,9 +757,6 @@ __device__ __forceinline__ void qmv_load_x1(XReg<MR, XS, Qmv<T>::kSums>& xr, boo
         for (int k = 0; k < 4; ++k) {
           w[4 * k] = v[k].x; w[4 * k + 1] = v[k].y; w[4 * k + 2] = v[k].z; w[4 * k + 3] = v[k].w;
         }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) w[i] = 0u;
       }
       if constexpr (NS > 0) {
         constexpr uint32_t kOnes = 0x3C003C00u;  // fp16 (1, 1)
@@ -758,9 +780,13 @@ __device__ __forceinline__ void qmv_load_x1(XReg<MR, XS, Qmv<T>::kSums>& xr, boo
       }
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        int e0, e1;
-        pair_idx<P::kPair>(i, e0, e1);
-        xr.h[m][i] = half_pair(w, e0, e1);
+        if constexpr (P::kPair == PAIR_NAT) {
+          xr.h[m][i] = w[i];  // pairs (2i, 2i + 1) are the loaded words
+        } else {
+          int e0, e1;
+          pair_idx<P::kPair>(i, e0, e1);
+          xr.h[m][i] = half_pair(w, e0, e1);
+        }
       }
     }
     return;
@@ -940,7 +966,12 @@ __device__ __forceinline__ void qmv_post_conv(const QmvArgs& a, int64_t r, float
 // stay one row each in the ring (separate buffers).
 // PRE: the variant with the fused activation prologue and convolution epilogue (QmvPre; one
 // fp16 row), a separate instantiation so that the plain kernels carry none of its code.
-template <int T, int MR, bool XS, int GL, bool A4, bool PR = false, bool PRE = false>
+// AL: alignment of the packed rows in the ring. 0: any (2-byte aligned); 1: every item starts
+// 4-byte aligned (packed and row bytes multiples of 4), so an item's offset within its 16-byte
+// granule goes into the wave-uniform buffer base and each lane's offsets within the item (and
+// the funnel shifts of its word reads) stay the same from item to item, computed once; 2: also
+// every superblock starts 4-byte aligned (block bytes a multiple of 4): plain word reads.
+template <int T, int MR, bool XS, int GL, int AL, bool PR = false, bool PRE = false>
 __global__ void __launch_bounds__(qmv_max_threads(qmv_weight(MR, GL, XS))) qmv_kernel(QmvArgs a) {
   static_assert(!PRE || (MR == 1 && !XS), "the fused prologue takes one fp16 row");
   using P = Qmv<T>;
@@ -1020,22 +1051,24 @@ __global__ void __launch_bounds__(qmv_max_threads(qmv_weight(MR, GL, XS))) qmv_k
       for (int k = 0; k < 2 * a.fill && issued < lim; ++k, ++issued)
         dma_item(base + (uintptr_t)issued * stride, item_bytes, a.cdma, ring + (issued % a.nb) * a.sbuf, lane);
       wait_vmcnt((issued - t - np) * a.cdma);
-      const uint8_t* bA = ring + (t % a.nb) * a.sbuf;
-      const uint8_t* bB = np == 2 ? ring + ((t + 1) % a.nb) * a.sbuf : bA;
       const uint32_t dA = (uint32_t)((base + (uintptr_t)t * stride) & 15u);
       const uint32_t dB = np == 2 ? (uint32_t)((base + (uintptr_t)(t + 1) * stride) & 15u) : dA;
+      // AL > 0: the item offsets go into the (uniform) bases, the lane offsets are item-invariant
+      const uint8_t* bA = ring + (t % a.nb) * a.sbuf + (AL ? dA : 0u);
+      const uint8_t* bB = np == 2 ? ring + ((t + 1) % a.nb) * a.sbuf + (AL ? dB : 0u) : bA;
+      const uint32_t eA = AL ? 0u : dA, eB = AL ? 0u : dB;
       float accA[MR], accB[MR], pt[MR];
 #pragma unroll
       for (int m = 0; m < MR; ++m) { accA[m] = 0.f; accB[m] = 0.f; pt[m] = 0.f; }
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         const uint32_t o = (uint32_t)((q * 8 + (lane >> 3)) * BB);
-        P::template dot<MR, XS, A4>(bA, dA + o, lane & 7, tbl, xr[q], accA);
-        if (np == 2) P::template dot<MR, XS, A4>(bB, dB + o, lane & 7, tbl, xr[q], accB);
+        P::template dot<MR, XS, AL == 2>(bA, eA + o, lane & 7, tbl, xr[q], accA);
+        if (np == 2) P::template dot<MR, XS, AL == 2>(bB, eB + o, lane & 7, tbl, xr[q], accB);
       }
       const bool rowA = lane < 32;
-      P::template dot<MR, XS, A4>(rowA ? bA : bB, (rowA ? dA : dB) + (uint32_t)((16 + ((lane & 31) >> 3)) * BB),
-                                  lane & 7, tbl, xr[2], pt);
+      P::template dot<MR, XS, AL == 2>(rowA ? bA : bB, (rowA ? eA : eB) + (uint32_t)((16 + ((lane & 31) >> 3)) * BB),
+                                       lane & 7, tbl, xr[2], pt);
 #pragma unroll
       for (int m = 0; m < MR; ++m) {
         accA[m] += rowA ? pt[m] : 0.f;
@@ -1066,7 +1099,8 @@ __global__ void __launch_bounds__(qmv_max_threads(qmv_weight(MR, GL, XS))) qmv_k
       dma_item(base + (uintptr_t)issued * stride, item_bytes, a.cdma, ring + (issued % a.nb) * a.sbuf, lane);
     const int64_t row = row0 + (int64_t)t * a.slots;
     const uint32_t delta = (uint32_t)((base + (uintptr_t)t * stride) & 15u);
-    const uint8_t* b = ring + buf * a.sbuf;
+    const uint8_t* b = ring + buf * a.sbuf + (AL ? delta : 0u);  // AL > 0: see the paired loop
+    const uint32_t e = AL ? 0u : delta;
     float acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = 0.f;
@@ -1079,7 +1113,7 @@ __global__ void __launch_bounds__(qmv_max_threads(qmv_weight(MR, GL, XS))) qmv_k
         float part[MR];
 #pragma unroll
         for (int m = 0; m < MR; ++m) part[m] = 0.f;
-        P::template dot<MR, XS, A4>(b, delta + (uint32_t)((ok ? blk : 0) * BB), lane & 7, tbl, xr[q], part);
+        P::template dot<MR, XS, AL == 2>(b, e + (uint32_t)((ok ? blk : 0) * BB), lane & 7, tbl, xr[q], part);
 #pragma unroll
         for (int m = 0; m < MR; ++m) acc[m] += ok ? part[m] : 0.f;
       }
@@ -1113,15 +1147,26 @@ __global__ void __launch_bounds__(qmv_max_threads(qmv_weight(MR, GL, XS))) qmv_k
   }
 }
 
-template <int T, int MR, bool XS, int GL, bool A4, bool PR = false, bool PRE = false>
+template <int T, int MR, bool XS, int GL, int AL, bool PR = false, bool PRE = false>
 static hipError_t launch_qmv_t(const QmvArgs& a, int grid, int threads, size_t lds, hipStream_t s) {
-  auto k = qmv_kernel<T, MR, XS, GL, A4, PR, PRE>;
-  static bool attr_set = false;
-  if (!attr_set) {
+  auto k = qmv_kernel<T, MR, XS, GL, AL, PR, PRE>;
+  // 0: not set up; 1: ready; 2: an AL = 1 build that spills registers (its item-invariant lane
+  // offsets stay live across the loop), replaced by the AL = 0 build of the same variant
+  static int state = 0;
+  if (!state) {
     hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
                                        160 * 1024 - Qmv<T>::kLds);
     if (e != hipSuccess) return e;
-    attr_set = true;
+    state = 1;
+    if constexpr (AL == 1) {
+      hipFuncAttributes fa;
+      e = hipFuncGetAttributes(&fa, (const void*)k);
+      if (e != hipSuccess) return e;
+      if (fa.localSizeBytes > 0) state = 2;
+    }
+  }
+  if constexpr (AL == 1) {
+    if (state == 2) return launch_qmv_t<T, MR, XS, GL, 0, PR, PRE>(a, grid, threads, lds, s);
   }
   hipLaunchKernelGGL(k, dim3(grid), dim3(threads), lds, s, a);
   return hipGetLastError();
@@ -1140,32 +1185,37 @@ static int qmv_gl(int mr, bool xs) {
   return 1;
 }
 
-template <int T, bool A4>
+template <int T, int AL>
 static hipError_t launch_qmv_variant(const QmvArgs& a, int mr, bool xs, int gl, int grid, int threads, size_t lds,
                                      hipStream_t s) {
   if (a.pre.op != QMV_PRE_NONE || a.pre.conv_rows > 0) {  // one fp16 row (checked by the plan)
-    if (gl == 1) return launch_qmv_t<T, 1, false, 1, A4, false, true>(a, grid, threads, lds, s);
-    if (a.pair) return launch_qmv_t<T, 1, false, 3, A4, true, true>(a, grid, threads, lds, s);
-    return launch_qmv_t<T, 1, false, 3, A4, false, true>(a, grid, threads, lds, s);
+    if (gl == 1) return launch_qmv_t<T, 1, false, 1, AL, false, true>(a, grid, threads, lds, s);
+    if (a.pair) return launch_qmv_t<T, 1, false, 3, AL, true, true>(a, grid, threads, lds, s);
+    return launch_qmv_t<T, 1, false, 3, AL, false, true>(a, grid, threads, lds, s);
   }
-  if (mr == 1 && !xs && gl == 1) return launch_qmv_t<T, 1, false, 1, A4>(a, grid, threads, lds, s);
-  if (mr == 1 && !xs && a.pair) return launch_qmv_t<T, 1, false, 3, A4, true>(a, grid, threads, lds, s);
-  if (mr == 1) return xs ? launch_qmv_t<T, 1, true, 1, A4>(a, grid, threads, lds, s) : launch_qmv_t<T, 1, false, 3, A4>(a, grid, threads, lds, s);
-  if (mr == 2) return xs ? launch_qmv_t<T, 2, true, 1, A4>(a, grid, threads, lds, s) : launch_qmv_t<T, 2, false, 1, A4>(a, grid, threads, lds, s);
-  if (mr == 4 && !xs) return launch_qmv_t<T, 4, false, 1, A4>(a, grid, threads, lds, s);
+  if (mr == 1 && !xs && gl == 1) return launch_qmv_t<T, 1, false, 1, AL>(a, grid, threads, lds, s);
+  if (mr == 1 && !xs && a.pair) return launch_qmv_t<T, 1, false, 3, AL, true>(a, grid, threads, lds, s);
+  if (mr == 1) return xs ? launch_qmv_t<T, 1, true, 1, AL>(a, grid, threads, lds, s) : launch_qmv_t<T, 1, false, 3, AL>(a, grid, threads, lds, s);
+  if (mr == 2) return xs ? launch_qmv_t<T, 2, true, 1, AL>(a, grid, threads, lds, s) : launch_qmv_t<T, 2, false, 1, AL>(a, grid, threads, lds, s);
+  if (mr == 4 && !xs) return launch_qmv_t<T, 4, false, 1, AL>(a, grid, threads, lds, s);
   return hipErrorInvalidValue;
 }
 
-// Types whose superblock size is a multiple of 4 read their fields with plain dword loads when
-// the packed matrix is 4-byte aligned (every superblock then is); the rest funnel-shift.
+// Alignment variant (qmv_kernel AL): types whose superblock size is a multiple of 4 read their
+// fields with plain dword loads when the packed matrix is 4-byte aligned (every superblock then
+// is); the rest funnel-shift, with item-invariant shifts when the packed matrix and its rows
+// are 4-byte aligned (an even number of superblocks per row), else per item.
 template <int T>
 static hipError_t launch_qmv_type(const QmvArgs& a, int mr, bool xs, int gl, int grid, int threads, size_t lds,
                                   hipStream_t s) {
+  const bool rows4 = (reinterpret_cast<uintptr_t>(a.packed) & 3) == 0 && (a.row_bytes & 3) == 0;
   if constexpr (BlockBytes<T>::v % 4 == 0) {
     if ((reinterpret_cast<uintptr_t>(a.packed) & 3) == 0)
-      return launch_qmv_variant<T, true>(a, mr, xs, gl, grid, threads, lds, s);
+      return launch_qmv_variant<T, 2>(a, mr, xs, gl, grid, threads, lds, s);
+  } else {
+    if (rows4) return launch_qmv_variant<T, 1>(a, mr, xs, gl, grid, threads, lds, s);
   }
-  return launch_qmv_variant<T, false>(a, mr, xs, gl, grid, threads, lds, s);
+  return launch_qmv_variant<T, 0>(a, mr, xs, gl, grid, threads, lds, s);
 }
 
 int qmv_table_bytes(int qt) {
@@ -1198,26 +1248,49 @@ static uint32_t sign_mask_pair_host(uint32_t s, int i) {
   return (((s >> (2 * i)) & 1u) << 15) | (((s >> (2 * i + 1)) & 1u) << 31);
 }
 
-// The exact LDS table image of type qt (qmv_table_bytes(qt) bytes): the fp16 codebook
-// (grid16, entries x coords) followed by the type's sign masks, or the IQ4_XS value pairs.
-// Returns false for a type without a table.
-bool build_qmv_table(int qt, const uint16_t* grid16, const uint8_t* ksigns, std::vector<uint8_t>& out) {
+static int grid_image_bytes(int qt) {
+  switch (qt) {
+    case IQ1_S: case IQ1_M: return 2048 * 8 * 2;
+    case IQ2_XXS: return 256 * 8 * 2;
+    case IQ2_XS: return 512 * 8 * 2;
+    case IQ2_S: return 1024 * 8 * 2;
+    case IQ3_XXS: return 256 * 4 * 2;
+    case IQ3_S: return 512 * 4 * 2;
+    default: return 0;
+  }
+}
+
+// fp16 bits of v if it is exact in fp16, else -1
+static int32_t exact_h(float v) {
+  const _Float16 h = (_Float16)v;
+  return (float)h == v ? (int32_t)__builtin_bit_cast(uint16_t, h) : -1;
+}
+
+// Signed half-entry table (Qmv<IQ3_S / IQ3_XXS / IQ2_XXS>): for every entry e, group of four
+// values hf (halves of an 8-value entry) and sign nibble nb, the four values with bit c of nb
+// flipping the sign of value c, at fp16 index ((e * halves + hf) * 16 + nb) * 4.
+static void build_signed_table(const uint16_t* grid16, int entries, int coords, uint16_t* out) {
+  const int halves = coords / 4;
+  for (int e = 0; e < entries; ++e)
+    for (int hf = 0; hf < halves; ++hf)
+      for (int nb = 0; nb < 16; ++nb)
+        for (int c = 0; c < 4; ++c)
+          out[((e * halves + hf) * 16 + nb) * 4 + c] =
+              (uint16_t)(grid16[e * coords + 4 * hf + c] ^ (((nb >> c) & 1) ? 0x8000u : 0u));
+}
+
+// The exact LDS table image of type qt for the QMV kernel (qmv_table_bytes(qt) bytes; its first
+// kLds bytes are copied into LDS): the IQ4_XS value pairs; the signed half-entry tables of IQ3_S,
+// IQ3_XXS and IQ2_XXS; IQ1_M's codebook with both deltas added; the fp16 codebook of IQ1_S,
+// IQ2_S and IQ2_XS, the last followed by its 16 nibble sign masks. Returns 1 when built, 0 for
+// a type without a table, -1 when a value of the image is not exact in fp16.
+int build_qmv_table(int qt, const uint16_t* grid16, const uint8_t* ksigns, std::vector<uint8_t>& out) {
+  (void)ksigns;
   const int bytes = qmv_table_bytes(qt);
-  if (bytes <= 0) return false;
+  if (bytes <= 0) return 0;
   out.assign((size_t)bytes, 0);
   uint32_t* w = reinterpret_cast<uint32_t*>(out.data());
-  int grid_bytes = 0;
-  switch (qt) {
-    case IQ1_S: case IQ1_M: grid_bytes = 2048 * 8 * 2; break;
-    case IQ2_XXS: grid_bytes = 256 * 8 * 2; break;
-    case IQ2_XS: grid_bytes = 512 * 8 * 2; break;
-    case IQ2_S: grid_bytes = 1024 * 8 * 2; break;
-    case IQ3_XXS: grid_bytes = 256 * 4 * 2; break;
-    case IQ3_S: grid_bytes = 512 * 4 * 2; break;
-    default: break;
-  }
-  if (grid_bytes) std::memcpy(out.data(), grid16, (size_t)grid_bytes);
-  uint32_t* m = reinterpret_cast<uint32_t*>(out.data() + grid_bytes);
+  uint16_t* h = reinterpret_cast<uint16_t*>(out.data());
   switch (qt) {
     case IQ4_XS: {
       static const int8_t kv[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
@@ -1225,18 +1298,62 @@ bool build_qmv_table(int qt, const uint16_t* grid16, const uint8_t* ksigns, std:
         const _Float16 lo = (_Float16)(float)kv[i & 15], hi = (_Float16)(float)kv[i >> 4];
         w[i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
       }
-      break;
+      return 1;
     }
-    case IQ3_S: case IQ2_S: case IQ3_XXS:  // 16 nibble masks, 2 dwords each
+    case IQ3_S: build_signed_table(grid16, 512, 4, h); return 1;
+    case IQ3_XXS: build_signed_table(grid16, 256, 4, h); return 1;
+    case IQ2_XXS: build_signed_table(grid16, 256, 8, h); return 1;
+    case IQ1_M:
+      for (int i = 0; i < 2 * 2048 * 8; ++i) {
+        const float g = (float)__builtin_bit_cast(_Float16, grid16[i & (2048 * 8 - 1)]);
+        const int32_t v = exact_h(g + (i < 2048 * 8 ? 0.125f : -0.125f));
+        if (v < 0) return -1;
+        h[i] = (uint16_t)v;
+      }
+      return 1;
+    case IQ2_XS: {
+      const int gb = grid_image_bytes(qt);
+      std::memcpy(out.data(), grid16, (size_t)gb);
+      uint32_t* m = reinterpret_cast<uint32_t*>(out.data() + gb);
       for (int i = 0; i < 16 * 2; ++i) m[i] = sign_mask_pair_host((uint32_t)(i >> 1), i & 1);
-      break;
-    case IQ2_XXS: case IQ2_XS:  // 16 nibble masks, then 128 ksigns masks of 4 dwords (QMM's)
-      for (int i = 0; i < 16 * 2; ++i) m[i] = sign_mask_pair_host((uint32_t)(i >> 1), i & 1);
-      for (int i = 0; i < 128 * 4; ++i) m[32 + i] = sign_mask_pair_host(ksigns[i >> 2], i & 3);
-      break;
-    default: break;
+      return 1;
+    }
+    case IQ1_S: case IQ2_S:
+      std::memcpy(out.data(), grid16, (size_t)grid_image_bytes(qt));
+      return 1;
+    default: return 0;
   }
-  return true;
+}
+
+// Byte size of the QMM kernels' table image of a type (their decoders' layout): the fp16
+// codebook followed by 16 nibble sign masks (IQ2_S, IQ3_S, IQ3_XXS), and for IQ2_XXS / IQ2_XS
+// the 128 ksigns masks of four words after those; the bare codebook for IQ1_S / IQ1_M.
+int qmm_table_bytes(int qt) {
+  switch (qt) {
+    case IQ1_S: case IQ1_M: return 2048 * 8 * 2;
+    case IQ2_XXS: return 256 * 8 * 2 + 16 * 8 + 128 * 16;
+    case IQ2_XS: return 512 * 8 * 2 + 16 * 8 + 128 * 16;
+    case IQ2_S: return 1024 * 8 * 2 + 16 * 8;
+    case IQ3_XXS: return 256 * 4 * 2 + 16 * 8;
+    case IQ3_S: return 512 * 4 * 2 + 16 * 8;
+    default: return 0;
+  }
+}
+
+// The QMM kernels' table image (qmm_table_bytes(qt) bytes); returns 1 when built, 0 for a type
+// without one.
+int build_qmm_table(int qt, const uint16_t* grid16, const uint8_t* ksigns, std::vector<uint8_t>& out) {
+  const int bytes = qmm_table_bytes(qt);
+  if (bytes <= 0) return 0;
+  out.assign((size_t)bytes, 0);
+  const int gb = grid_image_bytes(qt);
+  std::memcpy(out.data(), grid16, (size_t)gb);
+  uint32_t* m = reinterpret_cast<uint32_t*>(out.data() + gb);
+  if (qt != IQ1_S && qt != IQ1_M)  // 16 nibble masks, 2 dwords each
+    for (int i = 0; i < 16 * 2; ++i) m[i] = sign_mask_pair_host((uint32_t)(i >> 1), i & 1);
+  if (qt == IQ2_XXS || qt == IQ2_XS)  // then 128 ksigns masks of 4 dwords
+    for (int i = 0; i < 128 * 4; ++i) m[32 + i] = sign_mask_pair_host(ksigns[i >> 2], i & 3);
+  return 1;
 }
 
 static constexpr int kLdsBytes = 160 * 1024;

@@ -122,6 +122,9 @@ int upload_qmv_table(DevState& st, int qt, const uint16_t* grid16_host, const ui
     return fail(GSQ_E_VALUE, "%s codebook: a value of the QMV table (codebook entry +- 0.125) is not exact in fp16",
                 type_name(qt));
   const int rm = build_qmm_table(qt, grid16_host, ksigns_host, img_m);
+  if (rm < 0)
+    return fail(GSQ_E_VALUE, "%s codebook: a value of the QMM table (codebook entry +- 0.125) is not exact in fp16",
+                type_name(qt));
   if (rv > 0)
     if (int rc = upload_image(st.qmv_tbls, qt, img_v)) return rc;
   if (rm > 0)
@@ -300,9 +303,9 @@ int gsq_set_tables(int qt, const float* grid, int64_t entries, int64_t coords, c
       return fail(GSQ_E_VALUE, "%s codebook value %g at %zu is not exact in fp16", type_name(qt), (double)v, i);
     h16[i] = __builtin_bit_cast(uint16_t, h);
   }
-  {  // the QMV image must hold the codebook exactly (IQ1_M's holds entry +- 0.125): check first
+  {  // the table images must hold the codebook exactly (IQ1's hold entry +- 0.125): check first
     std::vector<uint8_t> img;
-    if (build_qmv_table(qt, h16.data(), ksigns, img) < 0)
+    if (build_qmv_table(qt, h16.data(), ksigns, img) < 0 || build_qmm_table(qt, h16.data(), ksigns, img) < 0)
       return fail(GSQ_E_VALUE, "%s codebook: entry +- 0.125 is not exact in fp16 for some value", type_name(qt));
   }
   int dev;

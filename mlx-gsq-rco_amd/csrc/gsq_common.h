@@ -103,8 +103,8 @@ struct QmvTuning {
 // Launch-plan overrides of the QMM kernels: activation tile height in 16-row blocks (0 = by
 // M), the fewest K columns (256 wide) per workgroup (0 = default) and waves per workgroup for
 // tiles of 128 or 256 rows (4, or 0 = 8); the small-batch kernel's largest M (0 = 16, -1 =
-// never used), waves (4, or 0 = 8), 16-row blocks per wave (2, or 0 = 1) and fewest columns
-// per workgroup (0 = 1).
+// never used), waves (4, 8 or 16; 0 = 16 on products of at least 2^26 weights, else 8), 16-row
+// blocks per wave (2 or 4 with 4 or 8 waves; 0 = 1) and fewest columns per workgroup (0 = 1).
 struct QmmTuning {
   int mf;
   int min_cols;

@@ -286,20 +286,21 @@ struct QmmDec<IQ2_S, A4> {
   }
 };
 
-// IQ1_S (iq_lookup_decode.py:27-30): w = d*(2*s+1)*(grid[qi][c] + delta) = fma(d, grid, d*delta)
+// IQ1_S (iq_lookup_decode.py:27-30): w = d*(2*s+1)*(grid[qi][c] + delta); the table holds
+// grid + delta (entry qi | 2048 for delta = -0.125, the sign bit 15 of qh)
 template <bool A4>
 struct QmmDec<IQ1_S, A4> {
   __device__ __forceinline__ static void run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
     const uint32_t h = lds_u16(sb, sd + 34 + 2 * g);
     const float d = h2f(lds_u16(sb, sd + 0)) * (float)(2u * ((h >> 12) & 7u) + 1u);
-    const float dd = (h & 32768u) ? -0.125f * d : 0.125f * d;
-    const uint32_t qi = lds_u8(sb, sd + 2 + 4 * g + kq) | (((h >> (3 * kq)) & 7u) << 8);
-    grid8<false>(tbl, qi, d, dd, nullptr, o);
+    const uint32_t qi = lds_u8(sb, sd + 2 + 4 * g + kq) | (((h >> (3 * kq)) & 7u) << 8) | ((h >> 15) << 11);
+    grid8<false>(tbl, qi, d, 0.f, nullptr, o);
   }
 };
 
 // IQ1_M (iq_lookup_decode.py:31-37): w = d*(2*sc+1)*(grid[qi][c] + delta), d from the four
-// scale words' top nibbles
+// scale words' top nibbles; the table holds grid + delta, indexed by the whole qh nibble (bit 3
+// = delta's sign)
 template <bool A4>
 struct QmmDec<IQ1_M, A4> {
   __device__ __forceinline__ static void run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
@@ -309,12 +310,172 @@ struct QmmDec<IQ1_M, A4> {
     const uint32_t dbits = ((w0 & 61440u) >> 12) | ((w1 & 61440u) >> 8) | ((w2 & 61440u) >> 4) | (w3 & 61440u);
     const int oo = 4 * g + kq;
     const uint32_t hn = (lds_u8(sb, sd + 32 + oo / 2) >> (4 * (oo & 1))) & 15u;
-    const uint32_t qi = lds_u8(sb, sd + oo) | ((hn & 7u) << 8);
+    const uint32_t qi = lds_u8(sb, sd + oo) | (hn << 8);
     const int sci = 2 * g + (kq >> 1);
     const uint32_t ww = (sci >> 2) == 0 ? w0 : ((sci >> 2) == 1 ? w1 : ((sci >> 2) == 2 ? w2 : w3));
     const uint32_t sc = (ww >> (3 * (sci & 3))) & 7u;
     const float d = h2f(dbits) * (float)(2u * sc + 1u);
-    grid8<false>(tbl, qi, d, (hn & 8u) ? -0.125f * d : 0.125f * d, nullptr, o);
+    grid8<false>(tbl, qi, d, 0.f, nullptr, o);
+  }
+};
+
+// ---- raw fragments for the small-batch kernel ----------------------------------------------
+// QmsRaw<T>::run gives the eight weights of octet kq of group g without the group's common
+// float scale: codebook values with their signs applied (a sign flip is exact) and, for the
+// types whose sub-scale changes every 16 weights (IQ2_XS, IQ2_S, IQ1_M), multiplied by that
+// sub-scale in fp16 (v_pk_mul_f16: (0.5 + sc) * grid for the IQ2 value sets {8, 25, 43, 62},
+// (2 sc + 1) * (grid +- 0.125) for IQ1, at most 11 significant bits, so exact); it returns the
+// float scale s of the group, whose weights are s times these values. The small-batch kernel
+// multiplies the raw values into a fresh accumulator and adds s times it to the output
+// accumulator: four FMAs per fragment, against one v_fma_mix per weight when every weight is
+// scaled and rounded to fp16 (QmmDec), and every product is formed from the exact weight.
+template <int T, bool A4>
+struct QmsRaw {
+  static constexpr bool kOn = false;
+};
+
+__device__ __forceinline__ uint32_t pk_mul_h(uint32_t v, _Float16 f) {
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, v) * (half2_t){f, f});
+}
+
+template <bool A4>
+struct QmsRaw<IQ3_S, A4> {
+  static constexpr bool kOn = true;
+  static constexpr uint32_t kMaskB = 512 * 4 * 2;
+  __device__ __forceinline__ static float run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+    const float d = h2f(lds_u16(sb, sd + 0));
+    const uint32_t sbyte = lds_u8(sb, sd + 106 + (g >> 1));
+    const float db = d * (float)(1u + 2u * ((sbyte >> (4 * (g & 1))) & 15u));
+    const uint32_t qh = lds_u8(sb, sd + 66 + g);
+    const uint32_t qq = lds_u16(sb, sd + 2 + 8 * g + 2 * kq);
+    const uint32_t i0 = (qq & 0xFFu) | ((qh << (8 - 2 * kq)) & 256u);
+    const uint32_t i1 = (qq >> 8) | ((qh << (7 - 2 * kq)) & 256u);
+    const uint32_t signs = lds_u8(sb, sd + 74 + 4 * g + kq);
+    const uint32_t* e0 = tbl_words(tbl, i0 * 8);
+    const uint32_t* e1 = tbl_words(tbl, i1 * 8);
+    const uint32_t* m0 = tbl_words(tbl, kMaskB + (signs & 15u) * 8);
+    const uint32_t* m1 = tbl_words(tbl, kMaskB + (signs >> 4) * 8);
+    o[0] = e0[0] ^ m0[0];
+    o[1] = e0[1] ^ m0[1];
+    o[2] = e1[0] ^ m1[0];
+    o[3] = e1[1] ^ m1[1];
+    return db;
+  }
+};
+
+template <bool A4>
+struct QmsRaw<IQ3_XXS, A4> {
+  static constexpr bool kOn = true;
+  static constexpr uint32_t kGridB = 256 * 4 * 2;
+  __device__ __forceinline__ static float run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+    const uint32_t u = lds_w32<A4>(sb, sd + 66 + 4 * g);
+    const float d = h2f(lds_u16(sb, sd + 0)) * (0.5f + (float)(u >> 28)) * 0.5f;
+    uint32_t m[4];
+    ksigns_masks(tbl, kGridB, (u >> (7 * kq)) & 127u, m);
+    const uint32_t qq = lds_u16(sb, sd + 2 + 8 * g + 2 * kq);
+    const uint32_t* e0 = tbl_words(tbl, (qq & 0xFFu) * 8);
+    const uint32_t* e1 = tbl_words(tbl, (qq >> 8) * 8);
+    o[0] = e0[0] ^ m[0];
+    o[1] = e0[1] ^ m[1];
+    o[2] = e1[0] ^ m[2];
+    o[3] = e1[1] ^ m[3];
+    return d;
+  }
+};
+
+template <bool A4>
+struct QmsRaw<IQ2_XXS, A4> {
+  static constexpr bool kOn = true;
+  static constexpr uint32_t kGridB = 256 * 8 * 2;
+  __device__ __forceinline__ static float run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+    const uint32_t u = lds_w32<A4>(sb, sd + 2 + 8 * g + 4);
+    const float d = h2f(lds_u16(sb, sd + 0)) * (0.5f + (float)(u >> 28)) * 0.25f;
+    const uint32_t* e = tbl_words(tbl, lds_u8(sb, sd + 2 + 8 * g + kq) * 16);
+    const uint32_t* m = tbl_words(tbl, kGridB + 16 * 8 + ((u >> (7 * kq)) & 127u) * 16);
+    uint32_t ev[4], mv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { ev[i] = e[i]; mv[i] = m[i]; }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = ev[i] ^ mv[i];
+    return d;
+  }
+};
+
+template <bool A4>
+struct QmsRaw<IQ2_XS, A4> {
+  static constexpr bool kOn = true;
+  static constexpr uint32_t kGridB = 512 * 8 * 2;
+  __device__ __forceinline__ static float run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+    const uint32_t q = lds_u16(sb, sd + 2 + 2 * (4 * g + kq));
+    const uint32_t sc = (lds_u8(sb, sd + 66 + g) >> (4 * (kq >> 1))) & 15u;
+    const _Float16 f = (_Float16)(0.5f + (float)sc);
+    const uint32_t* e = tbl_words(tbl, (q & 511u) * 16);
+    const uint32_t* m = tbl_words(tbl, kGridB + 16 * 8 + (q >> 9) * 16);
+    uint32_t ev[4], mv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { ev[i] = e[i]; mv[i] = m[i]; }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = pk_mul_h(ev[i], f) ^ mv[i];
+    return h2f(lds_u16(sb, sd + 0)) * 0.25f;
+  }
+};
+
+template <bool A4>
+struct QmsRaw<IQ2_S, A4> {
+  static constexpr bool kOn = true;
+  static constexpr uint32_t kGridB = 1024 * 8 * 2;
+  __device__ __forceinline__ static float run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+    const int oo = 4 * g + kq;
+    const uint32_t hi = (lds_u8(sb, sd + 66 + g) >> (2 * kq)) & 3u;
+    const uint32_t qi = lds_u8(sb, sd + 2 + oo) | (hi << 8);
+    const uint32_t sc = (lds_u8(sb, sd + 74 + g) >> (4 * (kq >> 1))) & 15u;
+    const _Float16 f = (_Float16)(0.5f + (float)sc);
+    const uint32_t sg = lds_u8(sb, sd + 34 + oo);
+    const uint32_t* e = tbl_words(tbl, qi * 16);
+    const uint32_t* m0 = tbl_words(tbl, kGridB + (sg & 15u) * 8);
+    const uint32_t* m1 = tbl_words(tbl, kGridB + (sg >> 4) * 8);
+    const uint32_t ev[4] = {e[0], e[1], e[2], e[3]};
+    const uint32_t mv[4] = {m0[0], m0[1], m1[0], m1[1]};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = pk_mul_h(ev[i], f) ^ mv[i];
+    return h2f(lds_u16(sb, sd + 0)) * 0.25f;
+  }
+};
+
+template <bool A4>
+struct QmsRaw<IQ1_S, A4> {
+  static constexpr bool kOn = true;
+  __device__ __forceinline__ static float run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+    const uint32_t h = lds_u16(sb, sd + 34 + 2 * g);
+    const uint32_t qi = lds_u8(sb, sd + 2 + 4 * g + kq) | (((h >> (3 * kq)) & 7u) << 8) | ((h >> 15) << 11);
+    const uint32_t* e = tbl_words(tbl, qi * 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = e[i];
+    return h2f(lds_u16(sb, sd + 0)) * (float)(2u * ((h >> 12) & 7u) + 1u);
+  }
+};
+
+template <bool A4>
+struct QmsRaw<IQ1_M, A4> {
+  static constexpr bool kOn = true;
+  __device__ __forceinline__ static float run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g, int kq, uint32_t (&o)[4]) {
+    uint32_t w[2];
+    lds_words<2, A4>(sb, sd + 48, w);
+    const uint32_t dbits = ((w[0] >> 12) & 0xFu) | ((w[0] >> 24) & 0xF0u) | ((w[1] >> 4) & 0xF00u) |
+                           ((w[1] >> 16) & 0xF000u);
+    const int oo = 4 * g + kq;
+    const uint32_t hn = (lds_u8(sb, sd + 32 + oo / 2) >> (4 * (oo & 1))) & 15u;
+    const uint32_t qi = lds_u8(sb, sd + oo) | (hn << 8);
+    const int sci = 2 * g + (kq >> 1);
+    const uint32_t sc = (lds_u16(sb, sd + 48 + 2 * (sci >> 2)) >> (3 * (sci & 3))) & 7u;
+    const _Float16 f = (_Float16)(float)(2u * sc + 1u);
+    const uint32_t* e = tbl_words(tbl, qi * 16);
+    uint32_t ev[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ev[i] = e[i];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = pk_mul_h(ev[i], f);
+    return h2f(dbits);
   }
 };
 

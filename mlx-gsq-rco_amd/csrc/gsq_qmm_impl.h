@@ -72,11 +72,12 @@ struct QmmGeo {
 };
 
 // Byte size of a type's LDS table image (fp16 codebook followed by the 16 nibble sign masks,
-// and for IQ2_XXS / IQ2_XS the 128 ksigns masks of four words that their decoders read; built
-// by build_qmm_table in gsq_qmv.hip); checked against the host-built image at launch.
+// and for IQ2_XXS / IQ2_XS the 128 ksigns masks of four words that their decoders read; for
+// IQ1_S / IQ1_M the codebook with each delta added; built by build_qmm_table in gsq_qmv.hip);
+// checked against the host-built image at launch.
 template <int T>
 constexpr int qmm_tbl_bytes() {
-  return T == IQ1_S || T == IQ1_M ? 2048 * 8 * 2
+  return T == IQ1_S || T == IQ1_M ? 2 * 2048 * 8 * 2
        : T == IQ2_XXS            ? 256 * 8 * 2 + 16 * 8 + 128 * 16
        : T == IQ2_XS             ? 512 * 8 * 2 + 16 * 8 + 128 * 16
        : T == IQ2_S              ? 1024 * 8 * 2 + 16 * 8
@@ -780,8 +781,14 @@ static hipError_t launch_qms_a4(const QmsArgs& a, bool a4, hipStream_t s) {
 template <int T>
 static hipError_t launch_qms(QmsArgs& a, int num_cus, const QmmWorkspace& ws, hipStream_t s) {
   if (a.tbl_bytes != qmm_tbl_bytes<T>()) return hipErrorInvalidValue;
-  const int wv = g_qmm_tuning.small_waves == 4 ? 4 : 8;
-  const int nb = g_qmm_tuning.small_nb == 2 ? 2 : 1;
+  // 16 waves of 16 rows on products of at least 2^26 weights (the 17408-row and 17408-wide 27B
+  // projections: 4-10% faster than 8 waves, whose two waves per SIMD leave the decode's LDS and
+  // MFMA latency exposed; the smaller products, with fewer row groups per CU, are faster with 8)
+  const bool big = (long long)a.N * a.K >= (1ll << 26) && QmsPlan<T, 16, 1>::kValid;
+  const int wv = g_qmm_tuning.small_waves == 4 ? 4
+               : g_qmm_tuning.small_waves == 16 ? 16
+               : g_qmm_tuning.small_waves == 8 ? 8 : (big ? 16 : 8);
+  const int nb = g_qmm_tuning.small_nb == 2 ? 2 : (g_qmm_tuning.small_nb == 4 ? 4 : 1);
   const int rg = wv * 16 * nb;
   const long long units = (((long long)a.N + rg - 1) / rg) * a.nblk;
   if (units >= (1ll << 31)) return hipErrorInvalidValue;
@@ -797,8 +804,12 @@ static hipError_t launch_qms(QmsArgs& a, int num_cus, const QmmWorkspace& ws, hi
   a.part_bytes = ws.part_bytes;
   a.cnt = ws.cnt;
   const bool a4 = (reinterpret_cast<uintptr_t>(a.packed) & 3) == 0;
-  if (wv == 8) return nb == 2 ? launch_qms_a4<T, 8, 2>(a, a4, s) : launch_qms_a4<T, 8, 1>(a, a4, s);
-  return nb == 2 ? launch_qms_a4<T, 4, 2>(a, a4, s) : launch_qms_a4<T, 4, 1>(a, a4, s);
+  if (wv == 16) return launch_qms_a4<T, 16, 1>(a, a4, s);
+  if (wv == 8)
+    return nb == 4 ? launch_qms_a4<T, 8, 4>(a, a4, s) : nb == 2 ? launch_qms_a4<T, 8, 2>(a, a4, s)
+                                                                 : launch_qms_a4<T, 8, 1>(a, a4, s);
+  return nb == 4 ? launch_qms_a4<T, 4, 4>(a, a4, s) : nb == 2 ? launch_qms_a4<T, 4, 2>(a, a4, s)
+                                                               : launch_qms_a4<T, 4, 1>(a, a4, s);
 }
 
 template <int T>

@@ -34,8 +34,9 @@ struct QmsGeo {
   static constexpr int kSlot = kGran * 16;
   static constexpr int kGW = (kRows * kGran + 63) / 64;  // weight DMA instructions per column
   static constexpr int kWCol = kGW * 1024;
-  static constexpr int kXI = 8 / WV;        // activation DMA instructions per column per wave
-  static constexpr int kE = kGW + kXI;      // DMA instructions per column per wave
+  // activation DMA instructions per column per wave (with 16 waves, waves 0-7 issue one each)
+  static constexpr int kXI = WV >= 8 ? 1 : 8 / WV;
+  static constexpr int kE = kGW + kXI;      // DMA instructions per column of a wave that stages activations
 };
 
 constexpr int kQmsX = 16 * 256 * 2;  // one column of activations (16 rows x 256 fp16)
@@ -51,7 +52,7 @@ struct QmsPlan {
   static constexpr int kWOff = kXOff + kD * kQmsX;
   static constexpr int kBcOff = kWOff + kD * WV * G::kWCol;
   static constexpr int kLds = kBcOff + 32;
-  static constexpr bool kValid = kD >= 2 && (WV == 4 || WV == 8) && (kD - 2) * G::kE <= 63;
+  static constexpr bool kValid = kD >= 2 && (WV == 4 || WV == 8 || WV == 16) && (kD - 2) * G::kE <= 63;
 };
 
 struct QmsArgs {
@@ -91,7 +92,7 @@ qms_kernel(QmsArgs args) {
   using Geo = QmsGeo<T, WV, NB>;
   using Plan = QmsPlan<T, WV, NB>;
   constexpr int BB = Geo::kBB, GW = Geo::kGW, GR = Geo::kGran, S = Geo::kSlot, RW = Geo::kRows;
-  constexpr int XI = Geo::kXI, E = Geo::kE, D = Plan::kD, TH = 64 * WV;
+  constexpr int XI = Geo::kXI, D = Plan::kD, TH = 64 * WV;
   static_assert(Plan::kValid, "ring needs two columns");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -109,6 +110,8 @@ qms_kernel(QmsArgs args) {
 
   // activation DMA sources of this lane: instruction i of this wave fills 1 KB (rows 2j, 2j+1)
   // of a column slot; lane -> row m, slot position p, source octet p ^ m
+  const bool xw = wave < 8;  // this wave stages activations (every wave unless there are 16)
+  const int E = Geo::kGW + (xw ? XI : 0);  // its DMA instructions per column
   const _Float16* xsrc[XI];
 #pragma unroll
   for (int i = 0; i < XI; ++i) {
@@ -121,9 +124,11 @@ qms_kernel(QmsArgs args) {
     const int grp = u / nblk, c = u - grp * nblk;
     const int slot = cl % D;
     uint8_t* xb = xring + slot * kQmsX + wave * XI * 1024;
+    if (xw) {
 #pragma unroll
-    for (int i = 0; i < XI; ++i)
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(xsrc[i] + c * 256), (lds_ptr_t)(xb + i * 1024), 16, 0, 0);
+      for (int i = 0; i < XI; ++i)
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(xsrc[i] + c * 256), (lds_ptr_t)(xb + i * 1024), 16, 0, 0);
+    }
     const int n0 = grp * Geo::kRG + wave * RW;
     uint8_t* wb = wring + slot * Geo::kWCol;
 #pragma unroll
@@ -177,8 +182,16 @@ qms_kernel(QmsArgs args) {
 #pragma unroll
       for (int j = 0; j < NB; ++j) {
         uint32_t o[4];
-        QmmDec<T, A4>::run(wb + (16 * j + am) * S, dl[j], tbl, g, aq, o);
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, __builtin_bit_cast(half8_t, o), acc[j], 0, 0, 0);
+        if constexpr (QmsRaw<T, A4>::kOn) {
+          // raw values into a fresh accumulator, scaled once per group
+          const float sc = QmsRaw<T, A4>::run(wb + (16 * j + am) * S, dl[j], tbl, g, aq, o);
+          const float4_t t = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, __builtin_bit_cast(half8_t, o),
+                                                                    (float4_t){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          acc[j] += sc * t;
+        } else {
+          QmmDec<T, A4>::run(wb + (16 * j + am) * S, dl[j], tbl, g, aq, o);
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, __builtin_bit_cast(half8_t, o), acc[j], 0, 0, 0);
+        }
       }
     }
 

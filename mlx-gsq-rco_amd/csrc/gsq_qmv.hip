@@ -1196,7 +1196,11 @@ static hipError_t launch_qmv_variant(const QmvArgs& a, int mr, bool xs, int gl, 
   if (mr == 1 && !xs && gl == 1) return launch_qmv_t<T, 1, false, 1, AL>(a, grid, threads, lds, s);
   if (mr == 1 && !xs && a.pair) return launch_qmv_t<T, 1, false, 3, AL, true>(a, grid, threads, lds, s);
   if (mr == 1) return xs ? launch_qmv_t<T, 1, true, 1, AL>(a, grid, threads, lds, s) : launch_qmv_t<T, 1, false, 3, AL>(a, grid, threads, lds, s);
-  if (mr == 2) return xs ? launch_qmv_t<T, 2, true, 1, AL>(a, grid, threads, lds, s) : launch_qmv_t<T, 2, false, 1, AL>(a, grid, threads, lds, s);
+  if (mr == 2) {
+    if (xs) return launch_qmv_t<T, 2, true, 1, AL>(a, grid, threads, lds, s);
+    return gl == 3 ? launch_qmv_t<T, 2, false, 3, AL>(a, grid, threads, lds, s)
+                   : launch_qmv_t<T, 2, false, 1, AL>(a, grid, threads, lds, s);
+  }
   if (mr == 4 && !xs) return launch_qmv_t<T, 4, false, 1, AL>(a, grid, threads, lds, s);
   return hipErrorInvalidValue;
 }
@@ -1327,10 +1331,11 @@ int build_qmv_table(int qt, const uint16_t* grid16, const uint8_t* ksigns, std::
 
 // Byte size of the QMM kernels' table image of a type (their decoders' layout): the fp16
 // codebook followed by 16 nibble sign masks (IQ2_S, IQ3_S, IQ3_XXS), and for IQ2_XXS / IQ2_XS
-// the 128 ksigns masks of four words after those; the bare codebook for IQ1_S / IQ1_M.
+// the 128 ksigns masks of four words after those; for IQ1_S / IQ1_M the codebook with both
+// deltas added (as IQ1_M's QMV image: entry i is grid[i % 2048] + (i < 2048 ? 0.125 : -0.125)).
 int qmm_table_bytes(int qt) {
   switch (qt) {
-    case IQ1_S: case IQ1_M: return 2048 * 8 * 2;
+    case IQ1_S: case IQ1_M: return 2 * 2048 * 8 * 2;
     case IQ2_XXS: return 256 * 8 * 2 + 16 * 8 + 128 * 16;
     case IQ2_XS: return 512 * 8 * 2 + 16 * 8 + 128 * 16;
     case IQ2_S: return 1024 * 8 * 2 + 16 * 8;
@@ -1345,12 +1350,12 @@ int qmm_table_bytes(int qt) {
 int build_qmm_table(int qt, const uint16_t* grid16, const uint8_t* ksigns, std::vector<uint8_t>& out) {
   const int bytes = qmm_table_bytes(qt);
   if (bytes <= 0) return 0;
+  if (qt == IQ1_S || qt == IQ1_M) return build_qmv_table(IQ1_M, grid16, ksigns, out);  // the delta table
   out.assign((size_t)bytes, 0);
   const int gb = grid_image_bytes(qt);
   std::memcpy(out.data(), grid16, (size_t)gb);
   uint32_t* m = reinterpret_cast<uint32_t*>(out.data() + gb);
-  if (qt != IQ1_S && qt != IQ1_M)  // 16 nibble masks, 2 dwords each
-    for (int i = 0; i < 16 * 2; ++i) m[i] = sign_mask_pair_host((uint32_t)(i >> 1), i & 1);
+  for (int i = 0; i < 16 * 2; ++i) m[i] = sign_mask_pair_host((uint32_t)(i >> 1), i & 1);  // 16 nibble masks
   if (qt == IQ2_XXS || qt == IQ2_XS)  // then 128 ksigns masks of 4 dwords
     for (int i = 0; i < 128 * 4; ++i) m[32 + i] = sign_mask_pair_host(ksigns[i >> 2], i & 3);
   return 1;
@@ -1404,6 +1409,11 @@ static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, 
                                                                        : g_qmv_tuning.gl1_rows;
   const bool gl1 = mr == 1 && !xs && a.nslices <= 3 && N <= gl1_rows;
   if (gl1) gl = 1;
+  // two fp16 rows: three slices per wave once a workgroup has at least 8 rows (17408 x 5120:
+  // 13% faster than one slice per wave, 5120 x 17408 13%, 5120 x 5120 2-4%; with 4 rows per
+  // workgroup, as on 1024 x 5120, three waves per row keep more waves busy and are 12% faster)
+  if (mr == 2 && !xs && N >= 8ll * num_cus && (a.nslices + 2) / 3 <= qmv_max_threads(qmv_weight(2, 3, false)) / 64)
+    gl = 3;
   a.W = (a.nslices + gl - 1) / gl;
   const int wpc = g_qmv_tuning.wg_per_cu < 1 ? 1 : g_qmv_tuning.wg_per_cu;
   const int max_waves = qmv_max_threads(qmv_weight(mr, gl, xs)) / 64;

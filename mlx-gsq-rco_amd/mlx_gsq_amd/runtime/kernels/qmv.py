@@ -42,17 +42,24 @@ def _check_tensors(x, packed):
 
 
 # gfx950 routing beyond the reference's row threshold: from 4 fp16 rows on (3 for matrices of
-# at least 2^24 weights) gsq_qmm's small-batch kernel, which decodes the weights once for all
-# rows, is faster than the vector kernel, whose dot-product work grows with the rows.
+# at least 2^24 weights, 2 when such a matrix is also at least 16384 wide) gsq_qmm's small-batch
+# kernel, which decodes the weights once for all rows, is faster than the vector kernel, whose
+# dot-product work grows with the rows (measured on the 27B projections: 5120 x 17408 Q4_K at
+# 2 rows 24 us against 28 us; 17408 x 5120 IQ2_S at 2 rows 23 us on the vector kernel against
+# 26 us).
 SMALL_BATCH_MIN_ROWS = 4
 SMALL_BATCH_LARGE_MIN_ROWS = 3
 SMALL_BATCH_LARGE_WEIGHTS = 1 << 24
+SMALL_BATCH_WIDE_MIN_ROWS = 2
+SMALL_BATCH_WIDE_K = 16384
 
 
 def _small_batch_faster(rows, dtype, out_features, in_features):
     if dtype != torch.float16:
         return False
     if out_features * in_features >= SMALL_BATCH_LARGE_WEIGHTS:
+        if in_features >= SMALL_BATCH_WIDE_K:
+            return rows >= SMALL_BATCH_WIDE_MIN_ROWS
         return rows >= SMALL_BATCH_LARGE_MIN_ROWS
     return rows >= SMALL_BATCH_MIN_ROWS
 

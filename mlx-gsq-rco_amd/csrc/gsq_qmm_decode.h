@@ -69,6 +69,27 @@ __device__ __forceinline__ void codes8(const uint32_t (&q)[2], float a24, float 
 #endif
 }
 
+// four fp16 pairs h -> {fma(a, h.lo, c), fma(a, h.hi, c)} as one asm block ending in the two
+// wait states an MFMA needs after a VALU write (for results that reach an MFMA directly, with
+// no compiler-visible instruction in between); outputs early-clobber, as in codes8.
+__device__ __forceinline__ void mix8(float a, const uint32_t (&h)[4], float c, uint32_t (&o)[4]) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm("v_fma_mixlo_f16 %0, %4, %5, %6 op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixlo_f16 %1, %4, %7, %6 op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixlo_f16 %2, %4, %8, %6 op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixlo_f16 %3, %4, %9, %6 op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixhi_f16 %0, %4, %5, %6 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixhi_f16 %1, %4, %7, %6 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixhi_f16 %2, %4, %8, %6 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixhi_f16 %3, %4, %9, %6 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+      "s_nop 1"
+      : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3])
+      : "v"(a), "v"(h[0]), "v"(c), "v"(h[1]), "v"(h[2]), "v"(h[3]));
+#else
+  o[0] = h[0]; o[1] = h[1]; o[2] = h[2]; o[3] = h[3]; (void)a; (void)c;
+#endif
+}
+
 __device__ __forceinline__ const uint32_t* tbl_words(const uint8_t* tbl, uint32_t byte_off) {
   return reinterpret_cast<const uint32_t*>(tbl + byte_off);
 }
@@ -205,9 +226,11 @@ __device__ __forceinline__ void grid8(const uint8_t* tbl, uint32_t qi, float d, 
   if constexpr (HM) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) mv[i] = m[i];
-  }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = mix2(d, ev[i], c) ^ mv[i];
+    for (int i = 0; i < 4; ++i) o[i] = mix2(d, ev[i], c) ^ mv[i];  // the XOR is the visible VALU write
+  } else {
+    mix8(d, ev, c, o);  // no sign masks: the asm block carries the MFMA wait states itself
+  }
 }
 
 // Sign masks of one ksigns field (8 weights, 4 words): the sign byte from the ksigns table's

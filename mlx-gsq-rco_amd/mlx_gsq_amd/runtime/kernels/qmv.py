@@ -41,13 +41,13 @@ def _check_tensors(x, packed):
         raise ValueError("x and packed must be on the same GPU device")
 
 
-# gfx950 routing beyond the reference's row threshold: from 4 fp16 rows on (3 for matrices of
+# gfx950 routing beyond the reference's row threshold: from 5 fp16 rows on (3 for matrices of
 # at least 2^24 weights, 2 when such a matrix is also at least 16384 wide) gsq_qmm's small-batch
 # kernel, which decodes the weights once for all rows, is faster than the vector kernel, whose
 # dot-product work grows with the rows (measured on the 27B projections: 5120 x 17408 Q4_K at
-# 2 rows 24 us against 28 us; 17408 x 5120 IQ2_S at 2 rows 23 us on the vector kernel against
-# 26 us).
-SMALL_BATCH_MIN_ROWS = 4
+# 2 rows 23 us against 24 us; 17408 x 5120 IQ2_S at 2 rows 20 us on the vector kernel against
+# 25 us; 1024 x 5120 at 4 rows 6 us on the vector kernel against 7.5 us).
+SMALL_BATCH_MIN_ROWS = 5
 SMALL_BATCH_LARGE_MIN_ROWS = 3
 SMALL_BATCH_LARGE_WEIGHTS = 1 << 24
 SMALL_BATCH_WIDE_MIN_ROWS = 2

@@ -314,14 +314,16 @@ def test_qmm_fp16_output_and_fp32_input(qtype):
     assert rel_l2(y32, want) <= 1e-3
 
 
-@pytest.mark.parametrize("rows,n", [(4, 300), (3, 4096), (2, 4096)])
-def test_matvec_routes_small_fp16_batches(rows, n):
-    """fp16 batches of 4+ rows (3+ on matrices of 2^24+ weights) take the small-batch QMM
-    kernel (fp16-rounded weights, QMM tolerance); 2 rows stay on the vector kernel."""
+@pytest.mark.parametrize("rows,n,K", [(5, 300, 4096), (4, 300, 4096), (3, 4096, 4096), (2, 4096, 4096),
+                                      (2, 1024, 16384)])
+def test_matvec_routes_small_fp16_batches(rows, n, K):
+    """fp16 batches of 5+ rows (3+ on matrices of 2^24+ weights, 2+ when such a matrix is also
+    16384+ wide) take the small-batch QMM kernel (fp16-rounded weights, QMM tolerance); the
+    others stay on the vector kernel."""
     from mlx_gsq_amd.runtime.kernels import qmv
-    K = 4096
     routed = qmv._small_batch_faster(rows, torch.float16, n, K)
-    assert routed == (rows >= 3 and n * K >= 1 << 24 or rows >= 4)
+    big = n * K >= 1 << 24
+    assert routed == (rows >= 5 or (big and rows >= 3) or (big and K >= 16384 and rows >= 2))
     packed = synth.make_packed("Q4_K", n, K, seed=8)
     x = synth.make_x(rows, K, seed=8, dtype=np.float16)
     y = qmv.quantized_matvec(dev(x), dev(packed), qtype="Q4_K", out_features=n, in_features=K,

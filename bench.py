@@ -15,6 +15,8 @@ Printed JSON line (one, on stdout):
                 rocprofv3 counter summary (profiles/qmv_traffic.json) when it covers the
                 same kernel and shape, else null
   per_type      per-type GB/s and fraction of peak over its 4 shapes (kernel time)
+  per_type_graph the same from per_launch_graph_us: each product launched 32 times inside one
+                captured HIP graph (no eager launch cost), median of 3 replays
   per_launch_us time per launch of every (type, shape): median of 3 loops of 32 back-to-back
                 launches of that product alone over 8 rotating weight copies (HIP events)
   qmm           tiled QMM (configs[2]: IQ3_S and Q6_K, both shapes, M in {182, 512, 2048}):
@@ -237,9 +239,11 @@ def run_qmv(steps, warmup, device):
     g1.record(stream)
     torch.cuda.synchronize()
     graph_ms = g0.elapsed_time(g1) / steps
-    # per-product kernel time: loops of back-to-back launches of that product alone
+    # per-product kernel time: loops of back-to-back launches of that product alone, eager and
+    # inside a captured graph
     per_launch = [case_loop(c[0], c[2], c[3], CASE_REPS, device, repeats=CASE_REPEATS) for c in qc.cases]
-    return qc, per_launch, eager_ms, graph_ms
+    per_graph = [case_graph(c[0], c[2], c[3], CASE_REPS, device) for c in qc.cases]
+    return qc, (per_launch, per_graph), eager_ms, graph_ms
 
 
 QMM_TYPES = ("IQ3_S", "Q6_K")
@@ -749,6 +753,46 @@ def case_loop(q, n, k, reps, device, warmup=8, repeats=1):
     return statistics.median(per)
 
 
+def case_graph(q, n, k, reps, device, repeats=3):
+    """The same product launched `reps` times (8 rotating weight copies) inside one captured HIP
+    graph, replayed `repeats` times: median time per launch (us) without the host's eager launch
+    cost (the form the model's decode step runs in)."""
+    import torch
+    from mlx_gsq_amd import _lib, tables
+    from mlx_gsq_amd.formats import TYPE_IDS
+    tables.set_tables(tables.synthetic_tables(0))
+    _lib.ensure_tables(q, device)
+    lib = _lib.lib()
+    copies = [make_device_packed(q, n, k, seed=500 + i, device=device) for i in range(8)]
+    x = torch.randn(1, k, device=device).half()
+    y = torch.empty(1, n, device=device, dtype=torch.float32)
+    stream = torch.cuda.current_stream(device)
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream(device)
+    cap.wait_stream(stream)
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(graph, stream=cap):
+            sh = torch.cuda.current_stream(device).cuda_stream
+            for i in range(reps):
+                rc = lib.gsq_qmv(TYPE_IDS[q], copies[i % 8].data_ptr(), x.data_ptr(), 1, y.data_ptr(), 0, 1, n, k, sh)
+                if rc:
+                    raise RuntimeError(lib.gsq_last_error().decode())
+    stream.wait_stream(cap)
+    graph.replay()
+    torch.cuda.synchronize()
+    per = []
+    for _ in range(repeats):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        graph.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        per.append(e0.elapsed_time(e1) * 1e3 / reps)
+    del graph
+    return statistics.median(per)
+
+
 def profile_case(spec, reps, device):
     """Only one (type, shape) product: the loop the roofline figure is timed with."""
     q, shape = spec.split(":")
@@ -825,7 +869,7 @@ def main():
         tables.set_tables(tables.synthetic_tables(0))
         print(json.dumps({"model_decode": run_model_decode(device)}), flush=True)
         return
-    qc, per_launch, eager_ms, graph_ms = run_qmv(args.steps, args.warmup, device)
+    qc, (per_launch, per_graph), eager_ms, graph_ms = run_qmv(args.steps, args.warmup, device)
     qmm = {} if args.no_qmm else run_qmm(device)
     crossover = {} if args.no_layer else run_crossover(device)
     stack = {} if args.no_layer else run_stack(device)
@@ -836,16 +880,17 @@ def main():
     from mlx_gsq_amd.formats import QTYPES
     step_bytes = qc.step_bytes()
     value = step_bytes / (graph_ms * 1e-3) / 1e9
-    per_type = {}
-    launches = {}
+    per_type, per_type_graph = {}, {}
+    launches, launches_graph = {}, {}
     for i, c in enumerate(qc.cases):
         launches[f"{c[0]} {c[2]}x{c[3]}"] = round(per_launch[i], 2)
+        launches_graph[f"{c[0]} {c[2]}x{c[3]}"] = round(per_graph[i], 2)
     for ti, q in enumerate(QTYPES):
         idx = range(4 * ti, 4 * ti + 4)
         b = sum(qmv_bytes(qc.cases[i][0], qc.cases[i][2], qc.cases[i][3]) for i in idx)
-        us = sum(per_launch[i] for i in idx)
-        gbs = b / (us * 1e-6) / 1e9
-        per_type[q] = {"GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        for times, out in ((per_launch, per_type), (per_graph, per_type_graph)):
+            gbs = b / (sum(times[i] for i in idx) * 1e-6) / 1e9
+            out[q] = {"GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
     # the roofline kernel: Q6_K 17408x5120, the longest launch of the step (checked below), timed
     # on its own as 5 loops of 128 back-to-back launches, median loop (the loop of
     # --profile-case, which the committed kernel trace runs)
@@ -874,7 +919,10 @@ def main():
         "kernel_time_GBs": round(step_bytes / kernel_time / 1e9, 1),
         "mean_type_frac": round(sum(v["frac"] for v in per_type.values()) / len(per_type), 4),
         "per_type": per_type,
+        "mean_type_frac_graph": round(sum(v["frac"] for v in per_type_graph.values()) / len(per_type_graph), 4),
+        "per_type_graph": per_type_graph,
         "per_launch_us": launches,
+        "per_launch_graph_us": launches_graph,
         "qmm": qmm,
         "layer_crossover": crossover,
         "decode_stack": stack,

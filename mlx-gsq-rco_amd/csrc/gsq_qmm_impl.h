@@ -103,34 +103,55 @@ struct QmmPlan {
 };
 
 // The DMA schedule of one wave (per K32 stage q of Q): the table copy, then column 0 and
-// activation stages 0 .. min(LX-1, Q)-1; stage q issues activation stage q + LX - 1 (NX
-// instructions, while it exists) and, at a column start, the next column (GW instructions).
-// Stage q needs the column of stage q + 1 and activation stage q + 1 when the ring has three
-// or more stages (the A operands are read one stage ahead), else activation stage q.
-// qmm_wait_n is the number of this wave's instructions that may still be in flight at that
-// point (vmcnt is in order).
-constexpr int qmm_issued_before(int q, int Q, int LX, int NX, int GW) {
-  const int P = LX - 1 < Q ? LX - 1 : Q;
-  const int x = q < Q - LX + 1 ? q : Q - LX + 1;
+// activation stages 0 .. P-1; each stage issues the next activation stage (NX instructions,
+// while it exists) and, at a column start, the next column (GW instructions). With one barrier
+// per stage (BP false), P = LX - 1 and stage q issues activation stage q + LX - 1; it needs the
+// column of stage q + 1 and activation stage q + 1 when the A operands are read one stage
+// ahead (PF), else activation stage q. With one barrier per pair of stages (BP: rings of four
+// or more stages), P = LX - 2 and the pair (q, q + 1), q even, issues activation stages
+// q + LX - 2 and q + LX - 1 after its barrier, into the slots of stages q - 2 and q - 1, which
+// every wave has finished; it needs activation stages q and q + 1 and the columns of stages
+// q + 1 and q + 2. qmm_wait_n is the number of this wave's instructions that may still be in
+// flight at a wait (vmcnt is in order).
+constexpr int qmm_pro_x(int Q, int LX, bool BP) {
+  const int p = BP ? LX - 2 : LX - 1;
+  return p < Q ? p : Q;
+}
+constexpr int qmm_issued_before(int q, int Q, int LX, int NX, int GW, bool BP) {
+  const int P = qmm_pro_x(Q, LX, BP);
+  int x = 0;
+  if (BP) x = (q + LX - 2 < Q ? q + LX - 2 : Q) - P;
+  else x = q < Q - LX + 1 ? q : Q - LX + 1;
   const int cols = (q + 7) / 8 < Q / 8 - 1 ? (q + 7) / 8 : Q / 8 - 1;
   return GW + NX * P + NX * (x > 0 ? x : 0) + GW * cols;
 }
-constexpr int qmm_end_x(int k, int Q, int LX, int NX, int GW) {
-  const int P = LX - 1 < Q ? LX - 1 : Q;
-  return k < P ? GW + NX * (k + 1) : qmm_issued_before(k - LX + 1, Q, LX, NX, GW) + NX;
+constexpr int qmm_end_x(int k, int Q, int LX, int NX, int GW, bool BP) {
+  const int P = qmm_pro_x(Q, LX, BP);
+  if (k < P) return GW + NX * (k + 1);
+  if (!BP) return qmm_issued_before(k - LX + 1, Q, LX, NX, GW, false) + NX;
+  const int qp = 2 * ((k - LX + 2) >> 1);  // the pair that issues stage k
+  return qmm_issued_before(qp, Q, LX, NX, GW, true) + NX * (k - (qp + LX - 2) + 1);
 }
-constexpr int qmm_wait_n(int q, int Q, int LX, int NX, int GW) {
-  int need = qmm_end_x(LX >= 3 && q + 1 < Q ? q + 1 : q, Q, LX, NX, GW);
-  if (q + 1 < Q) {
-    const int c = (q + 1) / 8;
-    int ew = GW;
-    if (c > 0) {
-      const int qp = 8 * (c - 1);
-      ew = qmm_issued_before(qp, Q, LX, NX, GW) + (qp + LX - 1 < Q ? NX : 0) + GW;
-    }
+constexpr int qmm_end_w(int c, int Q, int LX, int NX, int GW, bool BP) {
+  if (c == 0) return GW;
+  const int qp = 8 * (c - 1);  // the stage (pair) that issues column c, after its activations
+  const int nx = BP ? (qp + LX - 2 < Q ? 1 : 0) + (qp + LX - 1 < Q ? 1 : 0) : (qp + LX - 1 < Q ? 1 : 0);
+  return qmm_issued_before(qp, Q, LX, NX, GW, BP) + NX * nx + GW;
+}
+constexpr int qmm_wait_n(int q, int Q, int LX, int NX, int GW, bool BP, bool PF) {
+  int need = 0, wc = -1;
+  if (BP) {
+    need = qmm_end_x(q + 1, Q, LX, NX, GW, true);
+    wc = (q + 2 < Q ? q + 2 : q + 1) >> 3;
+  } else {
+    need = qmm_end_x(PF && q + 1 < Q ? q + 1 : q, Q, LX, NX, GW, false);
+    wc = q + 1 < Q ? (q + 1) >> 3 : -1;
+  }
+  if (wc >= 0) {
+    const int ew = qmm_end_w(wc, Q, LX, NX, GW, BP);
     need = need > ew ? need : ew;
   }
-  return qmm_issued_before(q, Q, LX, NX, GW) - need;
+  return qmm_issued_before(q, Q, LX, NX, GW, BP) - need;
 }
 // Every count the schedule produces (column counts 1..40 cover the start, steady state and
 // end of any range), distinct, in descending order.
@@ -138,13 +159,13 @@ struct QmmWaitSet {
   int v[64];
   int n;
 };
-template <int LX, int NX, int GW>
+template <int LX, int NX, int GW, bool BP, bool PF>
 constexpr QmmWaitSet qmm_wait_set() {
   QmmWaitSet w{};
   w.n = 0;
   for (int cols = 1; cols <= 40; ++cols)
-    for (int q = 0; q < 8 * cols; ++q) {
-      int c = qmm_wait_n(q, 8 * cols, LX, NX, GW);
+    for (int q = 0; q < 8 * cols; q += BP ? 2 : 1) {
+      int c = qmm_wait_n(q, 8 * cols, LX, NX, GW, BP, PF);
       if (c > 63) c = 63;
       bool seen = false;
       for (int i = 0; i < w.n; ++i) seen = seen || w.v[i] == c;
@@ -165,15 +186,15 @@ __device__ __forceinline__ void wait_vm_imm() {
 }
 // s_waitcnt vmcnt(c) for the largest schedule count c <= n: a short chain of compile-time
 // immediates, largest (steady-state) counts first
-template <int LX, int NX, int GW, int K = 0>
+template <int LX, int NX, int GW, bool BP, bool PF, int K = 0>
 __device__ __forceinline__ void qmm_wait(int n) {
-  constexpr QmmWaitSet W = qmm_wait_set<LX, NX, GW>();
+  constexpr QmmWaitSet W = qmm_wait_set<LX, NX, GW, BP, PF>();
   if constexpr (K >= W.n) {
     wait_vm_imm<0>();
   } else {
     constexpr int c = W.v[K];
     if (n >= c) wait_vm_imm<c>();
-    else qmm_wait<LX, NX, GW, K + 1>(n);
+    else qmm_wait<LX, NX, GW, BP, PF, K + 1>(n);
   }
 }
 
@@ -372,21 +393,13 @@ __global__ void __launch_bounds__(64 * WV, 1) qmm_mfma_kernel(QmmMfmaArgs args) 
     }
   };
 
-  // DMA instructions this wave has issued before the issues of stage q (the table copy
-  // precedes everything and cancels out of every difference below)
-  const int P = min(lx - 1, Q);
-  auto issued_before = [&](int q) {
-    return GW + NX * P + NX * max(0, min(q, Q - lx + 1)) + GW * min((q + 7) >> 3, ncols - 1);
-  };
-  auto end_x = [&](int k) { return k < P ? GW + NX * (k + 1) : issued_before(k - lx + 1) + NX; };
   // A operands one stage ahead when the ring has a stage to spare: stage q reads stage q + 1's
   // activations while its MFMAs run on the operands read during stage q - 1
   constexpr bool PF = LX >= 3 && WV == 4;
-  auto end_w = [&](int c) {
-    if (c == 0) return GW;
-    const int qp = 8 * (c - 1);
-    return issued_before(qp) + (qp + lx - 1 < Q ? NX : 0) + GW;
-  };
+  // one barrier per pair of stages when the ring has four or more stages (the DMA schedule
+  // above; the waves drift apart by up to a stage between barriers)
+  constexpr bool BP = !PF && LX >= 4;
+  const int P = qmm_pro_x(Q, lx, BP);
 
   // B operands of stage q: the four 16-row blocks of the wave's weight rows, group q % 8 of
   // column q / 8; dl = the low address bits of the lane's four superblocks in that column
@@ -426,7 +439,7 @@ __global__ void __launch_bounds__(64 * WV, 1) qmm_mfma_kernel(QmmMfmaArgs args) 
   // prologue: table, column 0 and the first activation stages in flight; stage 0's weights
   issue_w(0);
   for (int q = 0; q < P; ++q) xi.issue(xring, wave, lane);
-  qmm_wait<LX, NX, GW>(NX * (P - 1));  // table, column 0 and stage 0 (this wave's share)
+  qmm_wait<LX, NX, GW, BP, PF>(NX * (P - 1));  // table, column 0 and stage 0 (this wave's share)
   __syncthreads();
   uint32_t dl[NB];
   col_delta(0, dl);
@@ -455,15 +468,21 @@ __global__ void __launch_bounds__(64 * WV, 1) qmm_mfma_kernel(QmmMfmaArgs args) 
     auto stage = [&](int q, const half8_t (&ua)[MF], const half8_t (&ub_)[NB], half8_t (&na)[MF],
                      half8_t (&nb)[NB]) __attribute__((always_inline)) {
       const int cl = q >> 3;
-      {  // the activations read now and the column of stage q + 1 have landed (this wave's DMAs)
-        int need = end_x(PF && q + 1 < Q ? q + 1 : q);
-        if (q + 1 < Q) need = max(need, end_w((q + 1) >> 3));
-        qmm_wait<LX, NX, GW>(issued_before(q) - need);
+      if (!BP || (q & 1) == 0) {
+        // the activations read until the next wait and the columns decoded until then have
+        // landed (this wave's DMAs)
+        qmm_wait<LX, NX, GW, BP, PF>(qmm_wait_n(q, Q, lx, NX, GW, BP, PF));
+        // every wave's DMAs of those stages are in; every wave is done with the slots of the
+        // stages before them
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if constexpr (BP) {
+          if (q + lx - 2 < Q) xi.issue(xring, wave, lane);
+          if (q + lx - 1 < Q) xi.issue(xring, wave, lane);
+        } else {
+          if (q + lx - 1 < Q) xi.issue(xring, wave, lane);
+        }
+        if ((q & 7) == 0 && cl + 1 < ncols) issue_w(cl + 1);
       }
-      // every wave's DMAs of stage q are in; every wave is done with stage q - 1's buffer
-      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      if (q + lx - 1 < Q) xi.issue(xring, wave, lane);
-      if ((q & 7) == 0 && cl + 1 < ncols) issue_w(cl + 1);
       // weights of stage q + 1 (after the last stage they come from stale, in-bounds LDS and
       // are not used): unconditional, in one scheduling region with the MFMAs
       if (((q + 1) & 7) == 0) col_delta(q + 1, dl);

@@ -260,6 +260,44 @@ __device__ __forceinline__ void qmm_store_tile(void* y, int ydt, int M, int N, c
     }
 }
 
+// One 16-row block of a wave's output (v[j][e]: row m + 4 (lane / 16) + e, column
+// n0 + 16 j + lane % 16) written as whole row pieces: the wave transposes it through its own
+// LDS area `st` (16 rows of 16 NB floats, row stride 16 NB + 4) and every lane stores 8
+// consecutive fp32 outputs of one row with two 16-byte stores, so each row piece of 64 NB bytes
+// is written whole (the accumulator layout alone gives four rows of 64 bytes per store
+// instruction). The LDS operations of one wave complete in order, so the reads see the writes.
+template <int NB>
+__device__ __forceinline__ void qmm_store_rows_f32(float* y, int M, int N, const float4_t (&v)[NB], int m, int n0,
+                                                   int lane, float* st) {
+  constexpr int W = 16 * NB, S = W + 4, LPR = W / 8, RPP = 64 / LPR;
+#pragma unroll
+  for (int j = 0; j < NB; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) st[(4 * (lane >> 4) + e) * S + 16 * j + (lane & 15)] = v[j][e];
+#pragma unroll
+  for (int r0 = 0; r0 < 16; r0 += RPP) {
+    const int r = r0 + lane / LPR, c = 8 * (lane % LPR);
+    if (r < 16) {
+      const float4_t a = *reinterpret_cast<const float4_t*>(st + r * S + c);
+      const float4_t b = *reinterpret_cast<const float4_t*>(st + r * S + c + 4);
+      const int mm = m + r, nn = n0 + c;
+      if (mm < M) {
+        float* yp = y + (int64_t)mm * N + nn;
+        if (nn + 8 <= N) {
+          *reinterpret_cast<float4_t*>(yp) = a;
+          *reinterpret_cast<float4_t*>(yp + 4) = b;
+        } else {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            if (nn + k < N) yp[k] = a[k];
+            if (nn + 4 + k < N) yp[4 + k] = b[k];
+          }
+        }
+      }
+    }
+  }
+}
+
 // Issues the activation stages of one workgroup in order: stage q (ring slot b) of tile t,
 // column c; row[i] = this lane's source row (clamped to the matrix) and octet for DMA
 // instruction i, laid out for the XOR-swizzled ring (octet o of row m at o ^ ((m >> 2) & 3)).
@@ -435,6 +473,11 @@ __global__ void __launch_bounds__(64 * WV, 1) qmm_mfma_kernel(QmmMfmaArgs args) 
     }
   };
   int* bc = reinterpret_cast<int*>(dyn + Plan::kBcOff);
+  // the per-wave transpose areas of the final row stores, over the rings
+  constexpr int kSt = 16 * (16 * NB + 4);  // floats per wave
+  static_assert(WV * kSt * 4 <= Plan::kBcOff - Plan::kXOff, "row-store areas exceed the rings");
+  float* const st = reinterpret_cast<float*>(xring) + wave * kSt;
+  const bool yrows = ydt == QDT_F32 && (N & 3) == 0 && (reinterpret_cast<uintptr_t>(yg) & 15) == 0;
 
   // prologue: table, column 0 and the first activation stages in flight; stage 0's weights
   issue_w(0);
@@ -515,8 +558,18 @@ __global__ void __launch_bounds__(64 * WV, 1) qmm_mfma_kernel(QmmMfmaArgs args) 
     // end of this workgroup's part of `tile`
     const int wf = qmm_owner(tile * nblk, units, G);
     const int wl = qmm_owner(tile * nblk + nblk - 1, units, G);
+    // after the workgroup's last stage the rings hold nothing that is still needed: fp32 rows
+    // of the tile are then written whole through a per-wave LDS transpose
+    const bool end_lds = yrows && q1 == Q;
     if (wf == wl) {
-      qmm_store_tile<MF, NB>(yg, ydt, M, N, acc, m0, n0, lane);
+      if (end_lds) {
+        __syncthreads();  // every wave is done with the rings
+#pragma unroll
+        for (int i = 0; i < MF; ++i)
+          if (m0 + 16 * i < M) qmm_store_rows_f32<NB>(static_cast<float*>(yg), M, N, acc[i], m0 + 16 * i, n0, lane, st);
+      } else {
+        qmm_store_tile<MF, NB>(yg, ydt, M, N, acc, m0, n0, lane);
+      }
     } else {
       // slot 2w: the tile this workgroup starts in; slot 2w + 1: the tile it ends in
       const int slot = 2 * w + (q0 == 0 ? 0 : 1);
@@ -553,14 +606,25 @@ __global__ void __launch_bounds__(64 * WV, 1) qmm_mfma_kernel(QmmMfmaArgs args) 
 #pragma unroll
             for (int t = 0; t < CH; ++t) sum[t] += ld[t];
           }
+          if (end_lds) {
 #pragma unroll
-          for (int t = 0; t < CH; ++t) {
-            const int ij = ij0 + t;
-            const int n = nb + 16 * (ij % NB);
+            for (int a = 0; a < CH / NB; ++a) {
+              const int i = ij0 / NB + a;
+              float4_t v[NB];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int m = mb + 16 * (ij / NB) + e;
-              if (m < M && n < N) qmm_store_y(yg, ydt, (int64_t)m * N + n, sum[t][e]);
+              for (int j = 0; j < NB; ++j) v[j] = sum[a * NB + j];
+              if (m0 + 16 * i < M) qmm_store_rows_f32<NB>(static_cast<float*>(yg), M, N, v, m0 + 16 * i, n0, lane, st);
+            }
+          } else {
+#pragma unroll
+            for (int t = 0; t < CH; ++t) {
+              const int ij = ij0 + t;
+              const int n = nb + 16 * (ij % NB);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int m = mb + 16 * (ij / NB) + e;
+                if (m < M && n < N) qmm_store_y(yg, ydt, (int64_t)m * N + n, sum[t][e]);
+              }
             }
           }
         }

@@ -24,7 +24,8 @@ Printed JSON line (one, on stdout):
   layer_crossover  configs[3]: QMV vs QMM time per projection of the mixed layer, M in 1..16
   decode_stack  configs[4]: 448 GEMVs (64 layers, 8.34 GB) in one HIP graph: GB/s, tokens/s
   decode_stack_fused  the same products with q|k and gate|up fused (320 launches)
-  decode_stack_grouped  the same through GSQGroupedLinear / GSQLinear modules (fp16 outputs)
+  decode_stack_grouped  the same through GSQGroupedLinear / GSQLinear modules (fp16 outputs; q|k
+                and v as one two-product launch, gate|up fused: 256 launches)
   model_decode  single-token decode of the whole 27B Qwen3.5-hybrid model (norms, GatedDeltaNet,
                 attention, MLP, lm_head) as one HIP graph per step: model tokens/s; `batched`:
                 8 sequences decoded together (tokens/s over all of them); `prefill`: one
@@ -488,10 +489,10 @@ def run_stack(device, layers=64, reps=10, fused=False):
 
 
 def run_stack_grouped(device, layers=64, reps=10):
-    """configs[4] through the modules a model uses: per layer GSQGroupedLinear(q, k, v) (q|k one
-    IQ2_XS launch, then v IQ4_XS), GSQLinear(o), GSQGroupedLinear(gate, up) (one IQ2_S launch)
-    and GSQLinear(down), at M=1 with fp16 outputs, the 64 layers captured in one HIP graph and
-    replayed."""
+    """configs[4] through the modules a model uses: per layer GSQGroupedLinear(q, k, v) (q|k
+    IQ2_XS and v IQ4_XS in one two-product launch), GSQLinear(o), GSQGroupedLinear(gate, up)
+    (one IQ2_S launch) and GSQLinear(down), at M=1 with fp16 outputs, the 64 layers captured in
+    one HIP graph and replayed (4 launches per layer)."""
     import torch
     from mlx_gsq_amd import _lib
     from mlx_gsq_amd.formats import BLOCK_BYTES, TYPE_IDS
@@ -547,7 +548,7 @@ def run_stack_grouped(device, layers=64, reps=10):
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / reps
     gbs = total / (ms * 1e-3) / 1e9
-    res = {"gemvs": 7 * layers, "launches": 5 * layers, "bytes": int(total), "ms_per_token": round(ms, 4),
+    res = {"gemvs": 7 * layers, "launches": 4 * layers, "bytes": int(total), "ms_per_token": round(ms, 4),
            "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "linear_tokens_per_s": round(1e3 / ms, 1),
            "mix": "as decode_stack; GSQGroupedLinear(q,k,v) and (gate,up), fp16 outputs"}
     del mods, graph

@@ -2,6 +2,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -20,6 +21,9 @@ hipError_t launch_qmv_pre(int qt, const uint8_t* packed, const void* x, void* y,
 hipError_t launch_qmv(int qt, const uint8_t* packed, const void* x, int xdt, void* y, int ydt, int64_t M, int64_t N,
                       int K, const DevTables& tb, int num_cus, hipStream_t s);
 hipError_t launch_stage_copy(const void* src, void* dst, int64_t bytes, hipStream_t s);
+hipError_t launch_qmv_group2(int qt0, const uint8_t* p0, int64_t N0, void* y0, const DevTables& tb0, int qt1,
+                             const uint8_t* p1, int64_t N1, void* y1, const DevTables& tb1, const void* x, int ydt,
+                             int K, int num_cus, hipStream_t s);
 hipError_t launch_qmm(int qt, const uint8_t* packed, const void* x, int xdt, void* y, int ydt, int64_t M, int64_t N,
                       int K, const DevTables& tb, int num_cus, const QmmWorkspace& ws, hipStream_t s);
 hipError_t launch_embedding(int qt, const uint8_t* packed, const void* ids, int ids64, int64_t n_ids, int64_t vocab,
@@ -418,6 +422,36 @@ int gsq_qmv(int qt, const void* packed, const void* x, int xdt, void* y, int ydt
     if (e != hipSuccess) return fail(GSQ_E_HIP, "qmv launch: %s", hipGetErrorString(e));
   }
   return GSQ_OK;
+}
+
+int gsq_qmv_group2(int qt0, const void* packed0, int64_t N0, void* y0, int qt1, const void* packed1, int64_t N1,
+                   void* y1, const void* x, int y_dtype, int64_t K, void* stream) {
+  if (int rc = check_common(qt0, packed0, 1, N0, K, GSQ_F16, y_dtype)) return rc;
+  if (int rc = check_common(qt1, packed1, 1, N1, K, GSQ_F16, y_dtype)) return rc;
+  if (!x || !y0 || !y1) return fail(GSQ_E_VALUE, "NULL pointer");
+  if (K > 65536) return fail(GSQ_E_VALUE, "QMV supports K <= 65536 for fp16 activations (got %lld)", (long long)K);
+  if (reinterpret_cast<uintptr_t>(x) & 1) return fail(GSQ_E_VALUE, "x is not aligned to its element size");
+  // every workgroup reads x while others already write their outputs
+  const int64_t ye = y_dtype == GSQ_F32 ? 4 : 2;
+  if (overlaps(y0, N0 * ye, y1, N1 * ye) || overlaps(y0, N0 * ye, x, K * 2) || overlaps(y1, N1 * ye, x, K * 2))
+    return fail(GSQ_E_VALUE, "y0, y1 and x must not overlap");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  DevTables tb0, tb1;
+  int cus;
+  if (int rc = resolve(qt0, &tb0, &cus, s)) return rc;
+  if (int rc = resolve(qt1, &tb1, &cus, s)) return rc;
+  if ((reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+    hipError_t e = launch_qmv_group2(qt0, static_cast<const uint8_t*>(packed0), N0, y0, tb0, qt1,
+                                     static_cast<const uint8_t*>(packed1), N1, y1, tb1, x, y_dtype, (int)K, cus, s);
+    if (e == hipSuccess) return GSQ_OK;
+    if (e != hipErrorNotSupported) return fail(GSQ_E_HIP, "qmv group launch: %s", hipGetErrorString(e));
+  }
+  // (for tests of the shared kernel: refuse instead of launching the products one by one)
+  if (std::getenv("GSQ_QMV_GROUP_NO_FALLBACK"))
+    return fail(GSQ_E_UNSUPPORTED, "the shared kernel does not take these two products");
+  // the two products one by one (plans the shared kernel does not take, or an x to stage)
+  if (int rc = gsq_qmv(qt0, packed0, x, GSQ_F16, y0, y_dtype, 1, N0, K, stream)) return rc;
+  return gsq_qmv(qt1, packed1, x, GSQ_F16, y1, y_dtype, 1, N1, K, stream);
 }
 
 int gsq_qmv_pre(int qt, const void* packed, int pre_op, const void* x, const void* pre_a, const void* pre_w,

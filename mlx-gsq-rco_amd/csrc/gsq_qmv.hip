@@ -51,6 +51,7 @@ struct QmvArgs {
   int cdma;         // DMA instructions per item
   int fill;         // most ring items issued per main-loop step (per item pair: 2 x fill)
   int pair;         // items decoded in pairs (the PR variant of qmv_kernel)
+  int qtype;        // the type id (read by the kernel over two products of any types)
   int tbl_bytes, x_off, x_bytes, x_lds, red_off, ring_off;  // LDS layout
   int conv_lds, conv_off;  // prefetched convolution inputs (16 bytes per row of the workgroup)
   DevTables tb;
@@ -971,24 +972,35 @@ __device__ __forceinline__ void qmv_post_conv(const QmvArgs& a, int64_t r, float
 // granule goes into the wave-uniform buffer base and each lane's offsets within the item (and
 // the funnel shifts of its word reads) stay the same from item to item, computed once; 2: also
 // every superblock starts 4-byte aligned (block bytes a multiple of 4): plain word reads.
-template <int T, int MR, bool XS, int GL, int AL, bool PR = false, bool PRE = false>
-__global__ void __launch_bounds__(qmv_max_threads(qmv_weight(MR, GL, XS))) qmv_kernel(QmvArgs a) {
+// The kernel body for workgroup `bid` of the product `a`. The type's LDS table is static LDS at
+// address 0 (a constant the table reads fold into their address arithmetic), or with DT the
+// start of dynamic LDS (kernels over products of several types); either way the layout offsets
+// of `a` count from the table's start. Both are derived from the LDS arrays here, so that every
+// access through them is known to be an LDS access.
+template <int T, int MR, bool XS, int GL, int AL, bool PR, bool PRE, bool DT = false>
+__device__ __forceinline__ void qmv_body(const QmvArgs& a, int bid) {
   static_assert(!PRE || (MR == 1 && !XS), "the fused prologue takes one fp16 row");
   using P = Qmv<T>;
   constexpr int BB = BlockBytes<T>::v;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint8_t* tbl;
+  uint8_t* dyn;
+  if constexpr (DT) {
+    tbl = smem;
+    dyn = smem;
+  } else {
+    tbl = QmvTblLds<P::kLds>::get();
+    dyn = smem - a.tbl_bytes;
+  }
   // the wave index as a wave-uniform (scalar) value: everything derived from it (row slot,
   // item count, DMA wait counts, loop bounds) then stays in scalar registers and branches
   const int tid = threadIdx.x, lane = tid & 63, nw = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // layout offsets count from the table's start; dynamic LDS starts where the table ends
-  uint8_t* tbl = QmvTblLds<P::kLds>::get();
-  uint8_t* dyn = smem - a.tbl_bytes;
   uint8_t* xst = dyn + a.x_off;
   float* red = reinterpret_cast<float*>(dyn + a.red_off);   // [rows_per_wg][MR][W]
   uint8_t* ring = dyn + a.ring_off + wave * a.nb * a.sbuf;  // this wave's ring
 
-  const int64_t r0 = (int64_t)blockIdx.x * a.rows_per_wg;
+  const int64_t r0 = (int64_t)bid * a.rows_per_wg;
   const int64_t r1 = min(a.N, r0 + (int64_t)a.rows_per_wg);
   // row slot of this wave and its K range (slices sl0 .. sl0 + nq - 1). Slot s takes rows
   // r0 + s, r0 + s + slots, ...: at any time the waves of a workgroup read neighbouring rows,
@@ -1145,6 +1157,11 @@ __global__ void __launch_bounds__(qmv_max_threads(qmv_weight(MR, GL, XS))) qmv_k
       }
     }
   }
+}
+
+template <int T, int MR, bool XS, int GL, int AL, bool PR = false, bool PRE = false>
+__global__ void __launch_bounds__(qmv_max_threads(qmv_weight(MR, GL, XS))) qmv_kernel(QmvArgs a) {
+  qmv_body<T, MR, XS, GL, AL, PR, PRE>(a, blockIdx.x);
 }
 
 template <int T, int MR, bool XS, int GL, int AL, bool PR = false, bool PRE = false>
@@ -1384,11 +1401,21 @@ static int qmv_rows_per_launch(int xdt) { return xdt == DT_F16 ? 4 : 2; }
 
 // Launch plan for up to 4 activation rows: one workgroup of nw waves per CU, each owning about
 // N / #CU consecutive rows; W waves per row (ceil(slices / GL)), nw / W row slots.
+// A plan computed without a launch (launch_qmv_rows with `plan`): the arguments, the slices per
+// wave and the launch shape, with the table counted in the dynamic LDS size (the kernel over two
+// products keeps both tables there).
+struct QmvPlan {
+  QmvArgs a;
+  int gl, grid, threads;
+  size_t lds;
+};
+
 static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, int xdt, void* y, int ydt, int mr,
                                   int M, int64_t N, int K, const DevTables& tb, int num_cus, hipStream_t s,
-                                  const QmvPre& pre = QmvPre()) {
+                                  const QmvPre& pre = QmvPre(), QmvPlan* plan = nullptr) {
   QmvArgs a;
   a.packed = packed; a.x = x; a.y = y; a.N = N; a.K = K; a.M = M; a.x_dtype = xdt; a.y_dtype = ydt; a.tb = tb;
+  a.qtype = qt;
   a.pre = pre;
   const bool has_pre = pre.op != QMV_PRE_NONE;
   if (has_pre && (M != 1 || xdt != DT_F16 || (K & 7))) return hipErrorInvalidValue;
@@ -1407,7 +1434,7 @@ static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, 
   // idle), while IQ4_XS and Q6_K (never paired) are 5-17% slower with it and the rest even
   const int gl1_rows = (qt == IQ1_S || qt == IQ2_XXS || qt == IQ2_XS) ? std::min(g_qmv_tuning.gl1_rows, 4096)
                                                                        : g_qmv_tuning.gl1_rows;
-  const bool gl1 = mr == 1 && !xs && a.nslices <= 3 && N <= gl1_rows;
+  const bool gl1 = !plan && mr == 1 && !xs && a.nslices <= 3 && N <= gl1_rows;
   if (gl1) gl = 1;
   // two fp16 rows: three slices per wave once a workgroup has at least 8 rows (17408 x 5120:
   // 13% faster than one slice per wave, 5120 x 17408 13%, 5120 x 5120 2-4%; with 4 rows per
@@ -1474,6 +1501,14 @@ static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, 
   const int threads = nw * 64;
   const size_t lds_all = (size_t)a.ring_off + (size_t)nw * nb * a.sbuf;
   if (lds_all > (size_t)lds_cap) return hipErrorInvalidValue;
+  if (plan) {
+    plan->a = a;
+    plan->gl = gl;
+    plan->grid = grid;
+    plan->threads = threads;
+    plan->lds = lds_all;
+    return hipSuccess;
+  }
   const size_t lds = lds_all - (size_t)a.tbl_bytes;  // dynamic part: the table is static LDS
   switch (qt) {
     case Q2_K: return launch_qmv_type<Q2_K>(a, mr, xs, gl, grid, threads, lds, s);
@@ -1489,6 +1524,64 @@ static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, 
     case IQ1_M: return launch_qmv_type<IQ1_M>(a, mr, xs, gl, grid, threads, lds, s);
     default: return hipErrorInvalidValue;
   }
+}
+
+// ---- two products of one activation row in one launch -----------------------------------
+// Workgroups [0, g0) compute product a0, the rest product a1, each with the body of its own
+// type (a switch on the type id; every type but Q6_K, which is never decoded in item pairs)
+// and its own launch plan; both tables sit at the start of dynamic LDS. The alignment variant
+// per type is fixed (plain word reads for superblocks of a multiple of 4 bytes, else
+// item-invariant funnel shifts; IQ3_S, whose build with those spills registers, per item), so
+// the launcher requires 4-byte aligned packed matrices and rows.
+template <int T>
+constexpr int qmv_group_al() { return BlockBytes<T>::v % 4 == 0 ? 2 : (T == IQ3_S ? 0 : 1); }
+
+__device__ __forceinline__ void qmv_group_part(const QmvArgs& a, int bid) {
+#define GSQ_QMV_GROUP_CASE(T) \
+  case T: qmv_body<T, 1, false, 3, qmv_group_al<T>(), true, false, true>(a, bid); break;
+  switch (a.qtype) {
+    GSQ_QMV_GROUP_CASE(Q2_K) GSQ_QMV_GROUP_CASE(Q4_K) GSQ_QMV_GROUP_CASE(IQ4_XS) GSQ_QMV_GROUP_CASE(IQ3_S)
+    GSQ_QMV_GROUP_CASE(IQ3_XXS) GSQ_QMV_GROUP_CASE(IQ2_XXS) GSQ_QMV_GROUP_CASE(IQ2_XS) GSQ_QMV_GROUP_CASE(IQ2_S)
+    GSQ_QMV_GROUP_CASE(IQ1_S) GSQ_QMV_GROUP_CASE(IQ1_M)
+    default: break;
+  }
+#undef GSQ_QMV_GROUP_CASE
+}
+
+__global__ void __launch_bounds__(qmv_max_threads(qmv_weight(1, 3, false))) qmv_group_kernel(QmvArgs a0, QmvArgs a1,
+                                                                                             int g0) {
+  if ((int)blockIdx.x < g0) qmv_group_part(a0, (int)blockIdx.x);
+  else qmv_group_part(a1, (int)blockIdx.x - g0);
+}
+
+// y0 = x W0^T and y1 = x W1^T for one fp16 activation row in one launch, the CUs shared in
+// proportion to the two matrices' bytes. hipErrorNotSupported when the two plans do not fit this
+// kernel (the caller then launches the products one by one).
+hipError_t launch_qmv_group2(int qt0, const uint8_t* p0, int64_t N0, void* y0, const DevTables& tb0, int qt1,
+                             const uint8_t* p1, int64_t N1, void* y1, const DevTables& tb1, const void* x, int ydt,
+                             int K, int num_cus, hipStream_t s) {
+  if (qt0 == Q6_K || qt1 == Q6_K || num_cus < 2) return hipErrorNotSupported;
+  const int64_t rb0 = (int64_t)(K / 256) * block_bytes_of(qt0), rb1 = (int64_t)(K / 256) * block_bytes_of(qt1);
+  if (((reinterpret_cast<uintptr_t>(p0) | reinterpret_cast<uintptr_t>(p1)) & 3) || (rb0 & 3) || (rb1 & 3))
+    return hipErrorNotSupported;
+  const double b0 = (double)N0 * (double)rb0, b1 = (double)N1 * (double)rb1;
+  int c0 = (int)(num_cus * b0 / (b0 + b1) + 0.5);
+  c0 = c0 < 1 ? 1 : (c0 > num_cus - 1 ? num_cus - 1 : c0);
+  QmvPlan q0, q1;
+  hipError_t e = launch_qmv_rows(qt0, p0, x, DT_F16, y0, ydt, 1, 1, N0, K, tb0, c0, s, QmvPre(), &q0);
+  if (e != hipSuccess) return e;
+  e = launch_qmv_rows(qt1, p1, x, DT_F16, y1, ydt, 1, 1, N1, K, tb1, num_cus - c0, s, QmvPre(), &q1);
+  if (e != hipSuccess) return e;
+  if (q0.gl != 3 || q1.gl != 3 || !q0.a.pair || !q1.a.pair || q0.threads != q1.threads) return hipErrorNotSupported;
+  static bool attr_set = false;
+  if (!attr_set) {
+    e = hipFuncSetAttribute((const void*)qmv_group_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const size_t lds = q0.lds > q1.lds ? q0.lds : q1.lds;
+  hipLaunchKernelGGL(qmv_group_kernel, dim3(q0.grid + q1.grid), dim3(q0.threads), lds, s, q0.a, q1.a, q0.grid);
+  return hipGetLastError();
 }
 
 // Copy of `bytes` (a multiple of 16) from a 2-byte aligned src to a 16-byte aligned dst: the

@@ -29,6 +29,7 @@ EXPORTS = {
     "gsq_tables_ready": (_I32, [_I32]),
     "gsq_dequant": (_I32, [_I32, _VP, _I64, _VP, _VP]),
     "gsq_qmv": (_I32, [_I32, _VP, _VP, _I32, _VP, _I32, _I64, _I64, _I64, _VP]),
+    "gsq_qmv_group2": (_I32, [_I32, _VP, _I64, _VP, _I32, _VP, _I64, _VP, _VP, _I32, _I64, _VP]),
     "gsq_qmv_pre": (_I32, [_I32, _VP, _I32, _VP, _VP, _VP, _F32, _VP, _VP, _VP, _I32, _I64, _I64, _VP, _VP, _I64,
                            _I64, _VP, _VP]),
     "gsq_qmm": (_I32, [_I32, _VP, _VP, _I32, _VP, _I32, _I64, _I64, _I64, _VP]),

@@ -15,7 +15,7 @@ from __future__ import annotations
 import torch
 
 from ..runtime.kernels.qmm import QMM_MIN_ROWS, quantized_matmul
-from ..runtime.kernels.qmv import quantized_matvec, quantized_matvec_pre
+from ..runtime.kernels.qmv import quantized_matvec, quantized_matvec_group2, quantized_matvec_pre
 
 
 def _apply(x, packed, qtype, out_features, in_features):
@@ -110,9 +110,10 @@ class GSQFusedLinear(torch.nn.Module):
 class GSQGroupedLinear(torch.nn.Module):
     """Projections of one input whose weights differ in quantization type (q/k/v of a decoder
     layer: IQ2_XS, IQ2_XS, IQ4_XS), applied as one group: the weights of each type are fused
-    into one launch (``GSQFusedLinear``), so a group costs one launch per type. ``forward``
-    returns one output per weight, in the order given; each is the one ``GSQFusedLinear`` gives
-    for its type's weights. The launches stay on the current stream: as parallel branches of a
+    (``GSQFusedLinear``), and one fp16 row over two types goes out as one launch
+    (``quantized_matvec_group2``), else one launch per type. ``forward`` returns one output per
+    weight, in the order given, each within the QMV tolerance of the one ``GSQFusedLinear``
+    gives for its type's weights. The launches stay on the current stream: as parallel branches of a
     captured HIP graph (side streams forked from and joined into the current stream) the
     64-layer decode stack ran 16% slower than with the launches in sequence (4.91 against 4.24
     ms per token). No counterpart in the reference, whose model applies each projection on its
@@ -143,8 +144,17 @@ class GSQGroupedLinear(torch.nn.Module):
 
     def forward(self, x):
         outs = [None] * len(self.out_features)
-        for slot, part in zip(self.slots, self.parts):
-            for j, r in zip(slot, part(x)):
+        if len(self.parts) == 2 and x.numel() == self.in_features and x.dtype == torch.float16:
+            # one row, two types: both fused parts in one launch
+            p0, p1 = self.parts
+            y0, y1 = quantized_matvec_group2(x, p0.packed_weight, p1.packed_weight, qtypes=(p0.qtype, p1.qtype),
+                                             out_features=(p0.out_features, p1.out_features),
+                                             in_features=self.in_features)
+            results = (p0._outputs(y0), p1._outputs(y1))
+        else:
+            results = tuple(part(x) for part in self.parts)
+        for slot, res in zip(self.slots, results):
+            for j, r in zip(slot, res):
                 outs[j] = r
         return tuple(outs)
 

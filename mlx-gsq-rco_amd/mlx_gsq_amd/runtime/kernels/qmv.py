@@ -105,6 +105,38 @@ def quantized_matvec(x, packed, *, qtype: str, out_features: int, in_features: i
     return y.reshape(*original, out_features)
 
 
+def quantized_matvec_group2(x, packed0, packed1, *, qtypes, out_features, in_features: int, out_dtype=None):
+    """``(x @ W0.T, x @ W1.T)`` for one activation row ``x`` (``in_features`` values) and two
+    packed matrices of any two quantization types (``qtypes``, ``out_features``: one per
+    matrix) in one launch (``gsq_qmv_group2``). No counterpart in the reference, whose model
+    applies each projection on its own; validation and exceptions as ``quantized_matvec``.
+    Not one fp16 row: the two products through ``quantized_matvec``."""
+    (q0, q1), (n0, n1) = qtypes, out_features
+    _validate(x, packed0, q0, n0, in_features)
+    _validate(x, packed1, q1, n1, in_features)
+    if x.numel() != in_features or x.dtype != torch.float16:
+        return (quantized_matvec(x, packed0, qtype=q0, out_features=n0, in_features=in_features, out_dtype=out_dtype),
+                quantized_matvec(x, packed1, qtype=q1, out_features=n1, in_features=in_features, out_dtype=out_dtype))
+    for q in (q0, q1):
+        if q not in QTYPES:
+            raise KeyError(q)
+    _check_tensors(x, packed0)
+    _check_tensors(x, packed1)
+    odt = out_dtype or x.dtype
+    flat = x.reshape(in_features).contiguous()
+    packed0, packed1 = packed0.contiguous(), packed1.contiguous()
+    y0 = torch.empty(x.shape[:-1] + (n0,), dtype=odt, device=x.device)
+    y1 = torch.empty(x.shape[:-1] + (n1,), dtype=odt, device=x.device)
+    _lib.ensure_tables(q0, x.device)
+    _lib.ensure_tables(q1, x.device)
+    with torch.cuda.device(x.device):
+        _lib.check(_lib.lib().gsq_qmv_group2(TYPE_IDS[q0], packed0.data_ptr(), n0, y0.data_ptr(), TYPE_IDS[q1],
+                                             packed1.data_ptr(), n1, y1.data_ptr(), flat.data_ptr(),
+                                             _lib.DTYPE_CODES[odt], in_features, _lib.stream_handle(x.device)),
+                   "quantized_matvec_group2")
+    return y0, y1
+
+
 PRE_OPS = {"add_rms_norm": 1, "swiglu": 2}  # GSQ_PRE_ADD_RMSNORM, GSQ_PRE_SWIGLU
 
 

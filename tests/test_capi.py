@@ -90,6 +90,16 @@ def test_c_validation_errors_without_gpu():
     assert pre(cr=4, ydt=0) == _lib.GSQ_E_VALUE and b"fp16 y" in lib.gsq_last_error()
     assert pre(cr=4, co=None) == _lib.GSQ_E_VALUE
     assert pre(k=300) == _lib.GSQ_E_VALUE  # K % 256
+    # two products of one row in one launch: checked before anything reaches a device; the
+    # outputs must not overlap each other or x (workgroups still read x while others write)
+    def group2(y0, y1, x, qt1=23, ydt=0):
+        return lib.gsq_qmv_group2(17, 2 << 12, 4, y0, qt1, 4 << 12, 4, y1, x, ydt, 256, None)
+    assert group2(6 << 12, 6 << 12, 8 << 12) == _lib.GSQ_E_VALUE and b"must not overlap" in lib.gsq_last_error()
+    assert group2(6 << 12, (6 << 12) + 8, 8 << 12) == _lib.GSQ_E_VALUE  # 4 fp32 outputs: 16 bytes
+    assert group2(6 << 12, 7 << 12, (7 << 12) - 256) == _lib.GSQ_E_VALUE  # x (512 bytes) reaches y1
+    assert group2(6 << 12, 7 << 12, None) == _lib.GSQ_E_VALUE and b"NULL" in lib.gsq_last_error()
+    assert group2(6 << 12, 7 << 12, 8 << 12, qt1=99) == _lib.GSQ_E_UNSUPPORTED
+    assert group2(6 << 12, 7 << 12, 8 << 12, ydt=5) == _lib.GSQ_E_TYPE
     # the decode-step kernels
     assert lib.gsq_add_rms_norm(16, None, 32, 48, 1, 12, 1e-6, 1, None) == _lib.GSQ_E_VALUE  # dim % 8
     assert lib.gsq_add_rms_norm(16, None, 32, 48, 1, 16, 1e-6, 5, None) == _lib.GSQ_E_TYPE

@@ -1567,12 +1567,14 @@ hipError_t launch_qmv_group2(int qt0, const uint8_t* p0, int64_t N0, void* y0, c
   const double b0 = (double)N0 * (double)rb0, b1 = (double)N1 * (double)rb1;
   int c0 = (int)(num_cus * b0 / (b0 + b1) + 0.5);
   c0 = c0 < 1 ? 1 : (c0 > num_cus - 1 ? num_cus - 1 : c0);
+  // a share of few CUs for many rows can leave a plan without room (its row sums outgrow LDS):
+  // the products then go one by one, each on all CUs
   QmvPlan q0, q1;
-  hipError_t e = launch_qmv_rows(qt0, p0, x, DT_F16, y0, ydt, 1, 1, N0, K, tb0, c0, s, QmvPre(), &q0);
-  if (e != hipSuccess) return e;
-  e = launch_qmv_rows(qt1, p1, x, DT_F16, y1, ydt, 1, 1, N1, K, tb1, num_cus - c0, s, QmvPre(), &q1);
-  if (e != hipSuccess) return e;
+  if (launch_qmv_rows(qt0, p0, x, DT_F16, y0, ydt, 1, 1, N0, K, tb0, c0, s, QmvPre(), &q0) != hipSuccess ||
+      launch_qmv_rows(qt1, p1, x, DT_F16, y1, ydt, 1, 1, N1, K, tb1, num_cus - c0, s, QmvPre(), &q1) != hipSuccess)
+    return hipErrorNotSupported;
   if (q0.gl != 3 || q1.gl != 3 || !q0.a.pair || !q1.a.pair || q0.threads != q1.threads) return hipErrorNotSupported;
+  hipError_t e;
   static bool attr_set = false;
   if (!attr_set) {
     e = hipFuncSetAttribute((const void*)qmv_group_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);

@@ -75,7 +75,8 @@ int gsq_qmv(int qtype_id, const void* packed, const void* x, int x_dtype, void* 
 
 /* y0[1, N0] = x * W0^T and y1[1, N1] = x * W1^T for one fp16 activation row x[K] and two packed
  * matrices of any two types (q|k and v of an attention layer) in one launch, the CUs shared in
- * proportion to the matrices' bytes. No counterpart in the reference, whose model applies each
+ * proportion to the two products' expected times (bytes x a per-type measured time per byte).
+ * No counterpart in the reference, whose model applies each
  * projection on its own (mlx_gsq/models/qwen35.py); for GSQGroupedLinear. Results as two gsq_qmv
  * calls give them within the QMV tolerance (the v product may use another launch plan alone).
  * Products the shared kernel does not take (Q6_K, rows of other than 20 superblocks, matrices

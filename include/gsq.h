@@ -76,12 +76,12 @@ int gsq_qmv(int qtype_id, const void* packed, const void* x, int x_dtype, void* 
 /* y0[1, N0] = x * W0^T and y1[1, N1] = x * W1^T for one fp16 activation row x[K] and two packed
  * matrices of any two types (q|k and v of an attention layer) in one launch, the CUs shared in
  * proportion to the two products' expected times (bytes x a per-type measured time per byte).
- * No counterpart in the reference, whose model applies each
- * projection on its own (mlx_gsq/models/qwen35.py); for GSQGroupedLinear. Results as two gsq_qmv
- * calls give them within the QMV tolerance (the v product may use another launch plan alone).
- * Products the shared kernel does not take (Q6_K, rows of other than 20 superblocks, matrices
- * or rows not 4-byte aligned, x not 16-byte aligned) run as those two calls. y0, y1 and x must
- * not overlap (GSQ_E_VALUE). */
+ * No counterpart in the reference, whose model applies each projection on its own
+ * (mlx_gsq/models/qwen35.py); for GSQGroupedLinear. Results as two gsq_qmv calls give them,
+ * within the QMV tolerance (a product alone may run another launch plan). Products the shared
+ * kernel does not take (plans that do not decode items in pairs: Q6_K, IQ3_S at K = 5120, rows
+ * of other than 20 superblocks; matrices or rows not 4-byte aligned; x not 16-byte aligned) run
+ * as those two calls. y0, y1 and x must not overlap (GSQ_E_VALUE). */
 int gsq_qmv_group2(int qtype_id0, const void* packed0, int64_t N0, void* y0, int qtype_id1, const void* packed1,
                    int64_t N1, void* y1, const void* x, int y_dtype, int64_t K, void* stream);
 

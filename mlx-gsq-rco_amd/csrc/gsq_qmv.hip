@@ -718,10 +718,12 @@ __device__ __forceinline__ float wave_sum_to_lane63(float v) {
 
 // Register weight of a variant = activation rows x slices per wave, doubled for
 // split-precision (fp32/bf16) activations, which keep two fp16 parts per value. Workgroups
-// shrink as the weight grows so that no variant spills: weight <= 2: 16 waves, 3: 12 waves,
-// 4 and more: 8 waves (16 waves of weight 3 measured no faster than 12).
+// shrink as the weight grows so that no variant spills: weight <= 2: 16 waves, 3 to 6: 12 waves
+// (two rows of three slices fit 168 registers: 129-145 used, and 12 waves make the 17408-row
+// and 17408-wide two-row products 4-32% faster than 8), 7 and more: 8 waves (16 waves of
+// weight 3 measured no faster than 12).
 constexpr int qmv_weight(int mr, int gl, bool xs) { return mr * gl * (xs ? 2 : 1); }
-constexpr int qmv_max_threads(int w) { return w >= 4 ? 512 : (w == 3 ? 768 : 1024); }
+constexpr int qmv_max_threads(int w) { return w >= 7 ? 512 : (w >= 3 ? 768 : 1024); }
 constexpr int kMaxRing = 16;
 
 // fp16 x[e0] (low half) and x[e1] (high half) out of the 16 words holding x[0..31], by one
@@ -1467,6 +1469,15 @@ static hipError_t launch_qmv_rows(int qt, const uint8_t* packed, const void* x, 
   // row sums; the fused prologue also sums per wave there (16 floats)
   int red_bytes = (a.rows_per_wg * mr * a.W * 4 + 15) & ~15;
   if (has_pre && red_bytes < 64) red_bytes = 64;
+  // two rows with one wave per row and fewer than two items per wave slot: a ring under three
+  // items deep (even with the activations outside LDS) costs more than the extra waves gain, so
+  // 8 waves (IQ3_S and Q6_K on 5120 x 5120 are 10-21% slower with 12; the 17408-row and
+  // 17408-wide products 4-32% faster with 12 than with 8)
+  if (mr == 2 && a.W == 1 && nw > 8 && a.rows_per_wg < 2 * nw &&
+      (lds_cap - a.tbl_bytes - red_bytes) / (nw * a.sbuf) < 3) {
+    nw = 8;
+    a.slots = nw;
+  }
   // activations go to LDS only if the ring keeps at least 3 items per wave (always with a
   // fused prologue, which forms them there)
   a.x_lds = (has_pre || (g_qmv_tuning.x_lds && a.tbl_bytes + a.x_bytes + red_bytes + nw * 3 * a.sbuf <= lds_cap))

@@ -42,24 +42,20 @@ def _check_tensors(x, packed):
 
 
 # gfx950 routing beyond the reference's row threshold: from 5 fp16 rows on (3 for matrices of
-# at least 2^24 weights, 2 when such a matrix is also at least 16384 wide) gsq_qmm's small-batch
-# kernel, which decodes the weights once for all rows, is faster than the vector kernel, whose
-# dot-product work grows with the rows (measured on the 27B projections: 5120 x 17408 Q4_K at
-# 2 rows 23 us against 24 us; 17408 x 5120 IQ2_S at 2 rows 20 us on the vector kernel against
-# 25 us; 1024 x 5120 at 4 rows 6 us on the vector kernel against 7.5 us).
+# at least 2^26 weights) gsq_qmm's small-batch kernel, which decodes the weights once for all
+# rows, is faster than the vector kernel, whose dot-product work grows with the rows (measured on
+# the 27B projections: at 2 rows the vector kernel takes 17-19 us on the 17408 x 5120 and
+# 5120 x 17408 products against 23-25 us; at 3-4 rows 29-34 us against 23-25; on 5120 x 5120 at
+# 4 rows 11 us against 12, on 1024 x 5120 6 us against 8).
 SMALL_BATCH_MIN_ROWS = 5
 SMALL_BATCH_LARGE_MIN_ROWS = 3
-SMALL_BATCH_LARGE_WEIGHTS = 1 << 24
-SMALL_BATCH_WIDE_MIN_ROWS = 2
-SMALL_BATCH_WIDE_K = 16384
+SMALL_BATCH_LARGE_WEIGHTS = 1 << 26
 
 
 def _small_batch_faster(rows, dtype, out_features, in_features):
     if dtype != torch.float16:
         return False
     if out_features * in_features >= SMALL_BATCH_LARGE_WEIGHTS:
-        if in_features >= SMALL_BATCH_WIDE_K:
-            return rows >= SMALL_BATCH_WIDE_MIN_ROWS
         return rows >= SMALL_BATCH_LARGE_MIN_ROWS
     return rows >= SMALL_BATCH_MIN_ROWS
 

@@ -117,8 +117,8 @@ def test_qmv_27b_row_widths(qtype, shape):
 @pytest.mark.parametrize("qtype", ["Q4_K", "IQ2_S", "IQ3_XXS"])
 @pytest.mark.parametrize("rows", [4, 7])
 def test_qmv_wide_rows_multi_row(qtype, rows, vector_kernel_only):
-    """4..7 activation rows of the 17408-wide down projection: more waves per row than the
-    4-row variant holds, so the rows go out in 2-row launches."""
+    """4..7 activation rows of the 17408-wide down projection: nine waves per row (one row
+    slot of the 4-row variant), the rows past 4 in a second launch."""
     from mlx_gsq_amd.runtime.kernels.qmv import quantized_matvec
     N, K = 160, 17408
     packed = synth.make_packed(qtype, N, K, seed=12)
@@ -314,16 +314,15 @@ def test_qmm_fp16_output_and_fp32_input(qtype):
     assert rel_l2(y32, want) <= 1e-3
 
 
-@pytest.mark.parametrize("rows,n,K", [(5, 300, 4096), (4, 300, 4096), (3, 4096, 4096), (2, 4096, 4096),
-                                      (2, 1024, 16384)])
+@pytest.mark.parametrize("rows,n,K", [(5, 300, 4096), (4, 300, 4096), (3, 4096, 4096), (3, 16384, 4096),
+                                      (2, 4096, 16384), (4, 5120, 5120)])
 def test_matvec_routes_small_fp16_batches(rows, n, K):
-    """fp16 batches of 5+ rows (3+ on matrices of 2^24+ weights, 2+ when such a matrix is also
-    16384+ wide) take the small-batch QMM kernel (fp16-rounded weights, QMM tolerance); the
-    others stay on the vector kernel."""
+    """fp16 batches of 5+ rows (3+ on matrices of 2^26+ weights) take the small-batch QMM kernel
+    (fp16-rounded weights, QMM tolerance); the others stay on the vector kernel."""
     from mlx_gsq_amd.runtime.kernels import qmv
     routed = qmv._small_batch_faster(rows, torch.float16, n, K)
-    big = n * K >= 1 << 24
-    assert routed == (rows >= 5 or (big and rows >= 3) or (big and K >= 16384 and rows >= 2))
+    big = n * K >= 1 << 26
+    assert routed == (rows >= 5 or (big and rows >= 3))
     packed = synth.make_packed("Q4_K", n, K, seed=8)
     x = synth.make_x(rows, K, seed=8, dtype=np.float16)
     y = qmv.quantized_matvec(dev(x), dev(packed), qtype="Q4_K", out_features=n, in_features=K,

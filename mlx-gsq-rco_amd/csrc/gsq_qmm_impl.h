@@ -19,12 +19,14 @@
 //    (octet o of row m at position o ^ ((m >> 2) & 3)) so that the ds_read_b128 A-operand
 //    reads of a wave are free of bank conflicts.
 //  * all DMA waits are exact s_waitcnt vmcnt counts derived from the fixed issue order; one
-//    s_barrier per K32 stage guards the shared activation ring.
+//    s_barrier per K32 stage (per pair of stages on rings of four or more stages) guards the
+//    shared activation ring.
 //  * stream-K work split: the (tile, K column) iterations are divided evenly over as many
 //    workgroups as there are CUs, so shapes whose tile count is not a multiple of the CU count
 //    (17408 = 17 * 1024 rows) still fill the chip. A tile split between workgroups is
 //    finished by the last one to arrive (per-tile arrival counter), which sums the fp32
-//    partials in a fixed order (deterministic) and writes y.
+//    partials in a fixed order (deterministic) and writes y; the workgroup holding a tile's
+//    first columns keeps its own piece in registers when it finds the others already in.
 //  * tiles are numbered weight tile fastest and workgroups renumbered so that consecutive work
 //    (one activation tile, neighbouring weight tiles and K ranges) lands on one XCD and shares
 //    its L2.
@@ -561,7 +563,63 @@ __global__ void __launch_bounds__(64 * WV, 1) qmm_mfma_kernel(QmmMfmaArgs args) 
     // after the workgroup's last stage the rings hold nothing that is still needed: fp32 rows
     // of the tile are then written whole through a per-wave LDS transpose
     const bool end_lds = yrows && q1 == Q;
-    if (wf == wl) {
+    // direct: this workgroup's accumulators hold the whole tile (its only piece, or the other
+    // pieces' partials added in place below)
+    constexpr int CH = 8;  // output blocks per batch of partial loads
+    bool direct = wf == wl;
+    bool last = false;
+    if (!direct) {
+      // slot 2w: the tile this workgroup starts in; slot 2w + 1: the tile it ends in
+      const int slot = 2 * w + (q0 == 0 ? 0 : 1);
+      // the workgroup holding the tile's first columns (its range's last work, so often the
+      // last to arrive) looks at the arrival count first: if every other piece is in, it stores
+      // no partial and adds the others' partials to its accumulators in place, in workgroup
+      // order from +0, the same sums as the memory path below (it also takes this path when
+      // its own increment shows it last)
+      const bool own = w == wf;
+      if (tid == 0) bc[0] = own ? __hip_atomic_load(&cnt[wf], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -1;
+      __syncthreads();
+      last = bc[0] == wl - wf;
+      if (!last) {
+        const __amdgpu_buffer_rsrc_t ps = qmm_slot_rsrc(part, slot, slot_floats);
+        // every store has completed (device-coherent) before the arrival count is incremented;
+        // 16-row blocks wholly past M (padding rows of the last activation tile) are not stored
+#pragma unroll
+        for (int i = 0; i < MF; ++i)
+          if (m0 + 16 * i < M) {
+#pragma unroll
+            for (int j = 0; j < NB; ++j) qmm_st_coherent(ps, ((i * NB + j) * TH + tid) * 16, acc[i][j]);
+          }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (tid == 0) bc[1] = __hip_atomic_fetch_add(&cnt[wf], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        last = bc[1] == wl - wf;
+      }
+      if (last && own) {
+#pragma unroll
+        for (int i = 0; i < MF; ++i)
+#pragma unroll
+          for (int j = 0; j < NB; ++j) acc[i][j] = (float4_t){0.f, 0.f, 0.f, 0.f} + acc[i][j];
+        for (int v = wf + 1; v <= wl; ++v) {
+          const int vs = 2 * v + (tile == qmm_first_col(v, units, G) / nblk ? 0 : 1);
+          const __amdgpu_buffer_rsrc_t pv = qmm_slot_rsrc(part, vs, slot_floats);
+#pragma unroll
+          for (int ij0 = 0; ij0 < MF * NB; ij0 += CH) {
+            if (m0 + 16 * (ij0 / NB) < M) {
+              float4_t ld[CH];
+#pragma unroll
+              for (int t = 0; t < CH; ++t) ld[t] = qmm_ld_coherent(pv, ((ij0 + t) * TH + tid) * 16);
+#pragma unroll
+              for (int t = 0; t < CH; ++t) acc[(ij0 + t) / NB][(ij0 + t) % NB] += ld[t];
+            }
+          }
+        }
+        if (tid == 0) __hip_atomic_store(&cnt[wf], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        direct = true;
+      }
+    }
+    if (direct) {
       if (end_lds) {
         __syncthreads();  // every wave is done with the rings
 #pragma unroll
@@ -571,25 +629,8 @@ __global__ void __launch_bounds__(64 * WV, 1) qmm_mfma_kernel(QmmMfmaArgs args) 
         qmm_store_tile<MF, NB>(yg, ydt, M, N, acc, m0, n0, lane);
       }
     } else {
-      // slot 2w: the tile this workgroup starts in; slot 2w + 1: the tile it ends in
-      const int slot = 2 * w + (q0 == 0 ? 0 : 1);
-      const __amdgpu_buffer_rsrc_t ps = qmm_slot_rsrc(part, slot, slot_floats);
-      // every store has completed (device-coherent) before the arrival count is incremented;
-      // 16-row blocks wholly past M (padding rows of the last activation tile) are not stored
-#pragma unroll
-      for (int i = 0; i < MF; ++i)
-        if (m0 + 16 * i < M) {
-#pragma unroll
-          for (int j = 0; j < NB; ++j) qmm_st_coherent(ps, ((i * NB + j) * TH + tid) * 16, acc[i][j]);
-        }
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();
-      if (tid == 0) bc[0] = __hip_atomic_fetch_add(&cnt[wf], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __syncthreads();
-      const int arrived = bc[0];
-      if (arrived == wl - wf) {  // last to arrive: sum the partials in workgroup order
+      if (last) {  // sum the partials in workgroup order
         const int mb = m0 + 4 * (lane >> 4), nb = n0 + (lane & 15);
-        constexpr int CH = 8;  // output blocks per batch of loads
 #pragma unroll 1
         for (int ij0 = 0; ij0 < MF * NB; ij0 += CH) {
           // batches that start past M hold only padding rows, whose partials were not stored

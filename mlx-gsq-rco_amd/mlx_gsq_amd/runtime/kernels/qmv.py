@@ -41,22 +41,18 @@ def _check_tensors(x, packed):
         raise ValueError("x and packed must be on the same GPU device")
 
 
-# gfx950 routing beyond the reference's row threshold: from 5 fp16 rows on (3 for matrices of
-# at least 2^26 weights) gsq_qmm's small-batch kernel, which decodes the weights once for all
-# rows, is faster than the vector kernel, whose dot-product work grows with the rows (measured on
-# the 27B projections: at 2 rows the vector kernel takes 17-19 us on the 17408 x 5120 and
-# 5120 x 17408 products against 23-25 us; at 3-4 rows 29-34 us against 23-25; on 5120 x 5120 at
-# 4 rows 11 us against 12, on 1024 x 5120 6 us against 8).
-SMALL_BATCH_MIN_ROWS = 5
-SMALL_BATCH_LARGE_MIN_ROWS = 3
-SMALL_BATCH_LARGE_WEIGHTS = 1 << 26
+# Rows below the reference's QMM threshold stay on gsq_qmv, whose quad-row kernel (3-8 fp16 rows)
+# is faster than gsq_qmm's small-batch kernel up to 7 rows and as fast at 8 (measured on the 27B
+# layer, 7 projections: gsq_qmv 80 / 84 / 88 / 107 / 111 / 118 us at 2 / 3 / 4 / 5 / 6 / 8 rows
+# against 118 for the small-batch kernel at every row count), so no batch below the reference's
+# threshold is sent to QMM for speed; the threshold below is that of the reference.
+SMALL_BATCH_MIN_ROWS = QMM_MIN_ROWS
 
 
 def _small_batch_faster(rows, dtype, out_features, in_features):
+    del out_features, in_features  # the crossover was the same on every 27B projection shape
     if dtype != torch.float16:
         return False
-    if out_features * in_features >= SMALL_BATCH_LARGE_WEIGHTS:
-        return rows >= SMALL_BATCH_LARGE_MIN_ROWS
     return rows >= SMALL_BATCH_MIN_ROWS
 
 

@@ -31,9 +31,9 @@ def _codebooks():
 
 @pytest.fixture
 def vector_kernel_only(monkeypatch):
-    """Keep quantized_matvec on the vector kernel for every row count below the reference's QMM
-    threshold (it otherwise sends fp16 batches of 3+ rows to the small-batch QMM kernel), so
-    the vector kernel's multi-row variants stay covered at their own tolerance."""
+    """Keep quantized_matvec on gsq_qmv for every row count below the reference's QMM threshold
+    (it otherwise sends fp16 batches of 5+ rows to the small-batch QMM kernel), so gsq_qmv's
+    multi-row kernels (vector for 2 rows, quad-row for 3-7) stay covered at their own tolerance."""
     from mlx_gsq_amd.runtime.kernels import qmv
     monkeypatch.setattr(qmv, "_small_batch_faster", lambda *a: False)
 
@@ -117,8 +117,8 @@ def test_qmv_27b_row_widths(qtype, shape):
 @pytest.mark.parametrize("qtype", ["Q4_K", "IQ2_S", "IQ3_XXS"])
 @pytest.mark.parametrize("rows", [4, 7])
 def test_qmv_wide_rows_multi_row(qtype, rows, vector_kernel_only):
-    """4..7 activation rows of the 17408-wide down projection: nine waves per row (one row
-    slot of the 4-row variant), the rows past 4 in a second launch."""
+    """4 and 7 activation rows of 17408-wide rows: the quad-row kernel (twelve waves of three
+    quad slices per row quad; one or two activation quads)."""
     from mlx_gsq_amd.runtime.kernels.qmv import quantized_matvec
     N, K = 160, 17408
     packed = synth.make_packed(qtype, N, K, seed=12)
@@ -314,15 +314,14 @@ def test_qmm_fp16_output_and_fp32_input(qtype):
     assert rel_l2(y32, want) <= 1e-3
 
 
-@pytest.mark.parametrize("rows,n,K", [(5, 300, 4096), (4, 300, 4096), (3, 4096, 4096), (3, 16384, 4096),
-                                      (2, 4096, 16384), (4, 5120, 5120)])
+@pytest.mark.parametrize("rows,n,K", [(5, 300, 4096), (4, 300, 4096), (3, 4096, 4096), (7, 16384, 4096),
+                                      (2, 4096, 16384), (8, 5120, 5120)])
 def test_matvec_routes_small_fp16_batches(rows, n, K):
-    """fp16 batches of 5+ rows (3+ on matrices of 2^26+ weights) take the small-batch QMM kernel
-    (fp16-rounded weights, QMM tolerance); the others stay on the vector kernel."""
+    """fp16 batches below the reference's 8 rows stay on gsq_qmv (3-7 rows: the quad-row kernel);
+    8 rows take QMM (fp16-rounded weights, QMM tolerance)."""
     from mlx_gsq_amd.runtime.kernels import qmv
-    routed = qmv._small_batch_faster(rows, torch.float16, n, K)
-    big = n * K >= 1 << 26
-    assert routed == (rows >= 5 or (big and rows >= 3))
+    routed = qmv.routes_to_qmm(rows, torch.float16, n, K)
+    assert routed == (rows >= 8)
     packed = synth.make_packed("Q4_K", n, K, seed=8)
     x = synth.make_x(rows, K, seed=8, dtype=np.float16)
     y = qmv.quantized_matvec(dev(x), dev(packed), qtype="Q4_K", out_features=n, in_features=K,

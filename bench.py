@@ -35,7 +35,8 @@ Printed JSON line (one, on stdout):
 Algorithmic bytes per QMV launch = N*(K/256)*block_bytes + M*K*2 (x fp16) + M*N*4 (y fp32).
 
 Extra modes for counter collection (rocprofv3 --pmc runs):
-  --profile-case Q6_K:17408x5120   only launches of that product (rotating 8 weight copies)
+  --profile-case Q6_K:17408x5120   only launches of that product (rotating 8 weight copies);
+                                   TYPE:NxK:M for M activation rows
   --copy-bytes N                   only a plain device-to-device copy of N bytes
   --qmm-profile-case IQ3_S:512x17408x5120   only launches of that QMM product
   --model-decode                   only the model_decode leg (for kernel traces of the step)
@@ -717,10 +718,11 @@ def qmm_profile_case(spec, reps, device):
     print(json.dumps({"qmm_profile_case": spec, "reps": reps, "flop_per_launch": 2 * m * n * k}), flush=True)
 
 
-def case_loop(q, n, k, reps, device, warmup=8, repeats=1):
-    """`repeats` timed loops of `reps` back-to-back launches of one (type, shape) product over 8
-    rotating weight copies on the current stream, after `warmup` untimed ones; returns the median
-    over the loops of the mean time per launch (us), each from a HIP event pair on that stream."""
+def case_loop(q, n, k, reps, device, warmup=8, repeats=1, m=1):
+    """`repeats` timed loops of `reps` back-to-back launches of one (type, shape) product with `m`
+    activation rows over 8 rotating weight copies on the current stream, after `warmup` untimed
+    ones; returns the median over the loops of the mean time per launch (us), each from a HIP
+    event pair on that stream."""
     import torch
     from mlx_gsq_amd import _lib, tables
     from mlx_gsq_amd.formats import TYPE_IDS
@@ -728,13 +730,13 @@ def case_loop(q, n, k, reps, device, warmup=8, repeats=1):
     _lib.ensure_tables(q, device)
     lib = _lib.lib()
     copies = [make_device_packed(q, n, k, seed=500 + i, device=device) for i in range(8)]
-    x = torch.randn(1, k, device=device).half()
-    y = torch.empty(1, n, device=device, dtype=torch.float32)
+    x = torch.randn(m, k, device=device).half()
+    y = torch.empty(m, n, device=device, dtype=torch.float32)
     stream = torch.cuda.current_stream(device)
     sh = stream.cuda_stream
 
     def launch(i):
-        rc = lib.gsq_qmv(TYPE_IDS[q], copies[i % 8].data_ptr(), x.data_ptr(), 1, y.data_ptr(), 0, 1, n, k, sh)
+        rc = lib.gsq_qmv(TYPE_IDS[q], copies[i % 8].data_ptr(), x.data_ptr(), 1, y.data_ptr(), 0, m, n, k, sh)
         if rc:
             raise RuntimeError(lib.gsq_last_error().decode())
 
@@ -795,12 +797,14 @@ def case_graph(q, n, k, reps, device, repeats=3):
 
 
 def profile_case(spec, reps, device):
-    """Only one (type, shape) product: the loop the roofline figure is timed with."""
-    q, shape = spec.split(":")
+    """Only one (type, shape) product, TYPE:NxK (one activation row) or TYPE:NxK:M (M rows
+    through gsq_qmv): the loop the roofline figure is timed with."""
+    q, shape, *rows = spec.split(":")
     n, k = (int(v) for v in shape.split("x"))
-    us = case_loop(q, n, k, reps, device, repeats=ROOF_REPEATS)
+    m = int(rows[0]) if rows else 1
+    us = case_loop(q, n, k, reps, device, repeats=ROOF_REPEATS, m=m)
     print(json.dumps({"profile_case": spec, "reps": reps, "repeats": ROOF_REPEATS, "warmup": 8,
-                      "bytes_per_launch": qmv_bytes(q, n, k),
+                      "bytes_per_launch": qmv_bytes(q, n, k, m),
                       "us_per_launch": round(us, 3)}), flush=True)
 
 

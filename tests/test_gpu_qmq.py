@@ -88,6 +88,17 @@ def test_qmq_27b_widths(qtype, shape):
     assert rel_l2(y, want) <= 1e-4, rel_l2(y, want)
 
 
+@pytest.mark.parametrize("shape", [(3, 1, 256), (4, 2, 512), (5, 3, 256), (8, 7, 1280), (3, 5, 4352)])
+@pytest.mark.parametrize("qtype", ["IQ3_XXS", "Q6_K", "IQ1_M"])
+def test_qmq_tiny_shapes(qtype, shape):
+    """1-7 weight rows (a single, partial quad: rows past N read the last row and are dropped),
+    one superblock (a half-filled slice), 17 superblocks (an odd count on several waves)."""
+    m, n, k = shape
+    y, want = check(qtype, m, n, k, seed=81)
+    assert rel_l2(y, want) <= 1e-4, rel_l2(y, want)
+    np.testing.assert_allclose(y, want, rtol=3e-5, atol=5e-4)
+
+
 @pytest.mark.parametrize("qtype", ["Q4_K", "IQ4_XS", "Q2_K", "IQ2_XXS"])
 def test_qmq_unaligned_packed_view(qtype):
     """A packed view 2 bytes past a 16-byte boundary: rows and superblocks not 4-byte aligned."""

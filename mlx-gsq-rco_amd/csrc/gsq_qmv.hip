@@ -1,4 +1,7 @@
-// Fused dequant + matrix-vector product (QMV) for M <= 4 activation rows.
+// Fused dequant + matrix-vector product (QMV): the vector kernel for up to 4 activation rows per
+// launch (gsq_qmv sends batches of 3-8 fp16 rows to the quad-row kernel in gsq_qmq.hip instead),
+// the per-type table images, the fused activation prologue and the two-product launch. The
+// per-type decoders are in gsq_qmv_decode.h.
 //
 // Counterpart of the reference's per-type packed-dot kernels
 // (mlx_gsq/runtime/kernels/qmv.py:76-528, dispatched by quantized_matvec qmv.py:537-576).

@@ -33,6 +33,7 @@
 // fp32 / bf16 activations use the generic kernel below.
 #pragma once
 #include <type_traits>
+#include <utility>
 
 #include "gsq_decode.h"
 #include "gsq_qmm_decode.h"
@@ -246,11 +247,24 @@ __device__ __forceinline__ int qmm_first_col(int w, int units, int G) {
   return (int)((long long)w * units / G);
 }
 
+// A loop over 0 .. N - 1 unrolled at compile time (each index a constant): code over the
+// accumulator arrays whose unrolled size exceeds the loop unroller's limits (MF x NB = 64 float4
+// with 4 waves) would otherwise index them at run time, which moves the whole array to scratch
+// memory (a scratch load and store around every MFMA).
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 template <int MF, int NB>
 __device__ __forceinline__ void qmm_store_tile(void* y, int ydt, int M, int N, const float4_t (&acc)[MF][NB], int m0,
                                                int n0, int lane) {
-#pragma unroll
-  for (int i = 0; i < MF; ++i)
+  static_for<MF>([&](auto ic) {
+    constexpr int i = decltype(ic)::value;
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       const int n = n0 + 16 * j + (lane & 15);
@@ -260,6 +274,7 @@ __device__ __forceinline__ void qmm_store_tile(void* y, int ydt, int M, int N, c
         if (m < M && n < N) qmm_store_y(y, ydt, (int64_t)m * N + n, acc[i][j][e]);
       }
     }
+  });
 }
 
 // One 16-row block of a wave's output (v[j][e]: row m + 4 (lane / 16) + e, column
@@ -622,9 +637,10 @@ __global__ void __launch_bounds__(64 * WV, 1) qmm_mfma_kernel(QmmMfmaArgs args) 
     if (direct) {
       if (end_lds) {
         __syncthreads();  // every wave is done with the rings
-#pragma unroll
-        for (int i = 0; i < MF; ++i)
+        static_for<MF>([&](auto ic) {
+          constexpr int i = decltype(ic)::value;
           if (m0 + 16 * i < M) qmm_store_rows_f32<NB>(static_cast<float*>(yg), M, N, acc[i], m0 + 16 * i, n0, lane, st);
+        });
       } else {
         qmm_store_tile<MF, NB>(yg, ydt, M, N, acc, m0, n0, lane);
       }

@@ -848,7 +848,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this path has no multi-GPU mode "
-              "(QMV/QMM would shard along N with no exchange; see DESIGN.md)", file=sys.stderr)
+              "(QMV/QMM would shard along N: a GPU's rows are one contiguous byte range of the packed matrix)", file=sys.stderr)
         sys.exit(2)
     # the CPU baseline runs first, in fresh worker processes, before anything touches the GPU
     cpu = None if (args.no_cpu or args.copy_bytes or args.profile_case or args.qmm_profile_case

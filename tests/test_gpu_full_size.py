@@ -1,4 +1,4 @@
-"""GPU parity at the BASELINE workload sizes (configs[0]-[3]), checked on sampled output columns.
+"""GPU parity at the benchmark workload sizes (configs[0]-[3]), checked on sampled output columns.
 
 Every product runs on the device at its full size; the oracle (dequant + float32 matmul,
 reference tests/test_all_qmv.py:22, test_all_qmm.py:41-57) then recomputes a seeded sample of

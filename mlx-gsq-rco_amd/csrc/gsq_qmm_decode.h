@@ -502,4 +502,201 @@ struct QmsRaw<IQ1_M, A4> {
   }
 };
 
+// ---- whole-group fragments for the small-batch kernel's group layout --------------------------
+// QmsGroup<T>::run gives the four fragments (octets kq = 0..3) of group g: for the codebook
+// types the signed codebook values times the group's or 16-weight sub-scale in fp16, (2 s + 1) x
+// value or (0.5 + s) x value, exact in fp16 for the published value sets (at most 11 significant
+// bits), and returns the superblock's float scale d (times a power of two): all groups of a
+// superblock share it, so one MFMA may take four groups' fragments and the scale goes onto the
+// sum. The group's field words are read first, then every codebook and sign-mask read of its 32
+// weights, then the arithmetic, so that the reads are in flight together.
+template <int T, bool A4>
+struct QmsGroup {
+  static constexpr bool kOn = false;
+};
+
+template <bool A4>
+struct QmsGroup<IQ2_S, A4> {
+  static constexpr bool kOn = true;
+  static constexpr uint32_t kGridB = 1024 * 8 * 2;
+  __device__ __forceinline__ static float run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g,
+                                              uint32_t (&o)[4][4]) {
+    const uint32_t qs4 = lds_w32<A4>(sb, sd + 2 + 4 * g);
+    const uint32_t sg4 = lds_w32<A4>(sb, sd + 34 + 4 * g);
+    const uint32_t qh = lds_u8(sb, sd + 66 + g);
+    const uint32_t scb = lds_u8(sb, sd + 74 + g);
+    uint4 e[4];
+    uint2 m0[4], m1[4];
+#pragma unroll
+    for (int kq = 0; kq < 4; ++kq) {
+      const uint32_t qi = bfe(qs4, 8 * kq, 8) | (bfe(qh, 2 * kq, 2) << 8);
+      const uint32_t s = bfe(sg4, 8 * kq, 8);
+      e[kq] = *reinterpret_cast<const uint4*>(tbl + qi * 16);
+      m0[kq] = *reinterpret_cast<const uint2*>(tbl + kGridB + (s & 15u) * 8);
+      m1[kq] = *reinterpret_cast<const uint2*>(tbl + kGridB + (s >> 4) * 8);
+    }
+    const _Float16 f0 = (_Float16)(0.5f + (float)(scb & 15u)), f1 = (_Float16)(0.5f + (float)(scb >> 4));
+#pragma unroll
+    for (int kq = 0; kq < 4; ++kq) {
+      const _Float16 f = kq < 2 ? f0 : f1;
+      o[kq][0] = pk_mul_h(e[kq].x, f) ^ m0[kq].x;
+      o[kq][1] = pk_mul_h(e[kq].y, f) ^ m0[kq].y;
+      o[kq][2] = pk_mul_h(e[kq].z, f) ^ m1[kq].x;
+      o[kq][3] = pk_mul_h(e[kq].w, f) ^ m1[kq].y;
+    }
+    return h2f(lds_u16(sb, sd)) * 0.25f;
+  }
+};
+
+template <bool A4>
+struct QmsGroup<IQ2_XS, A4> {
+  static constexpr bool kOn = true;
+  static constexpr uint32_t kGridB = 512 * 8 * 2;
+  __device__ __forceinline__ static float run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g,
+                                              uint32_t (&o)[4][4]) {
+    uint32_t qw[2];
+    lds_words<2, A4>(sb, sd + 2 + 8 * g, qw);
+    const uint32_t scb = lds_u8(sb, sd + 66 + g);
+    uint4 e[4], m[4];
+#pragma unroll
+    for (int kq = 0; kq < 4; ++kq) {
+      const uint32_t q = bfe(qw[kq >> 1], 16 * (kq & 1), 16);
+      e[kq] = *reinterpret_cast<const uint4*>(tbl + (q & 511u) * 16);
+      m[kq] = *reinterpret_cast<const uint4*>(tbl + kGridB + 16 * 8 + (q >> 9) * 16);
+    }
+    const _Float16 f0 = (_Float16)(0.5f + (float)(scb & 15u)), f1 = (_Float16)(0.5f + (float)(scb >> 4));
+#pragma unroll
+    for (int kq = 0; kq < 4; ++kq) {
+      const _Float16 f = kq < 2 ? f0 : f1;
+      o[kq][0] = pk_mul_h(e[kq].x, f) ^ m[kq].x;
+      o[kq][1] = pk_mul_h(e[kq].y, f) ^ m[kq].y;
+      o[kq][2] = pk_mul_h(e[kq].z, f) ^ m[kq].z;
+      o[kq][3] = pk_mul_h(e[kq].w, f) ^ m[kq].w;
+    }
+    return h2f(lds_u16(sb, sd)) * 0.25f;
+  }
+};
+
+template <bool A4>
+struct QmsGroup<IQ2_XXS, A4> {
+  static constexpr bool kOn = true;
+  static constexpr uint32_t kGridB = 256 * 8 * 2;
+  __device__ __forceinline__ static float run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g,
+                                              uint32_t (&o)[4][4]) {
+    uint32_t w[2];  // four codebook indices, then four 7-bit sign indices and the 4-bit scale
+    lds_words<2, A4>(sb, sd + 2 + 8 * g, w);
+    uint4 e[4], m[4];
+#pragma unroll
+    for (int kq = 0; kq < 4; ++kq) {
+      e[kq] = *reinterpret_cast<const uint4*>(tbl + bfe(w[0], 8 * kq, 8) * 16);
+      m[kq] = *reinterpret_cast<const uint4*>(tbl + kGridB + 16 * 8 + bfe(w[1], 7 * kq, 7) * 16);
+    }
+    const _Float16 f = (_Float16)(float)(2u * (w[1] >> 28) + 1u);  // (0.5 + s) / 4 = (2 s + 1) / 8
+#pragma unroll
+    for (int kq = 0; kq < 4; ++kq) {
+      o[kq][0] = pk_mul_h(e[kq].x, f) ^ m[kq].x;
+      o[kq][1] = pk_mul_h(e[kq].y, f) ^ m[kq].y;
+      o[kq][2] = pk_mul_h(e[kq].z, f) ^ m[kq].z;
+      o[kq][3] = pk_mul_h(e[kq].w, f) ^ m[kq].w;
+    }
+    return h2f(lds_u16(sb, sd)) * 0.125f;
+  }
+};
+
+template <bool A4>
+struct QmsGroup<IQ3_XXS, A4> {
+  static constexpr bool kOn = true;
+  static constexpr uint32_t kGridB = 256 * 4 * 2;
+  __device__ __forceinline__ static float run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g,
+                                              uint32_t (&o)[4][4]) {
+    uint32_t qw[2];  // eight codebook indices (one per 4 weights)
+    lds_words<2, A4>(sb, sd + 2 + 8 * g, qw);
+    const uint32_t u = lds_w32<A4>(sb, sd + 66 + 4 * g);
+    uint2 e[8];
+    uint32_t m[4][4];
+#pragma unroll
+    for (int kq = 0; kq < 4; ++kq) {
+      e[2 * kq] = *reinterpret_cast<const uint2*>(tbl + bfe(qw[kq >> 1], 16 * (kq & 1), 8) * 8);
+      e[2 * kq + 1] = *reinterpret_cast<const uint2*>(tbl + bfe(qw[kq >> 1], 16 * (kq & 1) + 8, 8) * 8);
+      ksigns_masks(tbl, kGridB, (u >> (7 * kq)) & 127u, m[kq]);
+    }
+    const _Float16 f = (_Float16)(float)(2u * (u >> 28) + 1u);  // (0.5 + s) / 2 = (2 s + 1) / 4
+#pragma unroll
+    for (int kq = 0; kq < 4; ++kq) {
+      o[kq][0] = pk_mul_h(e[2 * kq].x, f) ^ m[kq][0];
+      o[kq][1] = pk_mul_h(e[2 * kq].y, f) ^ m[kq][1];
+      o[kq][2] = pk_mul_h(e[2 * kq + 1].x, f) ^ m[kq][2];
+      o[kq][3] = pk_mul_h(e[2 * kq + 1].y, f) ^ m[kq][3];
+    }
+    return h2f(lds_u16(sb, sd)) * 0.25f;
+  }
+};
+
+template <bool A4>
+struct QmsGroup<IQ3_S, A4> {
+  static constexpr bool kOn = true;
+  static constexpr uint32_t kMaskB = 512 * 4 * 2;
+  __device__ __forceinline__ static float run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g,
+                                              uint32_t (&o)[4][4]) {
+    uint32_t qw[2];  // eight low index bytes (one per 4 weights)
+    lds_words<2, A4>(sb, sd + 2 + 8 * g, qw);
+    const uint32_t qh = lds_u8(sb, sd + 66 + g);
+    const uint32_t sg4 = lds_w32<A4>(sb, sd + 74 + 4 * g);
+    const uint32_t scb = lds_u8(sb, sd + 106 + (g >> 1));
+    uint2 e[8], m[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {  // codebook entry i: weights 4 i .. 4 i + 3, sign nibble i
+      const uint32_t qi = bfe(qw[i >> 2], 8 * (i & 3), 8) | (bfe(qh, i, 1) << 8);
+      e[i] = *reinterpret_cast<const uint2*>(tbl + qi * 8);
+      m[i] = *reinterpret_cast<const uint2*>(tbl + kMaskB + bfe(sg4, 4 * i, 4) * 8);
+    }
+    const _Float16 f = (_Float16)(float)(1u + 2u * ((scb >> (4 * (g & 1))) & 15u));
+#pragma unroll
+    for (int kq = 0; kq < 4; ++kq) {
+      o[kq][0] = pk_mul_h(e[2 * kq].x, f) ^ m[2 * kq].x;
+      o[kq][1] = pk_mul_h(e[2 * kq].y, f) ^ m[2 * kq].y;
+      o[kq][2] = pk_mul_h(e[2 * kq + 1].x, f) ^ m[2 * kq + 1].x;
+      o[kq][3] = pk_mul_h(e[2 * kq + 1].y, f) ^ m[2 * kq + 1].y;
+    }
+    return h2f(lds_u16(sb, sd));
+  }
+};
+
+template <bool A4>
+struct QmsGroup<IQ1_S, A4> {
+  static constexpr bool kOn = true;
+  __device__ __forceinline__ static float run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g,
+                                              uint32_t (&o)[4][4]) {
+    const uint32_t qs4 = lds_w32<A4>(sb, sd + 2 + 4 * g);
+    const uint32_t h = lds_u16(sb, sd + 34 + 2 * g);
+    uint4 e[4];
+#pragma unroll
+    for (int kq = 0; kq < 4; ++kq)  // the table holds entry + delta; entry qi | 2048 for delta -0.125
+      e[kq] = *reinterpret_cast<const uint4*>(
+          tbl + (bfe(qs4, 8 * kq, 8) | (bfe(h, 3 * kq, 3) << 8) | ((h >> 15) << 11)) * 16);
+    const _Float16 f = (_Float16)(float)(2u * ((h >> 12) & 7u) + 1u);
+#pragma unroll
+    for (int kq = 0; kq < 4; ++kq) {
+      o[kq][0] = pk_mul_h(e[kq].x, f);
+      o[kq][1] = pk_mul_h(e[kq].y, f);
+      o[kq][2] = pk_mul_h(e[kq].z, f);
+      o[kq][3] = pk_mul_h(e[kq].w, f);
+    }
+    return h2f(lds_u16(sb, sd));
+  }
+};
+
+// IQ1_M: the raw fragments (their 16-weight sub-scales already inside, d common to the superblock)
+template <bool A4>
+struct QmsGroup<IQ1_M, A4> {
+  static constexpr bool kOn = true;
+  __device__ __forceinline__ static float run(const uint8_t* sb, uint32_t sd, const uint8_t* tbl, int g,
+                                              uint32_t (&o)[4][4]) {
+    float d = 0.f;
+#pragma unroll
+    for (int kq = 0; kq < 4; ++kq) d = QmsRaw<IQ1_M, A4>::run(sb, sd, tbl, g, kq, o[kq]);
+    return d;
+  }
+};
+
 }  // namespace gsq

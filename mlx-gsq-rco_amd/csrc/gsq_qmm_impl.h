@@ -32,6 +32,7 @@
 //    its L2.
 // fp32 / bf16 activations use the generic kernel below.
 #pragma once
+#include <cstdlib>
 #include <type_traits>
 #include <utility>
 
@@ -907,12 +908,25 @@ static hipError_t launch_mfma(QmmMfmaArgs& a, int num_cus, const QmmWorkspace& w
   }
 }
 
+// Lane layout of the small-batch kernel's decode: whole groups per lane (HX) for every type but
+// Q6_K and Q2_K, whose fragment decoders share few field reads between a group's octets (at
+// M = 4 and 16 on 17408 / 8192 / 4096-row products: the codebook types 1-17% faster, IQ4_XS
+// 2-8%, Q4_K 1-7%, Q2_K -1 to +3%, Q6_K 8-16% slower). GSQ_QMS_HX=0 / 1 sets it for every type
+// (read once, for measurements).
+template <int T>
+constexpr bool qms_group_layout() { return T != Q6_K && T != Q2_K; }
+
 template <int T, int WV, int NB>
 static hipError_t launch_qms_a4(const QmsArgs& a, bool a4, hipStream_t s) {
+  static const int env_hx = [] {
+    const char* v = std::getenv("GSQ_QMS_HX");
+    return v ? std::atoi(v) : -1;
+  }();
+  const bool hx = env_hx < 0 ? qms_group_layout<T>() : env_hx > 0;
   if constexpr (BlockBytes<T>::v % 4 == 0) {
-    if (a4) return launch_qms_t<T, true, WV, NB>(a, s);
+    if (a4) return hx ? launch_qms_t<T, true, WV, NB, true>(a, s) : launch_qms_t<T, true, WV, NB, false>(a, s);
   }
-  return launch_qms_t<T, false, WV, NB>(a, s);
+  return hx ? launch_qms_t<T, false, WV, NB, true>(a, s) : launch_qms_t<T, false, WV, NB, false>(a, s);
 }
 
 // Plan and launch the small-batch kernel for type T (M <= 16): row groups of WV * 16 * NB

@@ -10,7 +10,7 @@
 // and the cost is the weight stream plus its decode, nearly independent of M:
 //  * work unit = (row group of WV * 16 * NB weight rows, one 256-wide K column); units are
 //    divided evenly over one workgroup per CU (stream-K), rows of a group split over the waves
-//    (16 * NB each, decoded straight into v_mfma_f32_16x16x32_f16 B operands by QmmDec);
+//    (16 * NB each, decoded straight into v_mfma_f32_16x16x32_f16 B operands);
 //  * per column, the workgroup stages the 16 x 256 fp16 activation slice in LDS (each wave
 //    DMAs 8 / WV of its eight 1 KB rows pairs, octet o of row m at position o ^ m so the A
 //    reads of 16 rows hit distinct banks) and each wave DMAs its rows' superblocks into a
@@ -18,6 +18,12 @@
 //    exact vmcnt waits and one barrier per column (not per 32-wide stage);
 //  * A operand: row m = lane % 16 of the staged slice (rows past M repeat row M - 1 and
 //    their outputs are dropped); output lane l holds rows 4(l/16)..+3 of weight row l % 16;
+//  * B operands, two lane layouts (HX): lane group q = lane / 16 either decodes octet q of each
+//    of the superblock's 8 groups (one MFMA per group, its k-slots one group), or whole groups
+//    q and q + 4 (HX, QmsGroup: a group's field reads and scale arithmetic serve its 32 weights
+//    instead of 8; one MFMA per octet takes four groups, lane group q's k-slots being octets of
+//    its own groups in A and B alike, with the groups' sub-scales inside the fp16 values and the
+//    superblock's d on the MFMA sum);
 //  * a row group split between workgroups is finished by the last to arrive, which sums
 //    the fp32 partials in workgroup order (deterministic), as in the tiled kernel.
 #pragma once
@@ -76,7 +82,7 @@ struct QmsArgs {
 
 // one workgroup per CU (LDS-bound): WV / 4 waves per SIMD, which the register allocation and
 // the scheduler may assume (latency hiding by independent work within the wave)
-template <int T, bool A4, int WV, int NB>
+template <int T, bool A4, int WV, int NB, bool HX>
 __global__ void __launch_bounds__(64 * WV, 1) __attribute__((amdgpu_waves_per_eu(WV / 4, WV / 4)))
 qms_kernel(QmsArgs args) {
   const uint8_t* const packed = args.packed;
@@ -174,6 +180,40 @@ qms_kernel(QmsArgs args) {
       dl[j] = (uint32_t)((reinterpret_cast<uintptr_t>(packed) + (uintptr_t)((long long)n * row_bytes) +
                           (uintptr_t)c * BB) & 15u);
     }
+    if constexpr (HX) {
+      // group layout: lane group aq decodes whole groups aq and aq + 4 of its row (the field
+      // reads serve 32 weights); the MFMA's k-slots of lane group aq are octets of those groups
+      // in A and B alike, so one MFMA takes four groups of a superblock
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        half8_t af[4];
+#pragma unroll
+        for (int f = 0; f < 4; ++f) {
+          const uint32_t* ap = reinterpret_cast<const uint32_t*>(xb + (((4 * (aq + 4 * h) + f) ^ am) << 4));
+          const uint32_t aw[4] = {ap[0], ap[1], ap[2], ap[3]};
+          af[f] = __builtin_bit_cast(half8_t, aw);
+        }
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+          const uint8_t* rb = wb + (16 * j + am) * S;
+          uint32_t o[4][4];
+          if constexpr (QmsGroup<T, A4>::kOn) {
+            const float d = QmsGroup<T, A4>::run(rb, dl[j], tbl, aq + 4 * h, o);
+            float4_t t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int f = 0; f < 4; ++f)
+              t = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[f], __builtin_bit_cast(half8_t, o[f]), t, 0, 0, 0);
+            acc[j] += d * t;
+          } else {
+#pragma unroll
+            for (int f = 0; f < 4; ++f) QmmDec<T, A4>::run(rb, dl[j], tbl, aq + 4 * h, f, o[f]);
+#pragma unroll
+            for (int f = 0; f < 4; ++f)
+              acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[f], __builtin_bit_cast(half8_t, o[f]), acc[j], 0, 0, 0);
+          }
+        }
+      }
+    } else {
 #pragma unroll
     for (int g = 0; g < 8; ++g) {
       const uint32_t* ap = reinterpret_cast<const uint32_t*>(xb + (((4 * g + aq) ^ am) << 4));
@@ -193,6 +233,7 @@ qms_kernel(QmsArgs args) {
           acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, __builtin_bit_cast(half8_t, o), acc[j], 0, 0, 0);
         }
       }
+    }
     }
 
     if (c != nblk - 1 && cl != ncols - 1) continue;
@@ -259,14 +300,14 @@ qms_kernel(QmsArgs args) {
   }
 }
 
-template <int T, bool A4, int WV, int NB>
+template <int T, bool A4, int WV, int NB, bool HX>
 static hipError_t launch_qms_t(QmsArgs a, hipStream_t s) {
   if constexpr (!QmsPlan<T, WV, NB>::kValid) {
     return hipErrorInvalidValue;
   } else {
     a.slot_floats = NB * 64 * WV * 4;  // every lane stores NB float4 accumulators
     if (2ll * a.G * a.slot_floats * 4 > a.part_bytes) return hipErrorInvalidValue;
-    auto k = qms_kernel<T, A4, WV, NB>;
+    auto k = qms_kernel<T, A4, WV, NB, HX>;
     static bool attr_set = false;
     if (!attr_set) {
       hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,

@@ -5,8 +5,9 @@ Drop-in counterpart of mlx_gsq/nn/linear.py:6-24 ``GSQLinear``: built from a
 ``packed_weight``, ``in_features``, ``out_features`` and ``qtype``. The reference sends one
 activation row to the fused QMV and every larger batch to the tiled QMM; here batches below
 the QMM threshold (``QMM_MIN_ROWS`` rows) go through ``quantized_matvec``, whose routing
-keeps 2-3 rows on the vector kernel where that is faster on gfx950 and sends larger fp16
-batches to the small-batch QMM; from the threshold on, the tiled QMM. The results agree
+keeps them on the matrix-vector kernels (one or two rows on the vector kernel, 3-7 fp16 rows on
+the quad-row kernel) except 5-7 fp16 rows of matrices of 2^26+ weights, which the small-batch
+QMM computes faster on gfx950; from the threshold on, QMM. The results agree
 with the reference's within the operators' tolerances either way. The optional bias is
 added afterwards.
 """

@@ -41,19 +41,21 @@ def _check_tensors(x, packed):
         raise ValueError("x and packed must be on the same GPU device")
 
 
-# Rows below the reference's QMM threshold stay on gsq_qmv, whose quad-row kernel (3-8 fp16 rows)
-# is faster than gsq_qmm's small-batch kernel up to 7 rows and as fast at 8 (measured on the 27B
-# layer, 7 projections: gsq_qmv 80 / 84 / 88 / 107 / 111 / 118 us at 2 / 3 / 4 / 5 / 6 / 8 rows
-# against 118 for the small-batch kernel at every row count), so no batch below the reference's
-# threshold is sent to QMM for speed; the threshold below is that of the reference.
-SMALL_BATCH_MIN_ROWS = QMM_MIN_ROWS
+# Rows below the reference's QMM threshold stay on gsq_qmv (the quad-row kernel takes 3-8 fp16
+# rows) except on matrices of at least 2^26 weights, where gsq_qmm's small-batch kernel is faster
+# from 5 rows. Measured per 27B projection at 4 / 5 / 6 / 7 / 8 rows (us, gsq_qmv against
+# gsq_qmm): gate/up IQ2_S 17408x5120 17.3 / 23.0 / 23.4 / 24.0 / 24.6 against 22.3-22.6, down
+# Q4_K 5120x17408 20.6 / 24.8 / 25.3 / 26.3 / 27.4 against 23.3-23.8; the 5120x5120 products
+# within 0.3 us of each other at 5-7 rows (q IQ2_XS 12.0-12.8 against 12.1-12.3) and the
+# 1024x5120 ones faster on gsq_qmv up to 8 rows (k 6.5-7.3 against 7.5-7.6).
+SMALL_BATCH_MIN_ROWS = 5
+SMALL_BATCH_MIN_WEIGHTS = 1 << 26
 
 
 def _small_batch_faster(rows, dtype, out_features, in_features):
-    del out_features, in_features  # the crossover was the same on every 27B projection shape
     if dtype != torch.float16:
         return False
-    return rows >= SMALL_BATCH_MIN_ROWS
+    return rows >= SMALL_BATCH_MIN_ROWS and out_features * in_features >= SMALL_BATCH_MIN_WEIGHTS
 
 
 def routes_to_qmm(rows, dtype, out_features, in_features):

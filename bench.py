@@ -318,7 +318,7 @@ def run_qmm(device, reps=10):
 LAYER = (("q", "IQ2_XS", 5120, 5120), ("k", "IQ2_XS", 1024, 5120), ("v", "IQ4_XS", 1024, 5120),
          ("o", "IQ3_S", 5120, 5120), ("gate", "IQ2_S", 17408, 5120), ("up", "IQ2_S", 17408, 5120),
          ("down", "Q4_K", 5120, 17408))
-CROSS_ROWS = (1, 2, 4, 8, 16)
+CROSS_ROWS = (1, 2, 3, 4, 5, 6, 7, 8, 16)
 
 
 def _time_launches(fn, stream, reps):
@@ -337,7 +337,7 @@ def _time_launches(fn, stream, reps):
 
 
 def run_crossover(device, reps=20):
-    """per projection of the mixed layer and M in {1,2,4,8,16}, QMV vs QMM time (HIP
+    """per projection of the mixed layer and M in {1..8, 16}, QMV vs QMM time (HIP
     events, weights resident); the crossover is the smallest M at which QMM is faster. gsq_qmm
     runs the small-batch kernel for M <= 16 fp16 rows. `routed_us` follows quantized_matvec's
     routing (QMM from 8 rows, from 5 on matrices of 2^26+ weights); `best_us` takes the faster."""

@@ -340,7 +340,7 @@ def run_crossover(device, reps=20):
     """per projection of the mixed layer and M in {1..8, 16}, QMV vs QMM time (HIP
     events, weights resident); the crossover is the smallest M at which QMM is faster. gsq_qmm
     runs the small-batch kernel for M <= 16 fp16 rows. `routed_us` follows quantized_matvec's
-    routing (QMM from 8 rows, from 5 on matrices of 2^26+ weights); `best_us` takes the faster."""
+    routing (QMM from 8 rows; on matrices of 2^26+ weights from 5 when K > 8192, else from 7); `best_us` takes the faster."""
     from mlx_gsq_amd.runtime.kernels.qmm import QMM_MIN_ROWS
     from mlx_gsq_amd.runtime.kernels.qmv import _small_batch_faster
     import torch

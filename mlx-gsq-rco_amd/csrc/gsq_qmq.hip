@@ -14,7 +14,8 @@
 //   per-row activation products that would take M v_dot2 per weight pair take M / 4 MFMAs per 4
 //   weights.
 // * A wave owns GL consecutive quad slices (a K range) and keeps the activations of its
-//   groups (its lane's activation row of every quad) in registers; the W waves of a row slot
+//   groups (its lane's activation row of every quad) in registers, read from one copy of the M
+//   rows that the workgroup stages in LDS when it fits (else from memory); the W waves of a row slot
 //   cover K; each wave streams its K range of consecutive row quads (one item per quad: four
 //   row pieces of 2 GL superblocks) through a private LDS ring with direct-to-LDS DMA and exact
 //   vmcnt waits, with no barrier in the main loop, like the vector kernel.
@@ -35,7 +36,7 @@ namespace gsq {
 // clamped to row M - 1 (their results are not stored), in the type's pairing; the partial sums
 // of all four rows of each quad come from the quad's other lanes (DPP broadcasts).
 template <int T, int NQ>
-__device__ __forceinline__ void qmq_load_x(XQuad<NQ, Qmv<T>::kSums>& xr, int u, const uint16_t* x, int K, int M,
+__device__ __forceinline__ void qmq_load_x(XQuad<NQ, Qmv<T>::kSums>& xr, int u, const uint16_t* x, int ld, int M,
                                            int r) {
   constexpr int NS = Qmv<T>::kSums;
   using P = Qmv<T>;
@@ -43,7 +44,7 @@ __device__ __forceinline__ void qmq_load_x(XQuad<NQ, Qmv<T>::kSums>& xr, int u, 
 #pragma unroll
   for (int t = 0; t < NQ; ++t) {
     const int m = min(4 * t + r, M - 1);
-    const uint4* p = reinterpret_cast<const uint4*>(x + (int64_t)m * K + 32 * u);
+    const uint4* p = reinterpret_cast<const uint4*>(x + (int64_t)m * ld + 32 * u);
     uint4 v[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) v[k] = p[k];
@@ -204,17 +205,36 @@ __global__ void __launch_bounds__(qmq_max_threads(NQ, GL)) qmq_kernel(QmvArgs a)
     issued = 1;
   }
   if constexpr (P::kLds > 0) dma_copy(a.tb.qmv_tbl, P::kLds, tbl, wave, nw, lane);
+  // activations staged in LDS once per workgroup (x_lds): rows of K + 8 fp16 (16 bytes of pad,
+  // so that the four rows a 16-lane read covers fall into distinct banks); the row slots then
+  // share one copy instead of each loading its own from L2
+  const uint16_t* xs = reinterpret_cast<const uint16_t*>(dyn + a.x_off);
+  if (a.x_lds)
+    for (int m = 0; m < a.M; ++m)
+      dma_copy(static_cast<const uint16_t*>(a.x) + (int64_t)m * a.K, 2 * a.K, dyn + a.x_off + m * (2 * a.K + 16), wave,
+               nw, lane);
 
-  // the lane's activations of each slice (group blk of slice sl0 + q), straight from memory
+  // the lane's activations of each slice (group blk of slice sl0 + q), from LDS or from memory
   XQuad<NQ, NS> xr[GL];
+  if (a.x_lds) {
+    wait_vmcnt(0);    // this wave's first item and its shares of the table and activations
+    __syncthreads();  // ... and every other wave's shares
 #pragma unroll
-  for (int q = 0; q < GL; ++q) {
-    const int u = (sl0 + q) * 16 + blk;
-    const bool act = q < nq && u < (a.K >> 5);
-    qmq_load_x<T, NQ>(xr[q], act ? u : 0, static_cast<const uint16_t*>(a.x), a.K, a.M, r);
+    for (int q = 0; q < GL; ++q) {
+      const int u = (sl0 + q) * 16 + blk;
+      const bool act = q < nq && u < (a.K >> 5);
+      qmq_load_x<T, NQ>(xr[q], act ? u : 0, xs, a.K + 8, a.M, r);
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < GL; ++q) {
+      const int u = (sl0 + q) * 16 + blk;
+      const bool act = q < nq && u < (a.K >> 5);
+      qmq_load_x<T, NQ>(xr[q], act ? u : 0, static_cast<const uint16_t*>(a.x), a.K, a.M, r);
+    }
+    wait_vmcnt(0);    // this wave's first item and its share of the table have landed
+    __syncthreads();  // ... and every other wave's share of the table
   }
-  wait_vmcnt(0);    // this wave's first item and its share of the table have landed
-  __syncthreads();  // ... and every other wave's share of the table
 
   for (int t = 0; t < nitems; ++t) {
     if (nitems > 2) set_progress_prio(t);
@@ -384,8 +404,16 @@ hipError_t launch_qmq(int qt, const uint8_t* packed, const void* x, void* y, int
   if (a.tbl_bytes > 0 && !tb.qmv_tbl) return hipErrorInvalidValue;
   a.red_off = a.tbl_bytes;
   const int red_bytes = (a.rows_per_wg * 4 * nq * a.W * 16 + 15) & ~15;
-  a.ring_off = a.red_off + red_bytes;
   const int lds_cap = 160 * 1024;
+  // the activations in LDS (rows of 2K + 16 bytes) when a ring of two items per wave still fits
+  static const int env_xlds = [] {
+    const char* v = std::getenv("GSQ_QMQ_XLDS");
+    return v ? std::atoi(v) : 1;
+  }();
+  a.x_off = a.red_off + red_bytes;
+  const int x_region = M * (2 * K + 16);
+  a.x_lds = env_xlds > 0 && a.x_off + x_region + 2 * nw * a.sbuf <= lds_cap ? 1 : 0;
+  a.ring_off = a.x_off + (a.x_lds ? x_region : 0);
   int nb = (lds_cap - a.ring_off) / (nw * a.sbuf);
   if (nb > 8) nb = 8;
   while (nb > 2 && (nb - 2) * a.cdma > 31) --nb;  // exact vmcnt waits go up to 31

@@ -6,8 +6,9 @@ Drop-in counterpart of mlx_gsq/nn/linear.py:6-24 ``GSQLinear``: built from a
 activation row to the fused QMV and every larger batch to the tiled QMM; here batches below
 the QMM threshold (``QMM_MIN_ROWS`` rows) go through ``quantized_matvec``, whose routing
 keeps them on the matrix-vector kernels (one or two rows on the vector kernel, 3-7 fp16 rows on
-the quad-row kernel) except 5-7 fp16 rows of matrices of 2^26+ weights, which the small-batch
-QMM computes faster on gfx950; from the threshold on, QMM. The results agree
+the quad-row kernel) except the fp16 batches of matrices of 2^26+ weights that the small-batch
+QMM computes faster on gfx950 (from 5 rows when K > 8192, from 7 otherwise); from the threshold
+on, QMM. The results agree
 with the reference's within the operators' tolerances either way. The optional bias is
 added afterwards.
 """

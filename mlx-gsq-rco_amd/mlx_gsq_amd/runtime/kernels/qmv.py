@@ -42,20 +42,20 @@ def _check_tensors(x, packed):
 
 
 # Rows below the reference's QMM threshold stay on gsq_qmv (the quad-row kernel takes 3-8 fp16
-# rows) except on matrices of at least 2^26 weights, where gsq_qmm's small-batch kernel is faster
-# from 5 rows. Measured per 27B projection at 4 / 5 / 6 / 7 / 8 rows (us, gsq_qmv against
-# gsq_qmm): gate/up IQ2_S 17408x5120 17.3 / 23.0 / 23.4 / 24.0 / 24.6 against 22.3-22.6, down
-# Q4_K 5120x17408 20.6 / 24.8 / 25.3 / 26.3 / 27.4 against 23.3-23.8; the 5120x5120 products
-# within 0.3 us of each other at 5-7 rows (q IQ2_XS 12.0-12.8 against 12.1-12.3) and the
-# 1024x5120 ones faster on gsq_qmv up to 8 rows (k 6.5-7.3 against 7.5-7.6).
-SMALL_BATCH_MIN_ROWS = 5
+# rows) except on matrices of at least 2^26 weights: there gsq_qmm's small-batch kernel is faster
+# from 5 rows when K is wider than the quad-row kernel stages in LDS (K > 8192) and from 7 rows
+# otherwise. Measured per 27B projection at 4 / 5 / 6 / 7 rows (us, gsq_qmv against gsq_qmm):
+# down Q4_K 5120x17408 20.7 / 24.3 / 25.1 / 26.0 against 23.3-23.8; gate/up IQ2_S 17408x5120
+# 15.1 / 21.6 / 21.3 / 23.8 against 22.3-22.6; the 5120x5120 and 1024x5120 products faster on
+# gsq_qmv up to 8 rows (q IQ2_XS 9.1-10.3 against 12.1-12.5, k 5.6-6.4 against 7.5).
 SMALL_BATCH_MIN_WEIGHTS = 1 << 26
+SMALL_BATCH_WIDE_K = 8192
 
 
 def _small_batch_faster(rows, dtype, out_features, in_features):
-    if dtype != torch.float16:
+    if dtype != torch.float16 or out_features * in_features < SMALL_BATCH_MIN_WEIGHTS:
         return False
-    return rows >= SMALL_BATCH_MIN_ROWS and out_features * in_features >= SMALL_BATCH_MIN_WEIGHTS
+    return rows >= (5 if in_features > SMALL_BATCH_WIDE_K else 7)
 
 
 def routes_to_qmm(rows, dtype, out_features, in_features):

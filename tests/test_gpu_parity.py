@@ -315,14 +315,15 @@ def test_qmm_fp16_output_and_fp32_input(qtype):
 
 
 @pytest.mark.parametrize("rows,n,K", [(5, 300, 4096), (4, 300, 4096), (3, 4096, 4096), (7, 16384, 4096),
-                                      (4, 16384, 4096), (5, 4096, 8192), (2, 4096, 16384), (8, 5120, 5120)])
+                                      (6, 16384, 4096), (5, 4096, 16384), (4, 4096, 16384), (5, 4096, 8192),
+                                      (2, 4096, 16384), (8, 5120, 5120)])
 def test_matvec_routes_small_fp16_batches(rows, n, K):
     """fp16 batches below the reference's 8 rows stay on gsq_qmv (3-7 rows: the quad-row kernel)
-    except 5-7 rows on matrices of 2^26+ weights; those and 8 rows take QMM (fp16-rounded
-    weights, QMM tolerance)."""
+    except on matrices of 2^26+ weights from 5 rows when K > 8192, from 7 otherwise; those and
+    8 rows take QMM (fp16-rounded weights, QMM tolerance)."""
     from mlx_gsq_amd.runtime.kernels import qmv
     routed = qmv.routes_to_qmm(rows, torch.float16, n, K)
-    assert routed == (rows >= 8 or (rows >= 5 and n * K >= 1 << 26))
+    assert routed == (rows >= 8 or (n * K >= 1 << 26 and rows >= (5 if K > 8192 else 7)))
     packed = synth.make_packed("Q4_K", n, K, seed=8)
     x = synth.make_x(rows, K, seed=8, dtype=np.float16)
     y = qmv.quantized_matvec(dev(x), dev(packed), qtype="Q4_K", out_features=n, in_features=K,

@@ -67,8 +67,9 @@ int gsq_tables_ready(int qtype_id);
 int gsq_dequant(int qtype_id, const void* packed, int64_t nblocks, float* out, void* stream);
 
 /* y[M, N] = x[M, K] * W[N, K]^T with the fused-dequant matrix-vector kernels (decode path,
- * small M): 1-2 rows (and fp32 / bf16 x) on the vector kernel, 3-8 fp16 rows on the quad-row
- * kernel (matrix-core products of four weight rows at a time), more rows in launches of 8.
+ * small M): 1-2 rows (and fp32 / bf16 x) on the vector kernel, 3-8 fp16 rows (2 on matrices of
+ * 2^26+ weights with K <= 8192) on the quad-row kernel (matrix-core products of four weight rows
+ * at a time), more rows in launches of 8.
  * Replaces quantized_matvec (mlx_gsq/runtime/kernels/qmv.py:537-576). x at any address aligned
  * to its element size: one that is not 16-byte aligned is first copied into the stream's QMM
  * workspace (see gsq_qmm; made on that first call). */

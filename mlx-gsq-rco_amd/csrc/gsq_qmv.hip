@@ -952,11 +952,18 @@ hipError_t launch_qmv(int qt, const uint8_t* packed, const void* x, int xdt, voi
                       int K, const DevTables& tb, int num_cus, hipStream_t s) {
   const size_t xe = xdt == DT_F32 ? 4 : 2, ye = ydt == DT_F32 ? 4 : 2;
   // fp16 rows in launches of up to 8 on the quad-row kernel (matrix-core products) while at
-  // least 3 are left and it takes the shape; 1-2 rows stay on the vector kernel, as fast there
-  // for 2 (the 27B layer: 80 us against 82)
+  // least 3 are left and it takes the shape, or 2 on matrices of 2^26+ weights with K <= 8192,
+  // whose activations it stages in LDS (IQ2_S 17408x5120 at 2 rows: 15.2 us against 17.4 on the
+  // vector kernel); other 1-2 row launches stay on the vector kernel, as fast or faster there
+  // (5120x17408 at 2 rows: 19.6 against 20.0). GSQ_QMQ_TWO=0 keeps 2 rows on the vector kernel.
   int64_t r0 = 0;
   if (g_qmv_quad && xdt == DT_F16) {
-    for (; M - r0 >= 3; r0 += 8) {
+    static const int env_min2 = [] {
+      const char* v = std::getenv("GSQ_QMQ_TWO");
+      return v ? std::atoi(v) : 1;
+    }();
+    const int min_rows = env_min2 > 0 && N * (int64_t)K >= (1ll << 26) && K <= 8192 ? 2 : 3;
+    for (; M - r0 >= min_rows; r0 += 8) {
       const int mrow = (int)(M - r0 < 8 ? M - r0 : 8);
       const hipError_t e = launch_qmq(qt, packed, static_cast<const char*>(x) + r0 * K * xe, static_cast<char*>(y) +
                                       r0 * N * ye, ydt, mrow, N, K, tb, num_cus, s);

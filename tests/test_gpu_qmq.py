@@ -1,7 +1,8 @@
-"""GPU parity of the quad-row QMV kernel (gsq_qmv with 3-8 fp16 activation rows).
+"""GPU parity of the quad-row QMV kernel (gsq_qmv with 3-8 fp16 activation rows, 2 on large
+matrices).
 
-gsq_qmv sends 3-8 fp16 rows to the kernel whose 4x4x4 MFMAs multiply four weight rows' decoded
-groups with up to eight activation rows. Held to the vector kernel's bar against the CPU oracle:
+gsq_qmv sends 3-8 fp16 rows (2 on matrices of 2^26+ weights with K <= 8192) to the kernel whose
+4x4x4 MFMAs multiply four weight rows' decoded groups with up to eight activation rows. Held to the vector kernel's bar against the CPU oracle:
 rel-L2 1e-4 and the elementwise tolerance of test_qmv_matches_oracle. The shapes cover rows that
 end in a partial quad (N % 4 != 0), an odd superblock count (a half-filled last quad slice),
 the 27B widths K = 5120 (two slices per wave, two row slots) and K = 17408 (three slices per
@@ -76,6 +77,15 @@ def test_qmq_more_rows_in_launches_of_eight(qtype, rows):
     """gsq_qmv with more than 8 fp16 rows: launches of 8 on the quad-row kernel, a last one of
     3-7 rows there too, one of 1-2 rows on the vector kernel."""
     y, want = check(qtype, rows, 515, 1024, seed=71)
+    assert rel_l2(y, want) <= 1e-4, rel_l2(y, want)
+    np.testing.assert_allclose(y, want, rtol=3e-5, atol=5e-4)
+
+
+@pytest.mark.parametrize("qtype", ["IQ2_S", "Q4_K", "IQ3_XXS"])
+def test_qmq_two_rows_on_large_matrices(qtype):
+    """Two fp16 rows of a matrix of 2^26 weights with K <= 8192 take the quad-row kernel (its
+    rows 2-3 repeat row 1 and are dropped)."""
+    y, want = check(qtype, 2, 16384, 4096, seed=91)
     assert rel_l2(y, want) <= 1e-4, rel_l2(y, want)
     np.testing.assert_allclose(y, want, rtol=3e-5, atol=5e-4)
 

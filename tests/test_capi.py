@@ -243,3 +243,21 @@ def test_grouped_linear_groups_by_type_and_validates():
     with pytest.raises(ValueError):
         GSQGroupedLinear([])
 
+
+
+def test_matvec_routing_rule():
+    """quantized_matvec's routing (host logic, no GPU): the reference's 8-row threshold, rows
+    wider than the vector kernel's registers, and the small fp16 batches of 2^26+ weight matrices
+    that the small-batch QMM computes faster (from 5 rows when K > 8192, from 7 otherwise)."""
+    from mlx_gsq_amd.runtime.kernels.qmv import routes_to_qmm
+    f16, f32 = torch.float16, torch.float32
+    big = 1 << 26
+    assert routes_to_qmm(8, f16, 64, 512) and routes_to_qmm(8, f32, 64, 512)  # the reference's rule
+    assert not routes_to_qmm(7, f16, 64, 512) and not routes_to_qmm(1, f32, 64, 512)
+    assert routes_to_qmm(1, f16, 64, 65536 + 256) and not routes_to_qmm(1, f16, 64, 65536)
+    assert routes_to_qmm(1, f32, 64, 32768 + 256) and not routes_to_qmm(1, f32, 64, 32768)
+    for rows in range(1, 8):
+        assert routes_to_qmm(rows, f16, -(-big // 17408), 17408) == (rows >= 5)  # K > 8192
+        assert routes_to_qmm(rows, f16, big // 4096, 4096) == (rows >= 7)
+        assert not routes_to_qmm(rows, f16, big // 4096 - 1, 4096)  # below 2^26 weights
+        assert not routes_to_qmm(rows, f32, big // 4096, 4096)  # fp16 activations only

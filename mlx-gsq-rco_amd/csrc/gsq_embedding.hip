@@ -27,7 +27,13 @@ struct EmbStage {
   static constexpr int kWave = 64 * kSlot;
 };
 
-template <int T, int OB>
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// NT: streaming (nontemporal) stores, for outputs of many rows that no later work of the kernel
+// reads (4096 ids: 15.5 -> 13.8 us); a few rows (a decode step's token) keep plain stores, whose
+// lines stay in L2 for the kernel that reads them next. A compile-time choice: a runtime branch
+// between the two stores is merged into one plain store by the compiler.
+template <int T, int OB, bool NT>
 __device__ __forceinline__ void embedding_body(const uint8_t* __restrict__ packed, const void* __restrict__ ids,
                                                int ids64, int64_t n_ids, int64_t vocab, int64_t dims,
                                                uint8_t* __restrict__ out, int odt, const DevTables& t,
@@ -83,21 +89,25 @@ __device__ __forceinline__ void embedding_body(const uint8_t* __restrict__ packe
     const int src = (1024 / OB) * i + lane / P;  // lane whose group holds this piece
     if (wave0 + src < total) {
       const uint4 val = *reinterpret_cast<const uint4*>(stage + src * S::kSlot + 16 * (lane % P));
-      *reinterpret_cast<uint4*>(out + (wave0 + src) * OB + 16 * (lane % P)) = val;
+      uint4* dst = reinterpret_cast<uint4*>(out + (wave0 + src) * OB + 16 * (lane % P));
+      if constexpr (NT) __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, val), reinterpret_cast<u32x4_t*>(dst));
+      else *dst = val;
     }
   }
 }
 
-template <int T>
+constexpr int64_t kEmbStreamRows = 64;  // rows from which the output is stored nontemporally
+
+template <int T, bool NT>
 __global__ void __launch_bounds__(256) embedding_kernel(const uint8_t* __restrict__ packed, const void* __restrict__ ids,
                                                         int ids64, int64_t n_ids, int64_t vocab, int64_t dims,
                                                         void* __restrict__ out, int odt, DevTables t) {
   __shared__ __attribute__((aligned(16))) uint8_t stage[4 * EmbStage<128>::kWave];
   uint8_t* ws = stage + (threadIdx.x >> 6) * (odt == EMB_F32 ? EmbStage<128>::kWave : EmbStage<64>::kWave);
   if (odt == EMB_F32)
-    embedding_body<T, 128>(packed, ids, ids64, n_ids, vocab, dims, static_cast<uint8_t*>(out), odt, t, ws);
+    embedding_body<T, 128, NT>(packed, ids, ids64, n_ids, vocab, dims, static_cast<uint8_t*>(out), odt, t, ws);
   else
-    embedding_body<T, 64>(packed, ids, ids64, n_ids, vocab, dims, static_cast<uint8_t*>(out), odt, t, ws);
+    embedding_body<T, 64, NT>(packed, ids, ids64, n_ids, vocab, dims, static_cast<uint8_t*>(out), odt, t, ws);
 }
 
 template <int T>
@@ -105,8 +115,12 @@ static hipError_t launch_embedding_t(const uint8_t* packed, const void* ids, int
                                      int64_t dims, void* out, int odt, const DevTables& t, hipStream_t s) {
   const int64_t threads = n_ids * (dims >> 5);
   const int64_t grid = (threads + 255) / 256;
-  hipLaunchKernelGGL(embedding_kernel<T>, dim3((unsigned)grid), dim3(256), 0, s, packed, ids, ids64, n_ids, vocab,
-                     dims, out, odt, t);
+  if (n_ids >= kEmbStreamRows)
+    hipLaunchKernelGGL((embedding_kernel<T, true>), dim3((unsigned)grid), dim3(256), 0, s, packed, ids, ids64, n_ids,
+                       vocab, dims, out, odt, t);
+  else
+    hipLaunchKernelGGL((embedding_kernel<T, false>), dim3((unsigned)grid), dim3(256), 0, s, packed, ids, ids64, n_ids,
+                       vocab, dims, out, odt, t);
   return hipGetLastError();
 }
 

@@ -46,10 +46,12 @@ enum { QDT_F32 = 0, QDT_F16 = 1, QDT_BF16 = 2 };
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
+// Final outputs are not read again by the kernel, so fp32 ones are written as streaming
+// (nontemporal) stores; the split-K partials, which the fix-up reads back, keep plain stores.
 __device__ __forceinline__ void qmm_store_y(void* y, int dt, int64_t i, float v) {
   if (dt == QDT_F16) reinterpret_cast<_Float16*>(y)[i] = (_Float16)v;
   else if (dt == QDT_BF16) reinterpret_cast<uint16_t*>(y)[i] = (uint16_t)f32_to_bf16_bits(v);
-  else reinterpret_cast<float*>(y)[i] = v;
+  else __builtin_nontemporal_store(v, reinterpret_cast<float*>(y) + i);
 }
 
 // ---- MFMA kernel ----------------------------------------------------------------------
@@ -302,8 +304,8 @@ __device__ __forceinline__ void qmm_store_rows_f32(float* y, int M, int N, const
       if (mm < M) {
         float* yp = y + (int64_t)mm * N + nn;
         if (nn + 8 <= N) {
-          *reinterpret_cast<float4_t*>(yp) = a;
-          *reinterpret_cast<float4_t*>(yp + 4) = b;
+          __builtin_nontemporal_store(a, reinterpret_cast<float4_t*>(yp));
+          __builtin_nontemporal_store(b, reinterpret_cast<float4_t*>(yp + 4));
         } else {
 #pragma unroll
           for (int k = 0; k < 4; ++k) {

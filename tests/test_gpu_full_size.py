@@ -166,3 +166,24 @@ def test_qmm_configs2_shapes(qtype, case):
     rows = sample_rows(n, seed)
     want = sampled_reference(x, packed, qtype, n, k, rows)
     check_qmm_bar(y[:, rows], want)
+
+
+@pytest.mark.parametrize("qtype", QTYPES)
+@pytest.mark.parametrize("m", [9, 16])
+def test_qmm_small_batch_large_ragged(qtype, m):
+    """The small-batch kernel's plan for products of 2^26+ weights (16 waves of 16 rows where
+    the type's ring fits, row groups of 256 rows split over the K columns of every CU) on a
+    4100 x 16384 matrix, whose last row group holds 4 rows; at M = 9 the rows past M repeat row
+    M - 1 and their outputs are dropped. Sampled columns include the last rows."""
+    from mlx_gsq_amd.runtime.kernels.qmm import quantized_matmul
+    n, k = 4100, 16384
+    print(f"full-size qmm small {qtype} M={m} {n}x{k}", flush=True)
+    seed = 700 + m + QTYPES.index(qtype)
+    packed = synth.make_packed(qtype, n, k, seed=seed)
+    x = synth.make_x(m, k, seed=seed + 1, dtype=np.float16)
+    y = quantized_matmul(torch.from_numpy(x).cuda(), torch.from_numpy(packed).cuda(), qtype=qtype,
+                         out_features=n, in_features=k, out_dtype=torch.float32).cpu().numpy()
+    assert y.shape == (m, n) and np.isfinite(y).all()
+    rows = np.union1d(sample_rows(n, seed), np.arange(n - 8, n))
+    want = sampled_reference(x, packed, qtype, n, k, rows)
+    check_qmm_bar(y[:, rows], want)
